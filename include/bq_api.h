@@ -1,0 +1,175 @@
+/*
+ * bq_api.h -- C ABI of the MI355X (gfx950) butterquant library, libbq.so.
+ *
+ * This is the drop-in boundary for the reference's butterquant kernel entry
+ * points (CoffeeVampir3/Mojo-Gemma4-CPU, butterquant_kernels/linear.mojo and
+ * butterquant_kernels/moe.mojo) and for the load-time pack they consume
+ * (butterquant/pack.mojo).  A Mojo caller binds these symbols with
+ * `external_call` the way butterquant/amx_tiles.mojo:46-53 already calls C.
+ *
+ * Conventions (mapping the reference's Mojo conventions to C):
+ *   - Every pointer is a DEVICE pointer unless marked (host).  bf16 values are
+ *     passed as their uint16_t bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Entry points only
+ *     enqueue work; the reference dispatchers join before returning
+ *     (kernels/helpers.mojo:320-327), which a caller gets with
+ *     bq_stream_synchronize().
+ *   - seq_len <= 0 is a no-op returning BQ_OK, as the reference returns early
+ *     (linear.mojo:134-135, 255-256; moe.mojo:317-318).
+ *   - Contract violations the reference enforces with compile-time asserts or
+ *     debug_assert (linear.mojo:132-133, vnni.mojo:91-99) or abort
+ *     (kernels.mojo:82-83) return BQ_ERR_SHAPE / BQ_ERR_INVALID with a message
+ *     in bq_last_error() and launch nothing.
+ *   - No entry point allocates device memory; buffers are caller-owned, as the
+ *     reference's arena-allocated bindings are (gemma_4_moe_bq.mojo:649-664).
+ *
+ * Weights: int8 codes in the GPU layout "tile16x64" (1 KiB fragments of 16
+ * rows x 64 K; see bq_weight_retile), per-row f32 scales (amax/127).  The
+ * colsum sidecar of the reference's VNNI layout is not needed: the GPU
+ * multiplies signed codes directly, which yields the same integer sums.
+ */
+#ifndef BQ_API_H
+#define BQ_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BQ_OK 0
+#define BQ_ERR_INVALID 1      /* null pointer / bad enum */
+#define BQ_ERR_SHAPE 2        /* shape contract violated */
+#define BQ_ERR_HIP 3          /* HIP runtime error (launch failed) */
+#define BQ_ERR_UNSUPPORTED 4  /* size beyond a kernel's stated limit */
+
+#define BQ_LAYOUT_ROWMAJOR 0  /* on-disk int8 [N,K] (quant/quantizer.mojo:1028-1036) */
+#define BQ_LAYOUT_VNNI 1      /* reference 32x64 tiles (butterquant/vnni.mojo:146-163) */
+
+/* kernels/moe_router.mojo:33-36 SparseRoute {token:i32, weight:f32}, 8 bytes */
+typedef struct bq_route {
+  int32_t token;
+  float weight;
+} bq_route;
+
+/* ---- runtime ------------------------------------------------------------ */
+int bq_init(int device);                 /* select + warm the device */
+const char* bq_last_error(void);         /* message of the last failure (thread-local) */
+int bq_stream_synchronize(void* stream); /* join, like fanout_dispatch's join_all */
+const char* bq_version(void);
+
+/* ---- weights (load time) -------------------------------------------------- */
+
+/* Re-tile packed int8 codes [n_rows, k] once at load into tile16x64.
+ * Replaces PackColsumKernel.execute / dispatch_pack_colsum
+ * (butterquant/pack.mojo:29-99, called from gemma_4_moe_bq.mojo:872-892).
+ * src_layout: BQ_LAYOUT_ROWMAJOR (quantizer output) or BQ_LAYOUT_VNNI.
+ * n_rows % 16 == 0, k % 64 == 0; src and dst must not overlap. */
+int bq_weight_retile(const int8_t* src, int src_layout, int8_t* dst, int n_rows, int k,
+                     void* stream);
+
+/* Inverse of bq_weight_retile to row-major (bit-exact unpack for tests and
+ * for exporting weights). */
+int bq_weight_unpack(const int8_t* tiled, int8_t* dst_rowmajor, int n_rows, int k, void* stream);
+
+/* The reference's own load-time pack: row-major -> VNNI 32x64 tiles plus the
+ * colsum sidecar (butterquant/vnni.mojo:86-114; task shape from
+ * modeling/slot.mojo:263-301).  colsum may be NULL.  colsum_row_major=1 gives
+ * [rows, cols/block_cols], 0 gives [cols/block_cols, rows].
+ * rows % 32 == 0, cols % 64 == 0, block_cols % 16 == 0, cols % block_cols == 0. */
+int bq_pack_colsum_vnni(const int8_t* src, int8_t* dst, float* colsum, int rows, int cols,
+                        int block_cols, int colsum_row_major, void* stream);
+
+/* Offline weight encoder (butterquant/kernels.mojo:148-168 rotate_and_quant
+ * as driven by quant/quantizer.mojo:963-1051): bf16 [rows, cols] (x gamma,
+ * f32 [cols] or NULL) -> FWHT(fwht_block) along K -> int8 row-major codes and
+ * scales amax/127, per row [rows] or per block [rows, cols/fwht_block].
+ * fwht_block in {16,32,64,128,256,512}; cols % 64 == 0; cols <= 16128. */
+int bq_quantize_weight(const uint16_t* w_bf16, const float* gamma, int8_t* codes,
+                       float* scales, int rows, int cols, int fwht_block, int per_block,
+                       void* stream);
+
+/* ---- activation prep ------------------------------------------------------ */
+
+/* dispatch_bq_norm_quant[hidden, block, sqrt_n, n_eps] (butterquant_kernels/
+ * linear.mojo:58-82 -> butterquant/runtime.mojo:11-37): per token,
+ * inv_rms = sqrt_n / sqrt(sum(x^2) + n_eps); x*inv_rms*gamma -> FWHT(block)
+ * -> per-row int8 with x_sa = amax.  gamma is the baked split gain (bf16).
+ * hidden % 64 == 0, hidden % block == 0, hidden <= 16128. */
+int bq_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                  int seq_len, int hidden, int block, float sqrt_n, float n_eps, void* stream);
+
+/* dispatch_bq_block_quant[block, apply_fwht] (linear.mojo:182-205 ->
+ * runtime.mojo:62-80): bf16 [seq_len, cols] -> [FWHT(block)] -> per-block int8,
+ * x_sa [seq_len, cols/block] = block amax.  cols % 64 == 0, cols % block == 0. */
+int bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa, int cols, int seq_len,
+                   int block, int apply_fwht, void* stream);
+
+/* ---- linears ------------------------------------------------------------- */
+
+/* dispatch_bq_linear[hidden] (linear.mojo:119-149; BqLinearKernel 85-116):
+ * out[m, n] = bf16((f32(sum_k x*w) * (x_sa[m]/127)) * w_scale[n]).
+ * out_f32 (optional, may be NULL) receives the pre-cast f32 values.
+ * n_rows % 16 == 0, hidden % 64 == 0. */
+int bq_linear(const int8_t* x_i8, const float* x_sa, const int8_t* w, const float* w_scale,
+              uint16_t* out, float* out_f32, int n_rows, int seq_len, int hidden, void* stream);
+
+/* dispatch_bq_block_linear[n_rows] (linear.mojo:240-270; gemm.mojo:173-243):
+ * facc = fma(f32(sum_{k in b} x*w), x_sa[m,b]/127, facc) over blocks b in
+ * order, out = bf16(facc * w_scale[n]).  block % 64 == 0 and a power of two,
+ * k_dim % block == 0, k_dim/block <= 64. */
+int bq_block_linear(const int8_t* x_i8, const float* x_sa, const int8_t* w, const float* w_scale,
+                    uint16_t* out, float* out_f32, int n_rows, int k_dim, int seq_len, int block,
+                    void* stream);
+
+/* dispatch_bq_qkv[hidden, qn_full, kvn_full] (linear.mojo:273-326): three
+ * per-row linears sharing one activation, in ONE launch over the
+ * concatenated q|k|v output tiles (the reference's Chain split). */
+int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float* q_scale,
+           const int8_t* k_w, const float* k_scale, const int8_t* v_w, const float* v_scale,
+           uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, int qn, int kvn, int seq_len,
+           int hidden, void* stream);
+
+/* ---- MoE ---------------------------------------------------------------- */
+
+/* dispatch_build_expert_schedules (kernels/moe_router.mojo:60-145): routes
+ * of experts [expert_base, expert_base+experts) into expert_offset[experts+1]
+ * and routes[] sorted by (expert, token, k).  Each token's top_k experts must
+ * be distinct (top-k routing).  experts <= 256; routes holds seq_len*top_k. */
+int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
+                          int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
+                          void* stream);
+
+/* dispatch_bq_phase1_gate_up[hidden, gate_up, inter] (moe.mojo:132-164):
+ * for every route record rec of expert e (rows of w_gate_up: gate
+ * [0,inter), up [inter, 2*inter) of expert e, expert stride 2*inter*hidden):
+ * bucket[rec, i] = bf16(gelu_tanh(g)*u), g/u the per-row dequantized
+ * projections of x_i8[token(rec)].  seq_len*top_k bounds the route count
+ * (grid sizing; the reference sizes its loop from expert_offset alone).
+ * inter % 16 == 0, hidden % 64 == 0. */
+int bq_moe_phase1_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
+                          const bq_route* routes, const int8_t* w_gate_up,
+                          const float* gate_up_scale, uint16_t* bucket, int experts_per_rank,
+                          int seq_len, int top_k, int hidden, int inter, void* stream);
+
+/* Bytes of device workspace bq_moe_phase2_down needs (per-route f32 results
+ * and per-token route lists). */
+size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden);
+
+/* dispatch_bq_phase2_down[hidden, inter] (moe.mojo:298-335): per-block
+ * (block = 64) down projection of the block-quantized bucket, route-weighted
+ * and accumulated per token in ascending expert order into moe_accum
+ * f32 [seq_len, hidden]; moe_out = bf16(moe_accum).  w_down rows are
+ * [experts_per_rank*hidden, inter] (expert stride hidden*inter).
+ * workspace: >= bq_moe_phase2_workspace_size() bytes, 256-byte aligned. */
+int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
+                       const int32_t* expert_offset, const bq_route* routes, const int8_t* w_down,
+                       const float* down_scale, float* moe_accum, uint16_t* moe_out,
+                       int experts_per_rank, int seq_len, int top_k, int hidden, int inter,
+                       int block, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BQ_API_H */

@@ -1,0 +1,295 @@
+"""Python binding of libbq.so (the gfx950 butterquant library) for tests and
+benchmarks.  torch supplies device memory and the current stream; every
+computation runs in libbq.so through its C ABI (include/bq_api.h).  If the
+library is missing this module raises on import -- there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libbq.so")
+
+LAYOUT_ROWMAJOR = 0
+LAYOUT_VNNI = 1
+
+
+class BqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"libbq error {code}: {msg}")
+        self.code = code
+
+
+_vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+
+# symbol -> argtypes (restype int unless listed in _RESTYPES)
+SIGNATURES = {
+    "bq_init": [_i],
+    "bq_last_error": [],
+    "bq_stream_synchronize": [_vp],
+    "bq_version": [],
+    "bq_weight_retile": [_vp, _i, _vp, _i, _i, _vp],
+    "bq_weight_unpack": [_vp, _vp, _i, _i, _vp],
+    "bq_pack_colsum_vnni": [_vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_quantize_weight": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_norm_quant": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
+    "bq_block_quant": [_vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
+    "bq_block_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_qkv": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "bq_moe_phase1_gate_up": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "bq_moe_phase2_workspace_size": [_i, _i, _i],
+    "bq_moe_phase2_down": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                           _vp, _sz, _vp],
+}
+_RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
+             "bq_moe_phase2_workspace_size": C.c_size_t}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run mojo-gemma4-cpu_amd/build.py "
+                          "(or __graft_entry__.build())")
+    lib = C.CDLL(LIB_PATH)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, C.c_int)
+    return lib
+
+
+_lib = _load()
+
+
+def lib():
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise BqError(rc, _lib.bq_last_error().decode())
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t: torch.Tensor, dtype=None):
+    if not t.is_cuda:
+        raise ValueError("libbq takes device tensors")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("libbq takes contiguous tensors")
+    return t
+
+
+def init(device: int = 0) -> None:
+    _check(_lib.bq_init(device))
+
+
+def synchronize() -> None:
+    _check(_lib.bq_stream_synchronize(_stream()))
+
+
+def norm_consts(hidden: int):
+    """(sqrt_n, n_eps) in f32 as gemma_4_moe_bq.mojo:646-647 computes them."""
+    import numpy as np
+    sqrt_n = np.sqrt(np.float32(hidden), dtype=np.float32)
+    n_eps = np.float32(hidden) * np.float32(1e-6)
+    return float(sqrt_n), float(n_eps)
+
+
+@dataclass
+class ButterquantWeight:
+    """Device view of a quantized weight (butterquant/weight.mojo:50-64):
+    codes in the tile16x64 layout + per-row scales."""
+    data: torch.Tensor   # int8 [n_rows * k] tile16x64
+    scale: torch.Tensor  # f32 [n_rows]
+    n_rows: int
+    k: int
+
+
+# --------------------------------------------------------------------------
+# weights
+# --------------------------------------------------------------------------
+
+def retile(codes: torch.Tensor, n_rows: int, k: int, layout: int = LAYOUT_ROWMAJOR) -> torch.Tensor:
+    _dev(codes, torch.int8)
+    out = torch.empty(n_rows * k, dtype=torch.int8, device=codes.device)
+    _check(_lib.bq_weight_retile(_p(codes), layout, _p(out), n_rows, k, _stream()))
+    return out
+
+
+def unpack(tiled: torch.Tensor, n_rows: int, k: int) -> torch.Tensor:
+    _dev(tiled, torch.int8)
+    out = torch.empty((n_rows, k), dtype=torch.int8, device=tiled.device)
+    _check(_lib.bq_weight_unpack(_p(tiled), _p(out), n_rows, k, _stream()))
+    return out
+
+
+def pack_colsum_vnni(codes: torch.Tensor, block_cols: int | None = None,
+                     colsum_row_major: bool = True):
+    _dev(codes, torch.int8)
+    rows, cols = codes.shape
+    bc = cols if block_cols is None else block_cols
+    dst = torch.empty(rows * cols, dtype=torch.int8, device=codes.device)
+    cs = torch.empty(rows * (cols // bc), dtype=torch.float32, device=codes.device)
+    _check(_lib.bq_pack_colsum_vnni(_p(codes), _p(dst), _p(cs), rows, cols, bc,
+                                    int(colsum_row_major), _stream()))
+    return dst, cs
+
+
+def quantize_weight(w: torch.Tensor, fwht_block: int, per_block: bool = False,
+                    gamma: torch.Tensor | None = None):
+    """bf16 [rows, cols] -> (int8 row-major codes, f32 scales)."""
+    _dev(w, torch.bfloat16)
+    rows, cols = w.shape
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=w.device)
+    shape = (rows, cols // fwht_block) if per_block else (rows,)
+    scales = torch.empty(shape, dtype=torch.float32, device=w.device)
+    if gamma is not None:
+        _dev(gamma, torch.float32)
+    _check(_lib.bq_quantize_weight(_p(w), _p(gamma), _p(codes), _p(scales), rows, cols,
+                                   fwht_block, int(per_block), _stream()))
+    return codes, scales
+
+
+def load_weight(w: torch.Tensor, fwht_block: int) -> ButterquantWeight:
+    """Quantize a bf16 weight (per-row recipe) and re-tile it for the GPU."""
+    codes, scales = quantize_weight(w, fwht_block)
+    n, k = w.shape
+    return ButterquantWeight(retile(codes, n, k), scales, n, k)
+
+
+# --------------------------------------------------------------------------
+# activations
+# --------------------------------------------------------------------------
+
+def norm_quant(x: torch.Tensor, gamma: torch.Tensor, block: int = 128, sqrt_n=None,
+               n_eps=None, out=None):
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    m, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    if out is None:
+        xq = torch.empty((m, h), dtype=torch.int8, device=x.device)
+        sa = torch.empty(m, dtype=torch.float32, device=x.device)
+    else:
+        xq, sa = out
+    _check(_lib.bq_norm_quant(_p(x), _p(gamma), _p(xq), _p(sa), m, h, block, sqrt_n, n_eps,
+                              _stream()))
+    return xq, sa
+
+
+def block_quant(x: torch.Tensor, block: int, apply_fwht: bool, out=None):
+    _dev(x, torch.bfloat16)
+    r, cols = x.shape
+    if out is None:
+        xq = torch.empty((r, cols), dtype=torch.int8, device=x.device)
+        sa = torch.empty((r, cols // block), dtype=torch.float32, device=x.device)
+    else:
+        xq, sa = out
+    _check(_lib.bq_block_quant(_p(x), _p(xq), _p(sa), cols, r, block, int(apply_fwht),
+                               _stream()))
+    return xq, sa
+
+
+# --------------------------------------------------------------------------
+# linears
+# --------------------------------------------------------------------------
+
+def linear(x_i8, x_sa, w: ButterquantWeight, want_f32: bool = False, out=None):
+    m, k = x_i8.shape
+    if out is None:
+        out = torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x_i8.device)
+    of = torch.empty((m, w.n_rows), dtype=torch.float32, device=x_i8.device) if want_f32 else None
+    _check(_lib.bq_linear(_p(x_i8), _p(x_sa), _p(w.data), _p(w.scale), _p(out), _p(of),
+                          w.n_rows, m, k, _stream()))
+    return (out, of) if want_f32 else out
+
+
+def block_linear(x_i8, x_sa, w: ButterquantWeight, block: int, want_f32: bool = False, out=None):
+    m, k = x_i8.shape
+    if out is None:
+        out = torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x_i8.device)
+    of = torch.empty((m, w.n_rows), dtype=torch.float32, device=x_i8.device) if want_f32 else None
+    _check(_lib.bq_block_linear(_p(x_i8), _p(x_sa), _p(w.data), _p(w.scale), _p(out), _p(of),
+                                w.n_rows, k, m, block, _stream()))
+    return (out, of) if want_f32 else out
+
+
+def qkv(x_i8, x_sa, q: ButterquantWeight, k: ButterquantWeight, v: ButterquantWeight, outs=None):
+    m, hidden = x_i8.shape
+    if outs is None:
+        outs = tuple(torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x_i8.device)
+                     for w in (q, k, v))
+    qo, ko, vo = outs
+    _check(_lib.bq_qkv(_p(x_i8), _p(x_sa), _p(q.data), _p(q.scale), _p(k.data), _p(k.scale),
+                       _p(v.data), _p(v.scale), _p(qo), _p(ko), _p(vo), q.n_rows, k.n_rows, m,
+                       hidden, _stream()))
+    return qo, ko, vo
+
+
+# --------------------------------------------------------------------------
+# MoE
+# --------------------------------------------------------------------------
+
+def build_schedule(route_idx: torch.Tensor, route_w: torch.Tensor, experts: int,
+                   expert_base: int = 0, out=None):
+    """-> (expert_offset int32 [E+1], routes int32 [T*k, 2] = {token, weight bits})."""
+    _dev(route_idx, torch.int32)
+    _dev(route_w, torch.float32)
+    t, k = route_idx.shape
+    if out is None:
+        eo = torch.empty(experts + 1, dtype=torch.int32, device=route_idx.device)
+        routes = torch.zeros((t * k, 2), dtype=torch.int32, device=route_idx.device)
+    else:
+        eo, routes = out
+    _check(_lib.bq_moe_build_schedule(_p(route_idx), _p(route_w), t, k, expert_base, experts,
+                                      _p(eo), _p(routes), _stream()))
+    return eo, routes
+
+
+def moe_phase1(x_i8, x_sa, eo, routes, w_gu: ButterquantWeight, experts: int, seq_len: int,
+               top_k: int, inter: int, out=None):
+    hidden = x_i8.shape[1]
+    if out is None:
+        out = torch.empty((seq_len * top_k, inter), dtype=torch.bfloat16, device=x_i8.device)
+    _check(_lib.bq_moe_phase1_gate_up(_p(x_i8), _p(x_sa), _p(eo), _p(routes), _p(w_gu.data),
+                                      _p(w_gu.scale), _p(out), experts, seq_len, top_k, hidden,
+                                      inter, _stream()))
+    return out
+
+
+def moe_phase2_workspace_size(seq_len: int, top_k: int, hidden: int) -> int:
+    return int(_lib.bq_moe_phase2_workspace_size(seq_len, top_k, hidden))
+
+
+def moe_phase2(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: int, seq_len: int,
+               top_k: int, hidden: int, block: int = 64, workspace=None, out=None):
+    inter = b_i8.shape[1]
+    dev = b_i8.device
+    if workspace is None:
+        nbytes = max(moe_phase2_workspace_size(seq_len, top_k, hidden), 256)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if out is None:
+        accum = torch.empty((seq_len, hidden), dtype=torch.float32, device=dev)
+        o = torch.empty((seq_len, hidden), dtype=torch.bfloat16, device=dev)
+    else:
+        accum, o = out
+    _check(_lib.bq_moe_phase2_down(_p(b_i8), _p(b_sa), _p(eo), _p(routes), _p(w_d.data),
+                                   _p(w_d.scale), _p(accum), _p(o), experts, seq_len, top_k,
+                                   hidden, inter, block, _p(workspace), workspace.numel(),
+                                   _stream()))
+    return accum, o

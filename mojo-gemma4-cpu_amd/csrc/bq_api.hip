@@ -1,0 +1,248 @@
+// bq_api.hip -- the extern "C" boundary (include/bq_api.h): argument and
+// shape validation (the reference's compile-time asserts / debug_asserts
+// become status codes), then kernel launches on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/bq_api.h"
+#include "bq_kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(BQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return BQ_OK;
+}
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+inline bool fwht_block_ok(int b) {
+  return b == 16 || b == 32 || b == 64 || b == 128 || b == 256 || b == 512;
+}
+constexpr int kMaxRowLds = 16128;  // f32 row kept in 64 KiB of LDS
+
+// int8 operands are moved 16 bytes per lane
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* bq_version(void) { return "bq-mi355x 0.1 (gfx950)"; }
+
+const char* bq_last_error(void) { return g_err; }
+
+int bq_init(int device) {
+  int r = check_hip(hipSetDevice(device), "hipSetDevice");
+  if (r) return r;
+  return check_hip(hipFree(nullptr), "hip runtime init");
+}
+
+int bq_stream_synchronize(void* stream) {
+  return check_hip(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+}
+
+int bq_weight_retile(const int8_t* src, int src_layout, int8_t* dst, int n_rows, int k,
+                     void* stream) {
+  if (!src || !dst) return fail(BQ_ERR_INVALID, "bq_weight_retile: null pointer");
+  if (src_layout != BQ_LAYOUT_ROWMAJOR && src_layout != BQ_LAYOUT_VNNI)
+    return fail(BQ_ERR_INVALID, "bq_weight_retile: unknown layout %d", src_layout);
+  if (n_rows < 0 || k < 0 || n_rows % 16 || k % 64)
+    return fail(BQ_ERR_SHAPE, "bq_weight_retile: need n_rows %% 16 == 0 and k %% 64 == 0 (got %d x %d)",
+                n_rows, k);
+  if (!a16(src) || !a16(dst)) return fail(BQ_ERR_INVALID, "bq_weight_retile: pointers must be 16-byte aligned");
+  if (src_layout == BQ_LAYOUT_VNNI && n_rows % 32)
+    return fail(BQ_ERR_SHAPE, "bq_weight_retile: VNNI source needs n_rows %% 32 == 0 (got %d)", n_rows);
+  return check_hip(bq::launch_retile(src, src_layout, dst, n_rows, k, S(stream)), "retile");
+}
+
+int bq_weight_unpack(const int8_t* tiled, int8_t* dst, int n_rows, int k, void* stream) {
+  if (!tiled || !dst) return fail(BQ_ERR_INVALID, "bq_weight_unpack: null pointer");
+  if (n_rows < 0 || k < 0 || n_rows % 16 || k % 64)
+    return fail(BQ_ERR_SHAPE, "bq_weight_unpack: need n_rows %% 16 == 0 and k %% 64 == 0");
+  if (!a16(tiled) || !a16(dst)) return fail(BQ_ERR_INVALID, "bq_weight_unpack: pointers must be 16-byte aligned");
+  return check_hip(bq::launch_unpack(tiled, dst, n_rows, k, S(stream)), "unpack");
+}
+
+int bq_pack_colsum_vnni(const int8_t* src, int8_t* dst, float* colsum, int rows, int cols,
+                        int block_cols, int colsum_row_major, void* stream) {
+  if (!src || !dst) return fail(BQ_ERR_INVALID, "bq_pack_colsum_vnni: null pointer");
+  if (src == dst) return fail(BQ_ERR_INVALID, "bq_pack_colsum_vnni: src and dst must differ on the GPU");
+  // butterquant/vnni.mojo:91-99
+  if (rows < 0 || cols <= 0 || cols % 64 || rows % 32 || block_cols <= 0 || cols % block_cols ||
+      block_cols % 16)
+    return fail(BQ_ERR_SHAPE,
+                "bq_pack_colsum_vnni: need cols %% 64 == 0, rows %% 32 == 0, block_cols | cols, "
+                "block_cols %% 16 == 0 (got %d x %d, block %d)", rows, cols, block_cols);
+  if (!a16(src) || (reinterpret_cast<uintptr_t>(dst) & 3u))
+    return fail(BQ_ERR_INVALID, "bq_pack_colsum_vnni: src must be 16-byte and dst 4-byte aligned");
+  return check_hip(bq::launch_pack_colsum(src, dst, colsum, rows, cols, block_cols,
+                                          colsum_row_major, S(stream)), "pack_colsum");
+}
+
+int bq_quantize_weight(const uint16_t* w, const float* gamma, int8_t* codes, float* scales,
+                       int rows, int cols, int fwht_block, int per_block, void* stream) {
+  if (!w || !codes || !scales) return fail(BQ_ERR_INVALID, "bq_quantize_weight: null pointer");
+  if (!fwht_block_ok(fwht_block))  // kernels.mojo:167-168 aborts
+    return fail(BQ_ERR_SHAPE, "bq_quantize_weight: unsupported FWHT block %d", fwht_block);
+  if (rows < 0 || cols <= 0 || cols % 64 || cols % fwht_block)
+    return fail(BQ_ERR_SHAPE, "bq_quantize_weight: cols %d not a multiple of 64 and the FWHT block", cols);
+  if (cols > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "bq_quantize_weight: cols %d > %d", cols, kMaxRowLds);
+  return check_hip(bq::launch_quantize_weight(w, gamma, codes, scales, rows, cols, fwht_block,
+                                              per_block, S(stream)), "quantize_weight");
+}
+
+int bq_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                  int seq_len, int hidden, int block, float sqrt_n, float n_eps, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!src || !gamma || !x_i8 || !x_sa) return fail(BQ_ERR_INVALID, "bq_norm_quant: null pointer");
+  if (!fwht_block_ok(block)) return fail(BQ_ERR_SHAPE, "bq_norm_quant: unsupported FWHT block %d", block);
+  // runtime.mojo:18-21
+  if (hidden <= 0 || hidden % 64 || hidden % block)
+    return fail(BQ_ERR_SHAPE, "bq_norm_quant: hidden %d must be a multiple of 64 and of block %d", hidden, block);
+  if (hidden > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "bq_norm_quant: hidden %d > %d", hidden, kMaxRowLds);
+  return check_hip(bq::launch_norm_quant(src, gamma, x_i8, x_sa, seq_len, hidden, block, sqrt_n,
+                                         n_eps, S(stream)), "norm_quant");
+}
+
+int bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa, int cols, int seq_len,
+                   int block, int apply_fwht, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!src || !x_i8 || !x_sa) return fail(BQ_ERR_INVALID, "bq_block_quant: null pointer");
+  if (apply_fwht ? !fwht_block_ok(block) : !(pow2(block) && block >= 16 && block <= 512))
+    return fail(BQ_ERR_SHAPE, "bq_block_quant: unsupported block %d", block);
+  if (cols <= 0 || cols % 64 || cols % block)  // runtime.mojo:68-70
+    return fail(BQ_ERR_SHAPE, "bq_block_quant: cols %d must be a multiple of 64 and of block %d", cols, block);
+  return check_hip(bq::launch_block_quant(src, x_i8, x_sa, seq_len, cols, block, apply_fwht,
+                                          S(stream)), "block_quant");
+}
+
+int bq_linear(const int8_t* x_i8, const float* x_sa, const int8_t* w, const float* w_scale,
+              uint16_t* out, float* out_f32, int n_rows, int seq_len, int hidden, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !w || !w_scale || !out) return fail(BQ_ERR_INVALID, "bq_linear: null pointer");
+  if (n_rows <= 0 || n_rows % 16 || hidden <= 0 || hidden % 64)
+    return fail(BQ_ERR_SHAPE, "bq_linear: need n_rows %% 16 == 0 and hidden %% 64 == 0 (got %d, %d)",
+                n_rows, hidden);
+  bq::LinArgs a{};
+  if (!a16(x_i8) || !a16(w)) return fail(BQ_ERR_INVALID, "bq_linear: int8 operands must be 16-byte aligned");
+  a.seg[0] = {w, w_scale, out, out_f32, n_rows, 0};
+  a.nseg = 1;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_linear(a, 0, S(stream)), "linear");
+}
+
+int bq_block_linear(const int8_t* x_i8, const float* x_sa, const int8_t* w, const float* w_scale,
+                    uint16_t* out, float* out_f32, int n_rows, int k_dim, int seq_len, int block,
+                    void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !w || !w_scale || !out) return fail(BQ_ERR_INVALID, "bq_block_linear: null pointer");
+  if (!pow2(block) || block < 64)  // amx_gemm.mojo:222 (block % 64 == 0)
+    return fail(BQ_ERR_SHAPE, "bq_block_linear: block %d must be a power of two >= 64", block);
+  if (n_rows <= 0 || n_rows % 16 || k_dim <= 0 || k_dim % block)
+    return fail(BQ_ERR_SHAPE, "bq_block_linear: need n_rows %% 16 == 0 and k_dim %% block == 0 (got %d, %d, %d)",
+                n_rows, k_dim, block);
+  if (k_dim / block > 64)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_block_linear: k_dim/block = %d > 64", k_dim / block);
+  bq::LinArgs a{};
+  if (!a16(x_i8) || !a16(w)) return fail(BQ_ERR_INVALID, "bq_block_linear: int8 operands must be 16-byte aligned");
+  a.seg[0] = {w, w_scale, out, out_f32, n_rows, 0};
+  a.nseg = 1;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = k_dim; a.block = block;
+  return check_hip(bq::launch_linear(a, 1, S(stream)), "block_linear");
+}
+
+int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float* q_scale,
+           const int8_t* k_w, const float* k_scale, const int8_t* v_w, const float* v_scale,
+           uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, int qn, int kvn, int seq_len,
+           int hidden, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !q_w || !q_scale || !k_w || !k_scale || !v_w || !v_scale || !q_out ||
+      !k_out || !v_out)
+    return fail(BQ_ERR_INVALID, "bq_qkv: null pointer");
+  if (qn <= 0 || kvn <= 0 || qn % 16 || kvn % 16 || hidden <= 0 || hidden % 64)
+    return fail(BQ_ERR_SHAPE, "bq_qkv: need qn, kvn %% 16 == 0 and hidden %% 64 == 0");
+  if (!a16(x_i8) || !a16(q_w) || !a16(k_w) || !a16(v_w))
+    return fail(BQ_ERR_INVALID, "bq_qkv: int8 operands must be 16-byte aligned");
+  bq::LinArgs a{};
+  a.seg[0] = {q_w, q_scale, q_out, nullptr, qn, 0};
+  a.seg[1] = {k_w, k_scale, k_out, nullptr, kvn, qn / 16};
+  a.seg[2] = {v_w, v_scale, v_out, nullptr, kvn, qn / 16 + kvn / 16};
+  a.nseg = 3;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_linear(a, 0, S(stream)), "qkv");
+}
+
+int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
+                          int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
+                          void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!route_idx || !route_w || !expert_offset || !routes)
+    return fail(BQ_ERR_INVALID, "bq_moe_build_schedule: null pointer");
+  if (top_k <= 0 || experts <= 0) return fail(BQ_ERR_SHAPE, "bq_moe_build_schedule: bad top_k/experts");
+  if (experts > 256) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_build_schedule: experts %d > 256", experts);
+  return check_hip(bq::launch_build_schedule(route_idx, route_w, seq_len, top_k, expert_base,
+                                             experts, expert_offset,
+                                             reinterpret_cast<bq::Route*>(routes), S(stream)),
+                   "build_schedule");
+}
+
+int bq_moe_phase1_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
+                          const bq_route* routes, const int8_t* w_gate_up,
+                          const float* gate_up_scale, uint16_t* bucket, int experts_per_rank,
+                          int seq_len, int top_k, int hidden, int inter, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !expert_offset || !routes || !w_gate_up || !gate_up_scale || !bucket)
+    return fail(BQ_ERR_INVALID, "bq_moe_phase1_gate_up: null pointer");
+  if (experts_per_rank <= 0 || top_k <= 0 || hidden <= 0 || hidden % 64 || inter <= 0 || inter % 16)
+    return fail(BQ_ERR_SHAPE, "bq_moe_phase1_gate_up: need hidden %% 64 == 0, inter %% 16 == 0");
+  if (!a16(x_i8) || !a16(w_gate_up))
+    return fail(BQ_ERR_INVALID, "bq_moe_phase1_gate_up: int8 operands must be 16-byte aligned");
+  return check_hip(bq::launch_moe_phase1(x_i8, x_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_gate_up,
+                                         gate_up_scale, bucket, experts_per_rank, seq_len * top_k,
+                                         hidden, inter, S(stream)), "moe_phase1");
+}
+
+size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden) {
+  if (seq_len <= 0 || top_k <= 0 || hidden <= 0) return 0;
+  return bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
+}
+
+int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
+                       const int32_t* expert_offset, const bq_route* routes, const int8_t* w_down,
+                       const float* down_scale, float* moe_accum, uint16_t* moe_out,
+                       int experts_per_rank, int seq_len, int top_k, int hidden, int inter,
+                       int block, void* workspace, size_t workspace_bytes, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!bucket_i8 || !bucket_sa || !expert_offset || !routes || !w_down || !down_scale ||
+      !moe_accum || !moe_out || !workspace)
+    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: null pointer");
+  if (top_k <= 0 || top_k > 16) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: top_k %d not in [1,16]", top_k);
+  if (!pow2(block) || block < 64 || inter % block || inter % 64 || hidden % 16 || hidden <= 0)
+    return fail(BQ_ERR_SHAPE, "bq_moe_phase2_down: need block a power of two >= 64 dividing inter, hidden %% 16 == 0");
+  if (!a16(bucket_i8) || !a16(w_down))
+    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: int8 operands must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: workspace must be 256-byte aligned");
+  const size_t need = bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
+  if (workspace_bytes < need)
+    return fail(BQ_ERR_SHAPE, "bq_moe_phase2_down: workspace %zu < %zu bytes", workspace_bytes, need);
+  return check_hip(bq::launch_moe_phase2(bucket_i8, bucket_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_down,
+                                         down_scale, moe_accum, moe_out, experts_per_rank, seq_len,
+                                         seq_len * top_k, hidden, inter, block, workspace,
+                                         S(stream)), "moe_phase2");
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+// bq_device.hpp -- device-side building blocks shared by the butterquant HIP
+// kernels (gfx950 / CDNA4, wave64).
+//
+// Numerics follow the reference CPU path exactly where the reference fixes
+// them (all files are compiled with -ffp-contract=off; fmaf appears only where
+// the reference calls .fma):
+//   * f32 -> bf16 is round-to-nearest-even by bit arithmetic
+//     (butterquant/convert.mojo:14-17);
+//   * FWHT stages run strides 1,2,4,... as (a+b, a-b), then one multiply by
+//     f32(1/f64(sqrtf(B))) (butterquant/fwht.mojo:20-57);
+//   * quantization is q = clamp(rne(x * (127/amax)), -128, 127)
+//     (butterquant/kernels.mojo:68-78, simd_math/ops.mojo:26-31);
+//   * GELU is the reference's tanh form with its fast exp polynomial
+//     (simd_math/ops.mojo:73-156).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kInv127 = 1.0f / 127.0f;
+
+// ---------------------------------------------------------------------------
+// GPU weight layout "tile16x64": the int8 codes of W[N,K] are stored as 1 KiB
+// fragments of 16 rows x 64 K, fragment (n/16, k/64) at
+// ((n/16)*(K/64) + k/64) * 1024; inside it lane L = ((k%64)/16)*16 + n%16 owns
+// bytes [L*16, L*16+16) holding k%16 = 0..15.  One 16-byte load per lane
+// fetches exactly the B operand of one v_mfma_i32_16x16x64_i8 for 16 output
+// rows, and a wave's 64 loads cover 1 KiB of contiguous HBM.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline size_t tile_offset(int n, int k, int K) {
+  return ((size_t)(n >> 4) * (size_t)(K >> 6) + (size_t)(k >> 6)) * 1024u +
+         (size_t)((((k & 63) >> 4) << 4) + (n & 15)) * 16u + (size_t)(k & 15);
+}
+
+// The reference's load-time VNNI layout (butterquant/vnni.mojo:146-163).
+__host__ __device__ inline size_t vnni_offset(int n, int k, int K) {
+  return (size_t)(n / 32) * 32u * (size_t)K + (size_t)(k / 64) * 2048u +
+         (size_t)((n % 32) / 16) * 1024u + (size_t)((k % 64) / 4) * 64u +
+         (size_t)(n % 16) * 4u + (size_t)(k % 4);
+}
+
+// ---------------------------------------------------------------------------
+// scalar numerics
+// ---------------------------------------------------------------------------
+__device__ inline uint16_t f32_to_bf16(float v) {
+  uint32_t bits = __float_as_uint(v);
+  uint32_t rne = bits + ((bits >> 16) & 1u) + 0x7FFFu;
+  return (uint16_t)(rne >> 16);
+}
+
+__device__ inline float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+__device__ inline int8_t quantize_i8(float v, float inv) {
+  float r = __builtin_rintf(v * inv);  // v_rndne_f32: round half to even
+  r = r < -128.0f ? -128.0f : r;
+  r = r > 127.0f ? 127.0f : r;
+  return (int8_t)(int)r;
+}
+
+// f32(1.0 / f64(sqrtf(B))) (butterquant/fwht.mojo:55); host computes it.
+__host__ inline float fwht_scale_host(int block) {
+  float s = __builtin_sqrtf((float)block);
+  return (float)(1.0 / (double)s);
+}
+
+// simd_math/ops.mojo:73-96
+__device__ inline float exp_f32_fast(float x) {
+  const float LN2 = 0.6931471805599453f;
+  const float INV_LN2 = 1.4426950408889634f;
+  float xc = x > -87.0f ? x : -87.0f;
+  float xn = xc * INV_LN2;
+  int n = (int)__builtin_rintf(xn);
+  float r = xc - (float)n * LN2;
+  float p = 1.0f + r * (0.9999f + r * (0.4985f + r * (0.1681f)));
+  int nc = n > -126 ? n : -126;
+  float pow2n = __uint_as_float(((uint32_t)(nc + 127)) << 23);
+  return p * pow2n;
+}
+
+// simd_math/ops.mojo:128-141
+__device__ inline float tanh_f32(float x) {
+  uint32_t sign_bits = __float_as_uint(x) & 0x80000000u;
+  float ax = __uint_as_float(__float_as_uint(x) & 0x7FFFFFFFu);
+  float e = exp_f32_fast(-2.0f * ax);
+  float t = (1.0f - e) / (1.0f + e);
+  return __uint_as_float(__float_as_uint(t) ^ sign_bits);
+}
+
+// simd_math/ops.mojo:145-156
+__device__ inline float gelu_tanh_f32(float x) {
+  const float sqrt_2_over_pi = 0.7978845608028654f;
+  const float gelu_a = 0.044715f;
+  float x3 = x * x * x;
+  float inner = sqrt_2_over_pi * (x + gelu_a * x3);
+  float t = tanh_f32(inner);
+  return 0.5f * x * (1.0f + t);
+}
+
+// ---------------------------------------------------------------------------
+// wave helpers
+// ---------------------------------------------------------------------------
+__device__ inline int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// max over aligned groups of `width` lanes (width a power of two <= 64)
+__device__ inline float group_max(float v, int width) {
+  for (int o = width >> 1; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// In-wave FWHT of one segment of S = R*64 values (R = max(1, B/64)), value
+// index r*64 + lane.  For B < 64 the wave holds 64/B independent blocks (one
+// value per lane, block = lane / B).  Every (a, b) pair of a stage is
+// combined as a+b (lower index) and a-b (upper index), exactly as the
+// reference's stage loop, so the result is bit-identical to it.
+template <int R>
+__device__ inline void fwht_wave(float (&v)[R], int block) {
+  const int lane = lane_id();
+  for (int s = 1; s < block && s < kWave; s <<= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float p = __shfl_xor(v[r], s, kWave);
+      v[r] = (lane & s) ? (p - v[r]) : (v[r] + p);
+    }
+  }
+#pragma unroll
+  for (int rs = 1; rs < R; rs <<= 1) {
+    if (rs * kWave >= block) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r & rs) continue;
+      float a = v[r], b = v[r + rs];
+      v[r] = a + b;
+      v[r + rs] = a - b;
+    }
+  }
+}
+
+// 16-byte global loads/stores
+__device__ inline v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
+__device__ inline void st16(int8_t* p, v4i v) { *reinterpret_cast<v4i*>(p) = v; }
+
+__device__ inline v4i mfma16x16x64(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+}  // namespace bq

@@ -1,0 +1,65 @@
+// bq_kernels.hpp -- host-side launch interface of the butterquant HIP kernels
+// (internal to the library; the public C ABI is include/bq_api.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bq {
+
+// One output segment of a (possibly fused) per-row / per-block linear: the
+// fused q/k/v projection (butterquant_kernels/linear.mojo:273-326) runs as
+// three segments of one launch sharing the activation.
+struct LinSeg {
+  const int8_t* w;   // tile16x64 codes [n, K]
+  const float* ws;   // per-row weight scale [n]
+  uint16_t* out;     // bf16 [M, n]
+  float* out_f32;    // optional f32 [M, n] (pre-cast values)
+  int n;             // output rows of this segment
+  int tile0;         // first global n-tile (16 rows) of this segment
+};
+
+struct LinArgs {
+  LinSeg seg[3];
+  int nseg;
+  const int8_t* act;  // int8 [M, K] row-major
+  const float* sa;    // per-row [M] or per-block [M, K/block] activation scales
+  int M, K;
+  int block;          // per-block K block (multiple of 64); K for per-row
+};
+
+hipError_t launch_retile(const int8_t* src, int layout, int8_t* dst, int N, int K, hipStream_t st);
+hipError_t launch_unpack(const int8_t* src, int8_t* dst, int N, int K, hipStream_t st);
+hipError_t launch_pack_colsum(const int8_t* src, int8_t* dst, float* colsum, int N, int K,
+                              int block_cols, int row_major, hipStream_t st);
+hipError_t launch_quantize_weight(const uint16_t* w, const float* gamma, int8_t* q, float* scales,
+                                  int rows, int cols, int block, int per_block, hipStream_t st);
+
+int pick_port_unroll(int cols);
+hipError_t launch_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* xq, float* sa,
+                             int seq_len, int hidden, int block, float sqrt_n, float n_eps,
+                             hipStream_t st);
+hipError_t launch_block_quant(const uint16_t* src, int8_t* xq, float* sa, int rows, int cols,
+                              int block, int apply_fwht, hipStream_t st);
+
+// per_block = 0: y = f32(acc) * (sa[m]/127) * ws[n]
+// per_block = 1: y = ws[n] * sum_b fma-chain f32(acc_b) * (sa[m,b]/127)
+hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st);
+
+struct Route { int32_t token; float weight; };
+
+hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
+                                 int top_k, int expert_base, int experts, int32_t* expert_offset,
+                                 Route* routes, hipStream_t st);
+hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
+                             const Route* routes, const int8_t* w_gu, const float* gu_scale,
+                             uint16_t* bucket, int experts, int max_routes, int hidden,
+                             int inter, hipStream_t st);
+size_t moe_phase2_workspace(int max_routes, int seq_len, int hidden);
+hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa,
+                             const int32_t* expert_offset, const Route* routes,
+                             const int8_t* w_down, const float* down_scale, float* accum,
+                             uint16_t* out, int experts, int seq_len, int max_routes, int hidden,
+                             int inter, int block, void* workspace, hipStream_t st);
+
+}  // namespace bq

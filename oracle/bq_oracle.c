@@ -1,0 +1,597 @@
+/*
+ * bq_oracle.c -- CPU restatement of the butterquant hot path (test
+ * infrastructure only: the parity checker and the CPU baseline).  See
+ * bq_oracle.h for the function list; each body cites the reference lines it
+ * follows.  Build: gcc -O2 -fPIC -ffp-contract=off -fno-fast-math (oracle/Makefile).
+ */
+#include "bq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* bf16                                                                      */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* convert.mojo:14-17 -- software RNE: (bits + ((bits>>16)&1) + 0x7FFF) >> 16 */
+uint16_t bqo_f32_to_bf16(float v) {
+    uint32_t bits = f2u(v);
+    uint32_t rne = bits + ((bits >> 16) & 1u) + 0x7FFFu;
+    return (uint16_t)(rne >> 16);
+}
+
+float bqo_bf16_to_f32(uint16_t b) { return u2f(((uint32_t)b) << 16); }
+
+/* ------------------------------------------------------------------------ */
+/* FWHT                                                                      */
+/* ------------------------------------------------------------------------ */
+
+static int is_fwht_block(int block) {
+    /* kernels.mojo:123-145 dispatch_fwht_block: 16,32,64,128,256,512 */
+    return block == 16 || block == 32 || block == 64 || block == 128 ||
+           block == 256 || block == 512;
+}
+
+/* fwht.mojo:55 -- Scalar[T](1.0 / Float64(sqrt[T,1](Scalar[T](block)))) */
+float bqo_fwht_scale(int block) {
+    float s = sqrtf((float)block);
+    return (float)(1.0 / (double)s);
+}
+
+/* fwht.mojo:20-57.  Stage s (stride 1<<s, ascending) maps every pair
+ * (i, i+stride) with bit s of i clear to (a+b, a-b).  The in-register stages
+ * (fwht.mojo:33-42) compute r*sign + partner with sign = -1 on lanes whose bit
+ * s is set, i.e. partner - self = a - b on the upper lane: the same values.
+ * Then every element is multiplied by the scale (fwht.mojo:55-57). */
+int bqo_fwht_block(float* buf, int block) {
+    if (!is_fwht_block(block)) return -1;
+    for (int stride = 1; stride < block; stride <<= 1) {
+        for (int i = 0; i < block; ++i) {
+            if (i & stride) continue;
+            float a = buf[i], b = buf[i + stride];
+            buf[i] = a + b;
+            buf[i + stride] = a - b;
+        }
+    }
+    float sc = bqo_fwht_scale(block);
+    for (int i = 0; i < block; ++i) buf[i] = buf[i] * sc;
+    return 0;
+}
+
+/* fwht.mojo:73-76 (cols % block must be 0: kernels.mojo:81-83 aborts) */
+int bqo_fwht_row(float* buf, int cols, int block) {
+    if (!is_fwht_block(block) || cols % block != 0) return -1;
+    for (int b = 0; b < cols / block; ++b) bqo_fwht_block(buf + (size_t)b * block, block);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantization                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* kernels.mojo:48-55 */
+float bqo_row_absmax(const float* x, int n) {
+    float m = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+/* simd_math/ops.mojo:26-31 quantize_i8: min(max(roundeven(v*inv), -128), 127) */
+static inline int8_t quantize_i8(float v, float inv) {
+    float r = nearbyintf(v * inv); /* default rounding mode: to nearest even */
+    if (r < -128.0f) r = -128.0f;
+    if (r > 127.0f) r = 127.0f;
+    return (int8_t)r;
+}
+
+/* kernels.mojo:68-78: scale = amax/127 (weights) or amax (activations);
+ * inv = 127/amax if amax > 0 else 0. */
+void bqo_quant_segment(const float* work, int8_t* qi, float* scale_slot, int n,
+                       int store_divided) {
+    float amax = bqo_row_absmax(work, n);
+    *scale_slot = store_divided ? amax / 127.0f : amax;
+    float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    for (int i = 0; i < n; ++i) qi[i] = quantize_i8(work[i], inv);
+}
+
+/* kernels.mojo:148-168 (single-sided; two-sided M-axis rotation is not on the
+ * hot path's recipes, gemma_4_moe_bq.mojo:91-121) */
+int bqo_rotate_and_quant(int block, float* work, int8_t* qi, float* scales,
+                         int rows, int cols, int per_block) {
+    if (!is_fwht_block(block) || cols % block != 0) return -1;
+    for (int r = 0; r < rows; ++r) bqo_fwht_row(work + (size_t)r * cols, cols, block);
+    if (per_block) { /* kernels.mojo:110-120 */
+        int nb = cols / block;
+        for (int r = 0; r < rows; ++r)
+            for (int b = 0; b < nb; ++b)
+                bqo_quant_segment(work + (size_t)r * cols + (size_t)b * block,
+                                  qi + (size_t)r * cols + (size_t)b * block,
+                                  scales + (size_t)r * nb + b, block, 1);
+    } else { /* kernels.mojo:105-107 */
+        for (int r = 0; r < rows; ++r)
+            bqo_quant_segment(work + (size_t)r * cols, qi + (size_t)r * cols,
+                              scales + r, cols, 1);
+    }
+    return 0;
+}
+
+/* kernels.mojo:36-45: g -> sign(g) * sqrt(max(|g|, eps)), stored bf16 */
+void bqo_bake_split_gain(uint16_t* gamma, int cols, float eps) {
+    for (int k = 0; k < cols; ++k) {
+        float g = bqo_bf16_to_f32(gamma[k]);
+        float a = fabsf(g);
+        float s = sqrtf(a > eps ? a : eps);
+        gamma[k] = bqo_f32_to_bf16(g < 0.0f ? -s : s);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* activation prep                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* simd_math/matrixops.mojo:233-246 with width = BW = 32 (AVX-512 bf16 lanes) */
+static int pick_port_unroll(int width, int cols) {
+    if (cols % (8 * width) == 0) return 8;
+    if (cols % (4 * width) == 0) return 4;
+    if (cols % (2 * width) == 0) return 2;
+    return 1;
+}
+
+/* rms_reduce_row = dot_to_scalar[hidden](src, src) (rmsnorm.mojo:16-17,
+ * dot_products.mojo:144-191).  PU accumulators of W=16 f32 lanes; per 32
+ * bf16: vdpbf16ps adds the odd product then the even product to lane j, each
+ * a single-rounded fma (exact bf16 products).  Then s = sum_p acc[p] lane-wise
+ * (dot_products.mojo:127-140) and a 16-lane halving-tree reduce_add. */
+float bqo_rms_reduce_row(const uint16_t* src, int hidden) {
+    enum { W = 16, BW = 32 };
+    int pu = pick_port_unroll(BW, hidden);
+    int stride = pu * BW;
+    float acc[8][W];
+    memset(acc, 0, sizeof(acc));
+    for (int i = 0; i < hidden / stride; ++i) {
+        for (int p = 0; p < pu; ++p) {
+            const uint16_t* x = src + (size_t)i * stride + (size_t)p * BW;
+            for (int j = 0; j < W; ++j) {
+                float o = bqo_bf16_to_f32(x[2 * j + 1]);
+                float e = bqo_bf16_to_f32(x[2 * j]);
+                acc[p][j] = fmaf(o, o, acc[p][j]);
+                acc[p][j] = fmaf(e, e, acc[p][j]);
+            }
+        }
+    }
+    float s[W];
+    for (int j = 0; j < W; ++j) s[j] = 0.0f;
+    for (int p = 0; p < pu; ++p)
+        for (int j = 0; j < W; ++j) s[j] = s[j] + acc[p][j];
+    for (int half = W / 2; half >= 1; half /= 2)
+        for (int j = 0; j < half; ++j) s[j] = s[j] + s[j + half];
+    return s[0];
+}
+
+/* runtime.mojo:11-37: inv_rms = sqrt_n / sqrt(ssq + n_eps); w = x*inv_rms*g;
+ * FWHT(block) over the row; per-row (sa = amax) or per-block quant. */
+int bqo_prepare_norm_activation(const uint16_t* src, const uint16_t* gamma,
+                                int8_t* x_i8, float* sa, int hidden, int block,
+                                float sqrt_n, float n_eps, int per_block) {
+    if (!is_fwht_block(block) || hidden % block != 0) return -1;
+    float* ws = (float*)malloc(sizeof(float) * (size_t)hidden);
+    float ssq = bqo_rms_reduce_row(src, hidden);
+    float inv_rms = sqrt_n / sqrtf(ssq + n_eps);
+    for (int k = 0; k < hidden; ++k) {
+        float x = bqo_bf16_to_f32(src[k]);
+        float g = bqo_bf16_to_f32(gamma[k]);
+        ws[k] = x * inv_rms * g;
+    }
+    bqo_fwht_row(ws, hidden, block);
+    if (per_block) {
+        for (int b = 0; b < hidden / block; ++b)
+            bqo_quant_segment(ws + b * block, x_i8 + b * block, sa + b, block, 0);
+    } else {
+        bqo_quant_segment(ws, x_i8, sa, hidden, 0);
+    }
+    free(ws);
+    return 0;
+}
+
+/* runtime.mojo:62-80 + quantize.mojo:12-23 */
+int bqo_prepare_block_activation(const uint16_t* src, int8_t* x_i8, float* sa,
+                                 int cols, int block, int apply_fwht) {
+    if (cols % block != 0 || block % 16 != 0) return -1;
+    if (apply_fwht && !is_fwht_block(block)) return -1;
+    float* ws = (float*)malloc(sizeof(float) * (size_t)cols);
+    for (int k = 0; k < cols; ++k) ws[k] = bqo_bf16_to_f32(src[k]);
+    if (apply_fwht) bqo_fwht_row(ws, cols, block);
+    for (int b = 0; b < cols / block; ++b)
+        bqo_quant_segment(ws + b * block, x_i8 + b * block, sa + b, block, 0);
+    free(ws);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* VNNI pack                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* vnni.mojo:146-163: 32 rows x 64 K per 2 KiB tile; within a tile two 16-row
+ * halves of 1 KiB, each the 16x16 dword transpose of the row-major bytes. */
+size_t bqo_vnni_offset(int n, int k, int cols) {
+    return (size_t)(n / 32) * 32 * (size_t)cols + (size_t)(k / 64) * 2048 +
+           (size_t)((n % 32) / 16) * 1024 + (size_t)((k % 64) / 4) * 64 +
+           (size_t)(n % 16) * 4 + (size_t)(k % 4);
+}
+
+/* vnni.mojo:31-114.  colsum = per-row sum of codes over each block_cols
+ * segment; row-major [rows, nb] or block-major [nb, rows] (vnni.mojo:61-64). */
+int bqo_pack_and_colsum_vnni(const int8_t* src, int8_t* dst, int rows, int cols,
+                             int block_cols, float* colsum, int colsum_row_major) {
+    if (cols % 64 != 0 || rows % 32 != 0 || block_cols <= 0 ||
+        cols % block_cols != 0 || block_cols % 16 != 0)
+        return -1; /* vnni.mojo:91-99 contracts */
+    int nb = cols / block_cols;
+    int8_t* tmp = (int8_t*)malloc((size_t)rows * cols);
+    for (int n = 0; n < rows; ++n) {
+        for (int b = 0; b < nb; ++b) {
+            int32_t acc = 0;
+            for (int k = b * block_cols; k < (b + 1) * block_cols; ++k)
+                acc += src[(size_t)n * cols + k];
+            float s = (float)acc;
+            if (colsum_row_major) colsum[(size_t)n * nb + b] = s;
+            else colsum[(size_t)b * rows + n] = s;
+        }
+        for (int k = 0; k < cols; ++k)
+            tmp[bqo_vnni_offset(n, k, cols)] = src[(size_t)n * cols + k];
+    }
+    memcpy(dst, tmp, (size_t)rows * cols); /* in-place capable, as pack.mojo:38-44 */
+    free(tmp);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMM                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* dot_products.mojo:7-37 restated: sum over k of (x^0x80 as u8) * w as i32,
+ * reading W through the packed layout (gemm.mojo:36-75). */
+static int32_t vnni_u8_dot(const int8_t* x, const int8_t* wp, int n, int K,
+                           int k_lo, int k_hi) {
+    int32_t acc = 0;
+    for (int k = k_lo; k < k_hi; ++k) {
+        uint8_t a = (uint8_t)x[k] ^ 0x80u;
+        acc += (int32_t)a * (int32_t)wp[bqo_vnni_offset(n, k, K)];
+    }
+    return acc;
+}
+
+static int32_t signed_dot(const int8_t* x, const int8_t* wp, int n, int K,
+                          int k_lo, int k_hi) {
+    int32_t acc = 0;
+    for (int k = k_lo; k < k_hi; ++k)
+        acc += (int32_t)x[k] * (int32_t)wp[bqo_vnni_offset(n, k, K)];
+    return acc;
+}
+
+void bqo_int_acc(const int8_t* act, int m, const int8_t* wpacked, int N, int K,
+                 int k_lo, int k_hi, int64_t* acc) {
+    for (int r = 0; r < m; ++r)
+        for (int n = 0; n < N; ++n) {
+            int64_t s = 0;
+            for (int k = k_lo; k < k_hi; ++k)
+                s += (int64_t)act[(size_t)r * K + k] *
+                     (int64_t)wpacked[bqo_vnni_offset(n, k, K)];
+            acc[(size_t)r * N + n] = s;
+        }
+}
+
+/* gemm.mojo:114-142 epilogue: ((f32(iacc) - 128*cs) * (sa*(1/127))) * sw */
+void bqo_gemm_i8_per_row(const int8_t* act, const float* act_scale, int m,
+                         const int8_t* wpacked, const float* wsc,
+                         const float* colsum, int n_rows, int K,
+                         uint16_t* out_bf16, float* out_f32) {
+    const float inv127 = 1.0f / 127.0f;
+    for (int r = 0; r < m; ++r) {
+        float ad = act_scale[r] * inv127;
+        for (int n = 0; n < n_rows; ++n) {
+            int32_t iacc = vnni_u8_dot(act + (size_t)r * K, wpacked, n, K, 0, K);
+            float corrected = (float)iacc - 128.0f * colsum[n];
+            float res = corrected * ad * wsc[n];
+            if (out_f32) out_f32[(size_t)r * n_rows + n] = res;
+            if (out_bf16) out_bf16[(size_t)r * n_rows + n] = bqo_f32_to_bf16(res);
+        }
+    }
+}
+
+/* gemm.mojo:173-215: facc = fma(f32(iacc_b) - 128*cs[b,n], sa[m,b]/127, facc)
+ * over blocks in order, then y = facc * sw. */
+void bqo_gemm_i8_per_block(const int8_t* act, const float* act_scale, int m,
+                           const int8_t* wpacked, const float* wsc,
+                           const float* colsum, int N, int k_dim, int block,
+                           uint16_t* out_bf16, float* out_f32) {
+    const float inv127 = 1.0f / 127.0f;
+    int nb = k_dim / block;
+    for (int r = 0; r < m; ++r)
+        for (int n = 0; n < N; ++n) {
+            float facc = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                int32_t iacc = vnni_u8_dot(act + (size_t)r * k_dim, wpacked, n,
+                                           k_dim, b * block, (b + 1) * block);
+                float adv = act_scale[(size_t)r * nb + b] * inv127;
+                float corrected = (float)iacc - 128.0f * colsum[(size_t)b * N + n];
+                facc = fmaf(corrected, adv, facc);
+            }
+            float res = facc * wsc[n];
+            if (out_f32) out_f32[(size_t)r * N + n] = res;
+            if (out_bf16) out_bf16[(size_t)r * N + n] = bqo_f32_to_bf16(res);
+        }
+}
+
+/* amx_gemm.mojo:28-44 (dequant_fused): f32(acc) * (sa*INV127) * ws */
+void bqo_gemm_signed_per_row(const int8_t* act, const float* act_scale, int m,
+                             const int8_t* wpacked, const float* wsc, int n_rows,
+                             int K, uint16_t* out_bf16, float* out_f32) {
+    const float inv127 = 1.0f / 127.0f;
+    for (int r = 0; r < m; ++r) {
+        float ad = act_scale[r] * inv127;
+        for (int n = 0; n < n_rows; ++n) {
+            int32_t acc = signed_dot(act + (size_t)r * K, wpacked, n, K, 0, K);
+            float res = (float)acc * ad * wsc[n];
+            if (out_f32) out_f32[(size_t)r * n_rows + n] = res;
+            if (out_bf16) out_bf16[(size_t)r * n_rows + n] = bqo_f32_to_bf16(res);
+        }
+    }
+}
+
+/* Per-block signed form with the VNNI path's explicit fma (gemm.mojo:208-209)
+ * applied to the signed accumulator (the AMX block_accumulate at
+ * amx_gemm.mojo:47-63 writes the same sum as slot + cv*adv). */
+void bqo_gemm_signed_per_block(const int8_t* act, const float* act_scale, int m,
+                               const int8_t* wpacked, const float* wsc, int N,
+                               int k_dim, int block, uint16_t* out_bf16,
+                               float* out_f32) {
+    const float inv127 = 1.0f / 127.0f;
+    int nb = k_dim / block;
+    for (int r = 0; r < m; ++r)
+        for (int n = 0; n < N; ++n) {
+            float facc = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                int32_t acc = signed_dot(act + (size_t)r * k_dim, wpacked, n, k_dim,
+                                         b * block, (b + 1) * block);
+                float adv = act_scale[(size_t)r * nb + b] * inv127;
+                facc = fmaf((float)acc, adv, facc);
+            }
+            float res = facc * wsc[n];
+            if (out_f32) out_f32[(size_t)r * N + n] = res;
+            if (out_bf16) out_bf16[(size_t)r * N + n] = bqo_f32_to_bf16(res);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoE                                                                       */
+/* ------------------------------------------------------------------------ */
+
+static inline float roundeven_f(float x) { return nearbyintf(x); }
+
+/* simd_math/ops.mojo:73-96 */
+float bqo_exp_f32_fast(float x) {
+    const float LN2 = 0.6931471805599453f;
+    const float INV_LN2 = 1.4426950408889634f;
+    float xc = x > -87.0f ? x : -87.0f;             /* max(x, -87) */
+    float xn = xc * INV_LN2;
+    int32_t n = (int32_t)roundeven_f(xn);
+    float r = xc - (float)n * LN2;
+    float p = 1.0f + r * (0.9999f + r * (0.4985f + r * (0.1681f)));
+    int32_t nc = n > -126 ? n : -126;
+    float pow2n = u2f(((uint32_t)(nc + 127)) << 23);
+    return p * pow2n;
+}
+
+/* simd_math/ops.mojo:128-141 */
+float bqo_tanh_f32(float x) {
+    uint32_t sign_bits = f2u(x) & 0x80000000u;
+    float ax = u2f(f2u(x) & 0x7FFFFFFFu);
+    float e = bqo_exp_f32_fast(-2.0f * ax);
+    float t = (1.0f - e) / (1.0f + e);
+    return u2f(f2u(t) ^ sign_bits);
+}
+
+/* simd_math/ops.mojo:145-156 */
+float bqo_gelu_tanh_f32(float x) {
+    const float sqrt_2_over_pi = 0.7978845608028654f;
+    const float gelu_a = 0.044715f;
+    float x3 = x * x * x;
+    float inner = sqrt_2_over_pi * (x + gelu_a * x3);
+    float t = bqo_tanh_f32(inner);
+    return 0.5f * x * (1.0f + t);
+}
+
+/* simd_math/exponential.mojo:178-194 */
+float bqo_fast_exp_softmax_biased(float x) {
+    const float A_MAGIC = 12102203.16156148f;
+    const float BIAS_F = 1059208216.0f;
+    const float INV_TWO23 = 1.0f / (float)(1 << 23);
+    const float QC_A = 1.6501418352127075f;
+    const float QC_B = -0.37554836273193359f;
+    const float QC_C = 0.38696467876434326f;
+    int32_t i = (int32_t)(A_MAGIC * x + BIAS_F);
+    uint32_t u = (uint32_t)i;
+    float k = u2f(u);
+    float f = (float)(u & 0x7FFFFFu) * INV_TWO23;
+    return k * (QC_A + f * (QC_B + f * QC_C));
+}
+
+/* moe_router.mojo:43-57 insert_candidate + :276-293 softmax merge */
+void bqo_route_topk_softmax(const float* logits, int T, int E, int top_k,
+                            int32_t* route_idx, float* route_w) {
+    int32_t* ce = (int32_t*)malloc(sizeof(int32_t) * top_k);
+    float* cl = (float*)malloc(sizeof(float) * top_k);
+    float* ev = (float*)malloc(sizeof(float) * top_k);
+    for (int t = 0; t < T; ++t) {
+        for (int k = 0; k < top_k; ++k) { ce[k] = -1; cl[k] = -INFINITY; }
+        const float* row = logits + (size_t)t * E;
+        for (int e = 0; e < E; ++e) {
+            float lg = row[e];
+            for (int k = 0; k < top_k; ++k) {
+                if (lg > cl[k] || (lg == cl[k] && e < ce[k])) {
+                    for (int j = top_k - 1; j > k; --j) { ce[j] = ce[j - 1]; cl[j] = cl[j - 1]; }
+                    ce[k] = e; cl[k] = lg;
+                    break;
+                }
+            }
+        }
+        float mx = cl[0], sum = 0.0f;
+        for (int k = 0; k < top_k; ++k) { ev[k] = bqo_fast_exp_softmax_biased(cl[k] - mx); sum += ev[k]; }
+        float inv_sum = 1.0f / sum;
+        for (int k = 0; k < top_k; ++k) {
+            route_idx[(size_t)t * top_k + k] = ce[k];
+            route_w[(size_t)t * top_k + k] = ev[k] * inv_sum * 1.0f;
+        }
+    }
+    free(ce); free(cl); free(ev);
+}
+
+/* moe_router.mojo:60-106 */
+void bqo_build_schedule(const int32_t* route_idx, const float* route_w, int T,
+                        int top_k, int E, int32_t* expert_offset,
+                        bqo_route* routes) {
+    int32_t* counts = (int32_t*)calloc((size_t)E, sizeof(int32_t));
+    int32_t* wr = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < top_k; ++k) {
+            int e = route_idx[(size_t)t * top_k + k];
+            if (e >= 0 && e < E) counts[e] += 1;
+        }
+    int32_t running = 0;
+    for (int e = 0; e < E; ++e) { expert_offset[e] = running; wr[e] = running; running += counts[e]; }
+    expert_offset[E] = running;
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < top_k; ++k) {
+            size_t slot = (size_t)t * top_k + k;
+            int e = route_idx[slot];
+            if (e >= 0 && e < E) {
+                routes[wr[e]].token = t;
+                routes[wr[e]].weight = route_w[slot];
+                wr[e] += 1;
+            }
+        }
+    free(counts); free(wr);
+}
+
+/* moe.mojo:25-129: bucket[rec, it*32+j] = bf16(gelu(g) * u) with
+ * g = ((f32(iacc)-128cs)*(sa/127))*sw for gate row it*32+j and up row
+ * inter + it*32+j of the expert (gate tile it, up tile n_inter_tiles+it). */
+void bqo_moe_phase1(const int8_t* x_i8, const float* x_sa, int hidden,
+                    const int32_t* expert_offset, const bqo_route* routes, int E,
+                    const int8_t* w_gu_packed, const float* gu_scale,
+                    const float* gu_colsum, int inter, uint16_t* bucket) {
+    const float inv127 = 1.0f / 127.0f;
+    int gate_up = 2 * inter;
+    for (int e = 0; e < E; ++e) {
+        const int8_t* w = w_gu_packed + (size_t)e * gate_up * hidden;
+        const float* wsc = gu_scale + (size_t)e * gate_up;
+        const float* cs = gu_colsum + (size_t)e * gate_up;
+        for (int rec = expert_offset[e]; rec < expert_offset[e + 1]; ++rec) {
+            int tok = routes[rec].token;
+            const int8_t* x = x_i8 + (size_t)tok * hidden;
+            float ad = x_sa[tok] * inv127;
+            for (int i = 0; i < inter; ++i) {
+                int ng = i, nu = inter + i;
+                int32_t ga = vnni_u8_dot(x, w, ng, hidden, 0, hidden);
+                int32_t ua = vnni_u8_dot(x, w, nu, hidden, 0, hidden);
+                float gv = ((float)ga - 128.0f * cs[ng]) * ad * wsc[ng];
+                float uv = ((float)ua - 128.0f * cs[nu]) * ad * wsc[nu];
+                float res = bqo_gelu_tanh_f32(gv) * uv;
+                bucket[(size_t)rec * inter + i] = bqo_f32_to_bf16(res);
+            }
+        }
+    }
+}
+
+/* moe.mojo:167-295: accum zeroed; experts ascending, records ascending;
+ * facc = fma over blocks; accum[tok] += (facc*sw)*route_w; out = bf16(accum). */
+void bqo_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, int inter,
+                    int block, const int32_t* expert_offset,
+                    const bqo_route* routes, int E, int T,
+                    const int8_t* w_d_packed, const float* d_scale,
+                    const float* d_colsum, int hidden, float* accum,
+                    uint16_t* out) {
+    const float inv127 = 1.0f / 127.0f;
+    int nb = inter / block;
+    size_t data_n = (size_t)E * hidden;
+    memset(accum, 0, sizeof(float) * (size_t)T * hidden);
+    for (int e = 0; e < E; ++e) {
+        const int8_t* w = w_d_packed + (size_t)e * hidden * inter;
+        const float* wsc = d_scale + (size_t)e * hidden;
+        size_t e_row_base = (size_t)e * hidden;
+        for (int rec = expert_offset[e]; rec < expert_offset[e + 1]; ++rec) {
+            const int8_t* x = bucket_i8 + (size_t)rec * inter;
+            float* dst = accum + (size_t)routes[rec].token * hidden;
+            float rw = routes[rec].weight;
+            for (int n = 0; n < hidden; ++n) {
+                float facc = 0.0f;
+                for (int b = 0; b < nb; ++b) {
+                    int32_t iacc = vnni_u8_dot(x, w, n, inter, b * block, (b + 1) * block);
+                    float adv = bucket_sa[(size_t)rec * nb + b] * inv127;
+                    float ccs = d_colsum[(size_t)b * data_n + e_row_base + n];
+                    float corrected = (float)iacc - 128.0f * ccs;
+                    facc = fmaf(corrected, adv, facc);
+                }
+                float res = facc * wsc[n] * rw;
+                dst[n] = dst[n] + res;
+            }
+        }
+    }
+    for (size_t i = 0; i < (size_t)T * hidden; ++i) out[i] = bqo_f32_to_bf16(accum[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic inputs                                                          */
+/* ------------------------------------------------------------------------ */
+
+uint64_t bqo_splitmix64(uint64_t* state) {
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* uniform in (0,1]: (top 53 bits + 1) * 2^-53 */
+static double u01(uint64_t* st) {
+    return ((double)(bqo_splitmix64(st) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+void bqo_synth_normal_f32(uint64_t seed, double sigma, float* out, size_t n) {
+    uint64_t st = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        double u1 = u01(&st), u2 = u01(&st);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(sigma * r * cos(two_pi * u2));
+        if (i + 1 < n) out[i + 1] = (float)(sigma * r * sin(two_pi * u2));
+    }
+}
+
+void bqo_synth_normal_bf16(uint64_t seed, double sigma, uint16_t* out, size_t n) {
+    const size_t chunk = 1 << 16;
+    float* tmp = (float*)malloc(sizeof(float) * chunk);
+    /* one generator stream across chunks: regenerate with a running state */
+    uint64_t st = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    size_t i = 0;
+    while (i < n) {
+        size_t m = n - i < chunk ? n - i : chunk;
+        for (size_t j = 0; j < m; j += 2) {
+            double u1 = u01(&st), u2 = u01(&st);
+            double r = sqrt(-2.0 * log(u1));
+            tmp[j] = (float)(sigma * r * cos(two_pi * u2));
+            if (j + 1 < m) tmp[j + 1] = (float)(sigma * r * sin(two_pi * u2));
+        }
+        for (size_t j = 0; j < m; ++j) out[i + j] = bqo_f32_to_bf16(tmp[j]);
+        i += m;
+    }
+    free(tmp);
+}

@@ -1,0 +1,368 @@
+"""numpy front-end of the C oracle (oracle/bq_oracle.c) and of the CPU baseline
+(oracle/cpu_baseline.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as the
+checker, and by bench.py's cpu_baseline leg.  The HIP library never calls it.
+Every wrapper names the reference lines its C function restates.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+BUILD = os.path.join(HERE, "_build")
+_ORACLE = os.path.join(BUILD, "libbq_oracle.so")
+_CPU = os.path.join(BUILD, "libbq_cpu_baseline.so")
+
+
+def build() -> None:
+    """Compile the oracle and the CPU baseline (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _load(path):
+    if not os.path.exists(path):
+        build()
+    return C.CDLL(path)
+
+
+_lib = None
+_cpu = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load(_ORACLE)
+        _declare(_lib)
+    return _lib
+
+
+def cpu():
+    global _cpu
+    if _cpu is None:
+        _cpu = _load(_CPU)
+        _declare(_cpu)
+        _cpu.bqcpu_isa.restype = C.c_char_p
+    return _cpu
+
+
+def _declare(L):
+    L.bqo_f32_to_bf16.restype = C.c_uint16
+    L.bqo_f32_to_bf16.argtypes = [C.c_float]
+    L.bqo_fwht_scale.restype = C.c_float
+    L.bqo_fwht_scale.argtypes = [C.c_int]
+    L.bqo_rms_reduce_row.restype = C.c_float
+    for name in ("bqo_exp_f32_fast", "bqo_tanh_f32", "bqo_gelu_tanh_f32",
+                 "bqo_fast_exp_softmax_biased"):
+        getattr(L, name).restype = C.c_float
+        getattr(L, name).argtypes = [C.c_float]
+    L.bqo_vnni_offset.restype = C.c_size_t
+    L.bqo_vnni_offset.argtypes = [C.c_int, C.c_int, C.c_int]
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+ROUTE_DTYPE = np.dtype([("token", np.int32), ("weight", np.float32)])
+
+# --------------------------------------------------------------------------
+# bf16
+# --------------------------------------------------------------------------
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """butterquant/convert.mojo:14-17 software RNE, vectorised in numpy
+    (pinned against the C restatement in tests)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rne = (b + ((b >> 16) & 1) + 0x7FFF) & 0xFFFFFFFF
+    return (rne >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------------------
+# FWHT + quant
+# --------------------------------------------------------------------------
+
+
+def fwht_rows(x: np.ndarray, block: int) -> np.ndarray:
+    """butterquant/fwht.mojo:20-76 over every row (in a copy)."""
+    x = _c(x, np.float32).copy()
+    rows, cols = x.reshape(-1, x.shape[-1]).shape
+    for r in range(rows):
+        rc = lib().bqo_fwht_row(C.c_void_p(x.ctypes.data + r * cols * 4), cols, block)
+        if rc != 0:
+            raise ValueError(f"unsupported FWHT block {block} for cols {cols}")
+    return x
+
+
+def fwht_scale(block: int) -> float:
+    return float(lib().bqo_fwht_scale(block))
+
+
+def quant_segment(x: np.ndarray, store_divided: bool):
+    """butterquant/kernels.mojo:68-78 -> (codes int8, scale f32)."""
+    x = _c(x, np.float32)
+    q = np.empty(x.size, np.int8)
+    s = np.zeros(1, np.float32)
+    lib().bqo_quant_segment(_p(x), _p(q), _p(s), x.size, int(store_divided))
+    return q, s[0]
+
+
+def rotate_and_quant(w: np.ndarray, block: int, per_block: bool = False):
+    """Weight encoding (butterquant/kernels.mojo:148-168): f32 [N,K] ->
+    (int8 [N,K] row-major, scales [N] or [N, K/block])."""
+    w = _c(w, np.float32).copy()
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty((rows, cols // block) if per_block else (rows,), np.float32)
+    rc = lib().bqo_rotate_and_quant(block, _p(w), _p(q), _p(s), rows, cols, int(per_block))
+    if rc != 0:
+        raise ValueError("rotate_and_quant: bad block/cols")
+    return q, s
+
+
+def bake_split_gain(gamma_bf16: np.ndarray, eps: float = 1e-12) -> np.ndarray:
+    g = _c(gamma_bf16, np.uint16).copy()
+    lib().bqo_bake_split_gain(_p(g), g.size, C.c_float(eps))
+    return g
+
+
+def rms_reduce_row(x_bf16: np.ndarray) -> float:
+    x = _c(x_bf16, np.uint16)
+    lib().bqo_rms_reduce_row.argtypes = [C.c_void_p, C.c_int]
+    return float(lib().bqo_rms_reduce_row(_p(x), x.size))
+
+
+def norm_consts(hidden: int):
+    """(sqrt_n, n_eps) as gemma_4_moe_bq.mojo:646-647 computes them in f32."""
+    sqrt_n = np.sqrt(np.float32(hidden), dtype=np.float32)
+    n_eps = np.float32(hidden) * np.float32(1e-6)
+    return float(sqrt_n), float(n_eps)
+
+
+def norm_quant(x_bf16: np.ndarray, gamma_bf16: np.ndarray, block: int = 128,
+               sqrt_n=None, n_eps=None):
+    """dispatch_bq_norm_quant (butterquant_kernels/linear.mojo:58-82 ->
+    runtime.mojo:11-37): bf16 [M,H] -> (int8 [M,H], sa [M])."""
+    x = _c(x_bf16, np.uint16)
+    g = _c(gamma_bf16, np.uint16)
+    m, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    q = np.empty((m, h), np.int8)
+    sa = np.empty(m, np.float32)
+    f = lib().bqo_prepare_norm_activation
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                  C.c_float, C.c_float, C.c_int]
+    for r in range(m):
+        rc = f(C.c_void_p(x.ctypes.data + r * h * 2), _p(g),
+               C.c_void_p(q.ctypes.data + r * h), C.c_void_p(sa.ctypes.data + r * 4),
+               h, block, sqrt_n, n_eps, 0)
+        if rc != 0:
+            raise ValueError("norm_quant: bad block/hidden")
+    return q, sa
+
+
+def block_quant(x_bf16: np.ndarray, block: int, apply_fwht: bool):
+    """dispatch_bq_block_quant (linear.mojo:182-205 -> runtime.mojo:62-80):
+    bf16 [R,cols] -> (int8 [R,cols], sa [R, cols/block])."""
+    x = _c(x_bf16, np.uint16)
+    r, cols = x.shape
+    nb = cols // block
+    q = np.empty((r, cols), np.int8)
+    sa = np.empty((r, nb), np.float32)
+    f = lib().bqo_prepare_block_activation
+    for i in range(r):
+        rc = f(C.c_void_p(x.ctypes.data + i * cols * 2), C.c_void_p(q.ctypes.data + i * cols),
+               C.c_void_p(sa.ctypes.data + i * nb * 4), cols, block, int(apply_fwht))
+        if rc != 0:
+            raise ValueError("block_quant: bad block/cols")
+    return q, sa
+
+
+# --------------------------------------------------------------------------
+# pack
+# --------------------------------------------------------------------------
+
+
+def vnni_offsets(rows: int, cols: int) -> np.ndarray:
+    """The pack bijection (butterquant/vnni.mojo:146-163) as an index array:
+    packed[off[n,k]] = W[n,k]."""
+    n = np.arange(rows, dtype=np.int64)[:, None]
+    k = np.arange(cols, dtype=np.int64)[None, :]
+    return ((n // 32) * 32 * cols + (k // 64) * 2048 + ((n % 32) // 16) * 1024
+            + ((k % 64) // 4) * 64 + (n % 16) * 4 + (k % 4))
+
+
+def pack_and_colsum(w_i8: np.ndarray, block_cols: int | None = None,
+                    colsum_row_major: bool = True):
+    """butterquant/vnni.mojo:86-114 -> (packed int8 [rows*cols], colsum f32)."""
+    w = _c(w_i8, np.int8)
+    rows, cols = w.shape
+    bc = cols if block_cols is None else block_cols
+    nb = cols // bc
+    dst = np.empty(rows * cols, np.int8)
+    cs = np.empty(rows * nb, np.float32)
+    rc = lib().bqo_pack_and_colsum_vnni(_p(w), _p(dst), rows, cols, bc, _p(cs),
+                                        int(colsum_row_major))
+    if rc != 0:
+        raise ValueError("pack_and_colsum: contract violated")
+    return dst, cs
+
+
+# --------------------------------------------------------------------------
+# GEMM
+# --------------------------------------------------------------------------
+
+
+def linear(act, sa, wpacked, wsc, colsum, n_rows: int):
+    """VNNI per-row linear (butterquant/gemm.mojo:114-170) -> (bf16, f32)."""
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    wpacked = _c(wpacked, np.int8); wsc = _c(wsc, np.float32); colsum = _c(colsum, np.float32)
+    m, K = act.shape
+    ob = np.empty((m, n_rows), np.uint16)
+    of = np.empty((m, n_rows), np.float32)
+    lib().bqo_gemm_i8_per_row(_p(act), _p(sa), m, _p(wpacked), _p(wsc), _p(colsum),
+                              n_rows, K, _p(ob), _p(of))
+    return ob, of
+
+
+def block_linear(act, sa, wpacked, wsc, colsum, n: int, block: int):
+    """VNNI per-block linear (butterquant/gemm.mojo:173-243) -> (bf16, f32)."""
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    wpacked = _c(wpacked, np.int8); wsc = _c(wsc, np.float32); colsum = _c(colsum, np.float32)
+    m, K = act.shape
+    ob = np.empty((m, n), np.uint16)
+    of = np.empty((m, n), np.float32)
+    lib().bqo_gemm_i8_per_block(_p(act), _p(sa), m, _p(wpacked), _p(wsc), _p(colsum),
+                                n, K, block, _p(ob), _p(of))
+    return ob, of
+
+
+def signed_linear(act, sa, wpacked, wsc, n_rows: int):
+    """Signed (AMX-branch) per-row epilogue (butterquant/amx_gemm.mojo:28-44)."""
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    wpacked = _c(wpacked, np.int8); wsc = _c(wsc, np.float32)
+    m, K = act.shape
+    ob = np.empty((m, n_rows), np.uint16)
+    of = np.empty((m, n_rows), np.float32)
+    lib().bqo_gemm_signed_per_row(_p(act), _p(sa), m, _p(wpacked), _p(wsc), n_rows, K,
+                                  _p(ob), _p(of))
+    return ob, of
+
+
+def signed_block_linear(act, sa, wpacked, wsc, n: int, block: int):
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    wpacked = _c(wpacked, np.int8); wsc = _c(wsc, np.float32)
+    m, K = act.shape
+    ob = np.empty((m, n), np.uint16)
+    of = np.empty((m, n), np.float32)
+    lib().bqo_gemm_signed_per_block(_p(act), _p(sa), m, _p(wpacked), _p(wsc), n, K, block,
+                                    _p(ob), _p(of))
+    return ob, of
+
+
+def int_acc(act, wpacked, n: int, k_lo: int = 0, k_hi: int | None = None):
+    act = _c(act, np.int8); wpacked = _c(wpacked, np.int8)
+    m, K = act.shape
+    k_hi = K if k_hi is None else k_hi
+    out = np.empty((m, n), np.int64)
+    lib().bqo_int_acc(_p(act), m, _p(wpacked), n, K, k_lo, k_hi, _p(out))
+    return out
+
+
+# --------------------------------------------------------------------------
+# MoE
+# --------------------------------------------------------------------------
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    f = lib().bqo_gelu_tanh_f32
+    return np.array([f(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))
+
+
+def exp_fast(x):
+    f = lib().bqo_exp_f32_fast
+    return np.array([f(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))
+
+
+def route_topk_softmax(logits: np.ndarray, top_k: int = 8):
+    """Top-k (moe_router.mojo:43-57) + softmax over the k (:276-293)."""
+    lg = _c(logits, np.float32)
+    T, E = lg.shape
+    idx = np.empty((T, top_k), np.int32)
+    w = np.empty((T, top_k), np.float32)
+    lib().bqo_route_topk_softmax(_p(lg), T, E, top_k, _p(idx), _p(w))
+    return idx, w
+
+
+def build_schedule(route_idx: np.ndarray, route_w: np.ndarray, E: int):
+    """kernels/moe_router.mojo:60-106 -> (expert_offset [E+1], routes)."""
+    ri = _c(route_idx, np.int32); rw = _c(route_w, np.float32)
+    T, k = ri.shape
+    eo = np.empty(E + 1, np.int32)
+    routes = np.zeros(T * k, ROUTE_DTYPE)
+    lib().bqo_build_schedule(_p(ri), _p(rw), T, k, E, _p(eo), _p(routes))
+    return eo, routes[: int(eo[E])]
+
+
+def moe_phase1(x_i8, x_sa, expert_offset, routes, w_gu_packed, gu_scale, gu_colsum,
+               inter: int):
+    """butterquant_kernels/moe.mojo:25-164 -> bucket bf16 [n_routes, inter]."""
+    x_i8 = _c(x_i8, np.int8); x_sa = _c(x_sa, np.float32)
+    eo = _c(expert_offset, np.int32); routes = np.ascontiguousarray(routes, ROUTE_DTYPE)
+    E = eo.size - 1
+    hidden = x_i8.shape[1]
+    bucket = np.zeros((max(int(eo[E]), 1), inter), np.uint16)
+    lib().bqo_moe_phase1(_p(x_i8), _p(x_sa), hidden, _p(eo), _p(routes), E,
+                         _p(_c(w_gu_packed, np.int8)), _p(_c(gu_scale, np.float32)),
+                         _p(_c(gu_colsum, np.float32)), inter, _p(bucket))
+    return bucket[: int(eo[E])]
+
+
+def moe_phase2(bucket_i8, bucket_sa, expert_offset, routes, T: int, w_d_packed,
+               d_scale, d_colsum, hidden: int, block: int = 64):
+    """butterquant_kernels/moe.mojo:167-335 -> (accum f32 [T,H], out bf16)."""
+    bi = _c(bucket_i8, np.int8); bs = _c(bucket_sa, np.float32)
+    eo = _c(expert_offset, np.int32); routes = np.ascontiguousarray(routes, ROUTE_DTYPE)
+    E = eo.size - 1
+    inter = bi.shape[1]
+    accum = np.empty((T, hidden), np.float32)
+    out = np.empty((T, hidden), np.uint16)
+    lib().bqo_moe_phase2(_p(bi), _p(bs), inter, block, _p(eo), _p(routes), E, T,
+                         _p(_c(w_d_packed, np.int8)), _p(_c(d_scale, np.float32)),
+                         _p(_c(d_colsum, np.float32)), hidden, _p(accum), _p(out))
+    return accum, out
+
+
+# --------------------------------------------------------------------------
+# synthetic inputs
+# --------------------------------------------------------------------------
+
+
+def synth_normal_bf16(seed: int, sigma: float, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    out = np.empty(n, np.uint16)
+    lib().bqo_synth_normal_bf16(C.c_uint64(seed), C.c_double(sigma), _p(out), C.c_size_t(n))
+    return out.reshape(shape)
+
+
+def synth_normal_f32(seed: int, sigma: float, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    out = np.empty(n, np.float32)
+    lib().bqo_synth_normal_f32(C.c_uint64(seed), C.c_double(sigma), _p(out), C.c_size_t(n))
+    return out.reshape(shape)

@@ -1,0 +1,87 @@
+"""CPU-side checks of the C ABI: libbq.so loads, exports every entry point
+include/bq_api.h declares, and rejects contract violations with the
+documented status codes before touching the GPU (the reference enforces
+these contracts with compile-time asserts / debug_assert / abort)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bq_api.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bq_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    import bq
+    return bq.lib()
+
+
+def test_header_symbols_exported(L):
+    names = declared_functions()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(L, n), f"libbq.so does not export {n}"
+
+
+def test_binding_covers_header():
+    import bq
+    assert set(declared_functions()) == set(bq.SIGNATURES)
+
+
+def test_version(L):
+    assert b"gfx950" in L.bq_version()
+
+
+P = C.c_void_p(16)  # a non-null placeholder: validation fails before any use
+
+
+def test_validation_errors(L):
+    # null pointers
+    assert L.bq_linear(None, P, P, P, P, None, 64, 1, 128, None) == 1
+    assert b"null" in L.bq_last_error()
+    # shape contracts (linear.mojo:132-136; vnni.mojo:91-99)
+    assert L.bq_linear(P, P, P, P, P, None, 15, 1, 128, None) == 2
+    assert L.bq_linear(P, P, P, P, P, None, 64, 1, 100, None) == 2
+    assert L.bq_block_linear(P, P, P, P, P, None, 64, 256, 1, 96, None) == 2
+    assert L.bq_block_linear(P, P, P, P, P, None, 64, 8192, 1, 64, None) == 4
+    assert L.bq_weight_retile(P, 0, P, 24, 128, None) == 2
+    assert L.bq_weight_retile(P, 7, P, 32, 128, None) == 1
+    assert L.bq_weight_retile(P, 1, P, 48, 128, None) == 2
+    assert L.bq_pack_colsum_vnni(P, C.c_void_p(32), P, 32, 100, 64, 1, None) == 2
+    assert L.bq_pack_colsum_vnni(P, C.c_void_p(32), P, 32, 128, 24, 1, None) == 2
+    assert L.bq_quantize_weight(P, None, P, P, 4, 256, 48, 0, None) == 2
+    assert L.bq_quantize_weight(P, None, P, P, 4, 32768, 128, 0, None) == 4
+    assert L.bq_norm_quant(P, P, P, P, 1, 2816, 48, C.c_float(1), C.c_float(1), None) == 2
+    assert L.bq_norm_quant(P, P, P, P, 1, 2880, 128, C.c_float(1), C.c_float(1), None) == 2
+    assert L.bq_block_quant(P, P, P, 704, 1, 256, 0, None) == 2
+    assert L.bq_moe_build_schedule(P, P, 4, 8, 0, 512, P, P, None) == 4
+    assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
+                                C.c_void_p(256), 0, None) == 2
+    assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
+                                C.c_void_p(100), 1 << 30, None) == 1
+
+
+def test_empty_batches_are_noops(L):
+    # seq_len <= 0 returns early (linear.mojo:134-135, 255-256; moe.mojo:317-318)
+    assert L.bq_linear(None, None, None, None, None, None, 64, 0, 128, None) == 0
+    assert L.bq_block_linear(None, None, None, None, None, None, 64, 256, 0, 64, None) == 0
+    assert L.bq_norm_quant(None, None, None, None, 0, 2816, 128, C.c_float(1), C.c_float(1), None) == 0
+    assert L.bq_block_quant(None, None, None, 704, -1, 64, 1, None) == 0
+    assert L.bq_moe_phase2_down(None, None, None, None, None, None, None, None, 128, 0, 8, 2816,
+                                704, 64, None, 0, None) == 0
+
+
+def test_workspace_size(L):
+    # per-route f32 results + per-token counters + per-token route lists
+    T, k, H = 32, 8, 2816
+    n = L.bq_moe_phase2_workspace_size(T, k, H)
+    assert n >= T * k * H * 4 + T * 4 + T * k * 4
+    assert L.bq_moe_phase2_workspace_size(0, 8, H) == 0

@@ -1,0 +1,365 @@
+"""GPU parity: libbq.so (through its C ABI) against the CPU oracle and the
+committed fixtures, on identical seeded inputs.
+
+Bar (tolerances are stated per assertion):
+  * int8 codes, re-tiled/unpacked bytes, colsums, schedules: bit-exact;
+  * f32 outputs of the linears and the MoE: bit-exact with the oracle's
+    signed-form restatement (which equals the reference's VNNI u8/colsum
+    form whenever |sum (x+128)w| < 2^24, asserted where it matters); the
+    north-star tolerance (normwise rel 1e-3, cosine > 0.9999) is checked too.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
+ONE = 0x3F80
+
+
+# ---------------------------------------------------------------- helpers
+def dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    import torch
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def tol_check(got, ref):
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    rel = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+    cos = got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref) + 1e-300)
+    assert rel <= 1e-3 and cos > 0.9999, (rel, cos)
+
+
+def weight(gpu, O, n, k, block, seed=0):
+    """Quantize with the oracle (reference recipe), upload, re-tile on GPU."""
+    wf = O.bf16_to_f32(O.synth_normal_bf16(seed, 0.02, (n, k)))
+    q, s = O.rotate_and_quant(wf, block)
+    t = gpu.retile(dev(q.reshape(-1)), n, k)
+    return q, s, gpu.ButterquantWeight(t, dev(s), n, k)
+
+
+@pytest.fixture(scope="module")
+def G():
+    return dict(np.load(GOLDEN, allow_pickle=False))
+
+
+# ---------------------------------------------------------------- layout
+def test_retile_unpack_roundtrip(gpu):
+    rng = np.random.default_rng(0)
+    n, k = 96, 320
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    t = gpu.retile(dev(w.reshape(-1)), n, k)
+    th = host(t)
+    # tile16x64 definition: fragment (n/16, k/64), lane ((k%64)/16)*16 + n%16
+    nn, kk = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    off = ((nn // 16) * (k // 64) + kk // 64) * 1024 + (((kk % 64) // 16) * 16 + nn % 16) * 16 + kk % 16
+    np.testing.assert_array_equal(th[off], w)
+    np.testing.assert_array_equal(host(gpu.unpack(t, n, k)), w)
+
+
+def test_retile_from_reference_vnni(gpu, O):
+    rng = np.random.default_rng(1)
+    n, k = 64, 256
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    p, _ = O.pack_and_colsum(w)
+    a = gpu.retile(dev(p), n, k, gpu.LAYOUT_VNNI)
+    b = gpu.retile(dev(w.reshape(-1)), n, k)
+    np.testing.assert_array_equal(host(a), host(b))
+
+
+@pytest.mark.parametrize("block,row_major", [(None, True), (64, False), (16, True)])
+def test_pack_colsum_vnni(gpu, O, G, block, row_major):
+    w = G["pack_w"]
+    p, cs = gpu.pack_colsum_vnni(dev(w), block, row_major)
+    rp, rcs = O.pack_and_colsum(w, block, row_major)
+    np.testing.assert_array_equal(host(p), rp)
+    np.testing.assert_array_equal(host(cs), rcs)
+    if block is None:
+        np.testing.assert_array_equal(host(p), G["pack_vnni"])
+        np.testing.assert_array_equal(host(cs), G["pack_colsum"])
+
+
+@pytest.mark.parametrize("B,per_block", [(128, False), (64, False), (16, False), (256, False),
+                                         (512, False), (64, True), (32, True)])
+def test_quantize_weight(gpu, O, B, per_block):
+    n, k = 48, 1024
+    w = O.synth_normal_bf16(0, 0.02, (n, k))
+    q, s = gpu.quantize_weight(dev(w), B, per_block)
+    rq, rs = O.rotate_and_quant(O.bf16_to_f32(w), B, per_block)
+    np.testing.assert_array_equal(host(q), rq)
+    np.testing.assert_array_equal(host(s), rs)
+
+
+def test_quantize_weight_golden(gpu, G):
+    q, s = gpu.quantize_weight(dev(G["rq_w"]), 128)
+    np.testing.assert_array_equal(host(q), G["rq_codes"])
+    np.testing.assert_array_equal(host(s), G["rq_scales"])
+    q, s = gpu.quantize_weight(dev(G["rq_w"]), 64, True)
+    np.testing.assert_array_equal(host(q), G["rq_codes_pb64"])
+    np.testing.assert_array_equal(host(s), G["rq_scales_pb64"])
+
+
+# ---------------------------------------------------------------- activations
+@pytest.mark.parametrize("H,B", [(2816, 128), (4096, 128), (2112, 64), (512, 16), (4096, 512),
+                                 (1024, 32), (8192, 256)])
+def test_norm_quant(gpu, O, H, B):
+    x = O.synth_normal_bf16(1, 1.0, (5, H))
+    g = O.f32_to_bf16(O.synth_normal_f32(9, 0.3, (H,)) + 1.0)
+    q, sa = gpu.norm_quant(dev(x), dev(g), B)
+    rq, rsa = O.norm_quant(x, g, B)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(q), rq)
+
+
+def test_norm_quant_golden(gpu, G):
+    q, sa = gpu.norm_quant(dev(G["nq_x"]), dev(G["nq_gamma"]), 128)
+    np.testing.assert_array_equal(host(q), G["nq_codes"])
+    np.testing.assert_array_equal(host(sa), G["nq_sa"])
+
+
+def test_norm_quant_zero_row(gpu, O):
+    x = np.zeros((2, 256), np.uint16)
+    x[1] = O.synth_normal_bf16(3, 1.0, (256,))
+    q, sa = gpu.norm_quant(dev(x), dev(np.full(256, ONE, np.uint16)), 128)
+    assert host(sa)[0] == 0.0 and (host(q)[0] == 0).all()
+    rq, rsa = O.norm_quant(x, np.full(256, ONE, np.uint16), 128)
+    np.testing.assert_array_equal(host(q), rq)
+
+
+@pytest.mark.parametrize("cols,B,fwht", [(704, 64, True), (2112, 64, True), (4096, 256, False),
+                                         (8192, 512, False), (512, 16, True), (512, 32, False),
+                                         (1024, 128, True)])
+def test_block_quant(gpu, O, cols, B, fwht):
+    x = O.synth_normal_bf16(2, 1.0, (37, cols))
+    q, sa = gpu.block_quant(dev(x), B, fwht)
+    rq, rsa = O.block_quant(x, B, fwht)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(q), rq)
+
+
+def test_block_quant_golden(gpu, G):
+    q, sa = gpu.block_quant(dev(G["bq_x"]), 64, True)
+    np.testing.assert_array_equal(host(q), G["bq_codes"])
+    np.testing.assert_array_equal(host(sa), G["bq_sa"])
+
+
+# ---------------------------------------------------------------- linears
+@pytest.mark.parametrize("M,K", [(1, 256), (1, 2816), (2, 2816), (16, 2816), (17, 256),
+                                 (40, 512), (128, 256), (300, 256)])
+def test_linear(gpu, O, M, K):
+    N = 256
+    q, s, W = weight(gpu, O, N, K, 128)
+    p, cs = O.pack_and_colsum(q)
+    x = O.synth_normal_bf16(1, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+    rb, rf = O.linear(xq, sa, p, s, cs, N)          # reference VNNI (u8, colsum) form
+    assert np.abs((xq.astype(np.int64) + 128) @ q.astype(np.int64).T).max() < 2 ** 24
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+    tol_check(host(of), rf)
+
+
+def test_linear_golden(gpu, G):
+    W = gpu.ButterquantWeight(gpu.retile(dev(G["rq_codes"].reshape(-1)), 64, 256),
+                              dev(G["rq_scales"]), 64, 256)
+    ob, of = gpu.linear(dev(G["lin_xq"]), dev(G["lin_sa"]), W, want_f32=True)
+    np.testing.assert_array_equal(host(of), G["lin_out_f32"])
+    np.testing.assert_array_equal(host(ob), G["lin_out_bf16"])
+
+
+@pytest.mark.parametrize("M,K,B", [(1, 2112, 64), (3, 4096, 256), (16, 8192, 512),
+                                   (17, 2112, 64), (33, 1024, 256), (100, 1024, 512),
+                                   (64, 704, 64)])
+def test_block_linear(gpu, O, M, K, B):
+    N = 128
+    q, s, W = weight(gpu, O, N, K, B, seed=4)
+    p, cs = O.pack_and_colsum(q, B, False)
+    x = O.synth_normal_bf16(5, 1.0, (M, K))
+    xq, sa = O.block_quant(x, B, B == 64)
+    ob, of = gpu.block_linear(dev(xq), dev(sa), W, B, want_f32=True)
+    rb, rf = O.block_linear(xq, sa, p, s, cs, N, B)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
+def test_block_linear_golden(gpu, G):
+    W = gpu.ButterquantWeight(gpu.retile(dev(G["blin_codes"].reshape(-1)), 64, 256),
+                              dev(G["blin_scales"]), 64, 256)
+    ob, of = gpu.block_linear(dev(G["blin_xq"]), dev(G["blin_sa"]), W, 64, want_f32=True)
+    np.testing.assert_array_equal(host(of), G["blin_out_f32"])
+    np.testing.assert_array_equal(host(ob), G["blin_out_bf16"])
+
+
+@pytest.mark.parametrize("M", [1, 20])
+def test_qkv_matches_three_linears(gpu, O, M):
+    K = 512
+    Ws = [weight(gpu, O, n, K, 128, seed=s)[2] for n, s in ((256, 1), (128, 2), (128, 3))]
+    x = O.synth_normal_bf16(6, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    outs = gpu.qkv(dev(xq), dev(sa), *Ws)
+    for o, W in zip(outs, Ws):
+        np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
+
+
+@pytest.mark.parametrize("M", [1, 512])
+def test_linear_full_size(gpu, O, M):
+    """Config sizes K = N = 4096: all rows against an exact f64 integer matmul
+    with the f32 epilogue in the reference's op order, and sampled rows
+    against the oracle."""
+    N = K = 4096
+    q, s, W = weight(gpu, O, N, K, 128)
+    x = O.synth_normal_bf16(1, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+    acc = xq.astype(np.float64) @ q.astype(np.float64).T          # exact: |acc| < 2^53
+    inv127 = np.float32(1.0) / np.float32(127.0)
+    ref = (acc.astype(np.float32) * (sa * inv127)[:, None]) * s[None, :]
+    np.testing.assert_array_equal(host(of), ref.astype(np.float32))
+    rows = np.unique(np.linspace(0, M - 1, 3).astype(int))
+    p, cs = O.pack_and_colsum(q)
+    rb, rf = O.linear(xq[rows], sa[rows], p, s, cs, N)
+    np.testing.assert_array_equal(host(of)[rows], rf)
+    tol_check(host(of), ref)
+
+
+# ---------------------------------------------------------------- MoE
+def route_table(O, T, E=128, k=8, seed=2):
+    logits = O.synth_normal_f32(seed, 1.0, (T, E))
+    return O.route_topk_softmax(logits, k)
+
+
+@pytest.mark.parametrize("T", [1, 32, 1500, 2048])
+def test_build_schedule(gpu, O, T):
+    idx, w = route_table(O, T)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), 128)
+    reo, rroutes = O.build_schedule(idx, w, 128)
+    np.testing.assert_array_equal(host(eo), reo)
+    r = host(routes)
+    np.testing.assert_array_equal(r[:, 0], rroutes["token"])
+    np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
+
+
+def test_build_schedule_expert_range(gpu, O):
+    # expert-parallel slice [32, 64) as a rank of degree 4 would build it
+    idx, w = route_table(O, 40)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), 32, expert_base=32)
+    sel = (idx >= 32) & (idx < 64)
+    reo, rroutes = O.build_schedule(np.where(sel, idx - 32, -1).astype(np.int32), w, 32)
+    np.testing.assert_array_equal(host(eo), reo)
+    np.testing.assert_array_equal(host(routes)[: reo[-1], 0], rroutes["token"])
+
+
+def gpu_moe(gpu, xq, xsa, idx, w, Wgu, Wd, E, H, I):
+    import torch
+    T, k = idx.shape
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    bucket = gpu.moe_phase1(xq, xsa, eo, routes, Wgu, E, T, k, I)
+    bi8, bsa = gpu.block_quant(bucket, 64, True)
+    accum, out = gpu.moe_phase2(bi8, bsa, eo, routes, Wd, E, T, k, H)
+    torch.cuda.synchronize()
+    return eo, routes, bucket, bi8, bsa, accum, out
+
+
+def test_moe_golden(gpu, G):
+    E, H, I = 4, 128, 64
+    idx, w = G["moe_idx"], G["moe_w"]
+    Wgu = gpu.ButterquantWeight(gpu.retile(dev(G["moe_gq"].reshape(-1)), E * 2 * I, H),
+                                dev(G["moe_gs"]), E * 2 * I, H)
+    Wd = gpu.ButterquantWeight(gpu.retile(dev(G["moe_dq"].reshape(-1)), E * H, I),
+                               dev(G["moe_ds"]), E * H, I)
+    eo, routes, bucket, bi8, bsa, accum, out = gpu_moe(
+        gpu, dev(G["moe_xq"]), dev(G["moe_xsa"]), idx, w, Wgu, Wd, E, H, I)
+    np.testing.assert_array_equal(host(eo), G["moe_eo"])
+    np.testing.assert_array_equal(host(bucket), G["moe_bucket"])
+    np.testing.assert_array_equal(host(bi8), G["moe_bucket_i8"])
+    np.testing.assert_array_equal(host(bsa), G["moe_bucket_sa"])
+    np.testing.assert_array_equal(host(accum), G["moe_accum"])
+    np.testing.assert_array_equal(host(out), G["moe_out"])
+
+
+@pytest.fixture(scope="module")
+def moe_model(gpu, O):
+    """128-expert Gemma-4-26B-A4B expert weights (bf16 N(0, 0.02), numpy RNG),
+    quantized with the oracle's reference recipe, re-tiled on the GPU once."""
+    E, H, I = 128, 2816, 704
+    rng = np.random.default_rng(0)
+    gu = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((E * 2 * I, H), np.float32) * np.float32(0.02)))
+    gq, gs = O.rotate_and_quant(gu, 128)
+    del gu
+    dn = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((E * H, I), np.float32) * np.float32(0.02)))
+    dq, ds = O.rotate_and_quant(dn, 64)
+    del dn
+    Wgu = gpu.ButterquantWeight(gpu.retile(dev(gq.reshape(-1)), E * 2 * I, H), dev(gs), E * 2 * I, H)
+    Wd = gpu.ButterquantWeight(gpu.retile(dev(dq.reshape(-1)), E * H, I), dev(ds), E * H, I)
+    gp, gcs = O.pack_and_colsum(gq)
+    dp, dcs = O.pack_and_colsum(dq, 64, False)
+    return dict(E=E, H=H, I=I, gs=gs, ds=ds, gp=gp, gcs=gcs, dp=dp, dcs=dcs, Wgu=Wgu, Wd=Wd)
+
+
+def test_moe_model_shape_decode(gpu, O, moe_model):
+    """Gemma-4-26B-A4B expert shapes (H=2816, I=704, 128 experts, top-8), T=8."""
+    m = moe_model
+    E, H, I, T = m["E"], m["H"], m["I"], 8
+    x = O.synth_normal_bf16(1, 1.0, (T, H))
+    idx, w = route_table(O, T)
+    xq, xsa = gpu.norm_quant(dev(x), dev(np.full(H, ONE, np.uint16)), 128)
+    eo, routes, bucket, bi8, bsa, accum, out = gpu_moe(gpu, xq, xsa, idx, w, m["Wgu"], m["Wd"], E, H, I)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    rb = O.moe_phase1(host(xq), host(xsa), reo, rroutes, m["gp"], m["gs"], m["gcs"], I)
+    np.testing.assert_array_equal(host(bucket), rb)
+    rbq, rbsa = O.block_quant(rb, 64, True)
+    np.testing.assert_array_equal(host(bi8), rbq)
+    np.testing.assert_array_equal(host(bsa), rbsa)
+    racc, rout = O.moe_phase2(rbq, rbsa, reo, rroutes, T, m["dp"], m["ds"], m["dcs"], H)
+    np.testing.assert_array_equal(host(accum), racc)
+    np.testing.assert_array_equal(host(out), rout)
+    tol_check(host(accum), racc)
+
+
+def test_moe_prefill_sampled(gpu, O, moe_model):
+    """T = 2048 at model shape: exact schedule; phase 1 checked against the
+    oracle on every route of the least-loaded expert; phase 2 on every route
+    of 3 tokens."""
+    m = moe_model
+    E, H, I, T = m["E"], m["H"], m["I"], 2048
+    x = O.synth_normal_bf16(1, 1.0, (T, H))
+    idx, w = route_table(O, T)
+    xq, xsa = gpu.norm_quant(dev(x), dev(np.full(H, ONE, np.uint16)), 128)
+    eo, routes, bucket, bi8, bsa, accum, out = gpu_moe(gpu, xq, xsa, idx, w, m["Wgu"], m["Wd"], E, H, I)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    np.testing.assert_array_equal(host(eo), reo)
+    counts = np.diff(reo)
+    assert counts.min() != counts.max()  # uneven histogram exercised
+    hb = host(bucket)
+    e = int(np.argmin(counts))
+    lo, hi = reo[e], reo[e + 1]
+    sub_eo = np.zeros(E + 1, np.int32)
+    sub_eo[e + 1:] = hi - lo
+    rb = O.moe_phase1(host(xq), host(xsa), sub_eo, rroutes[lo:hi], m["gp"], m["gs"], m["gcs"], I)
+    np.testing.assert_array_equal(hb[lo:hi], rb)
+    hbi8, hbsa = host(bi8), host(bsa)
+    toks = [0, 1000, 2047]
+    keep = np.isin(rroutes["token"], toks)
+    recs = np.nonzero(keep)[0]
+    sub_eo = np.concatenate([[0], np.cumsum([keep[reo[k]:reo[k + 1]].sum() for k in range(E)])]).astype(np.int32)
+    sub_routes = rroutes[recs].copy()
+    remap = {t: i for i, t in enumerate(toks)}
+    sub_routes["token"] = [remap[t] for t in sub_routes["token"]]
+    racc, rout = O.moe_phase2(hbi8[recs], hbsa[recs], sub_eo, sub_routes, len(toks), m["dp"],
+                              m["ds"], m["dcs"], H)
+    np.testing.assert_array_equal(host(accum)[toks], racc)
+    np.testing.assert_array_equal(host(out)[toks], rout)

@@ -1,0 +1,335 @@
+"""Pins of the CPU oracle (oracle/bq_oracle.c) against what mathematics or an
+independent library fixes, so that a dropped term, a wrong sign or index, or a
+transposed operand in the restatement fails here.  The reference ships no
+golden vectors for this path (its tests never call the butterquant GEMMs), so
+these pins plus the committed fixtures in tests/golden/ are the parity anchor.
+
+Pin map (oracle function -> pins):
+  fwht_block/row      unit-vector KAT (exact Sylvester signs x c_B), f64 matrix
+                      closed form, involution, Parseval, scale-constant KATs
+  quant_segment       tie-to-even KATs, zero segment, amax -> +-127
+  f32_to_bf16         torch's independent RNE conversion
+  rms_reduce_row      f64 sum of squares
+  prepare_norm_act.   f64 pipeline (codes within 1, scale rel 1e-5)
+  prepare_block_act.  f64 pipeline
+  pack_and_colsum     hand-derived byte positions, bijection, int64 row sums
+  gemm per-row/block  int64 brute force + f64 epilogue closed forms; VNNI
+                      (u8, colsum) form == signed form
+  exp/tanh/gelu fast  numpy exp/tanh/exact GELU within the stated error
+  route top-k/softmax numpy stable argsort; weights sum to 1
+  build_schedule      python stable sort of (expert, token, k)
+  moe phase1/phase2   f64 closed forms over the unpacked weights
+"""
+import math
+
+import numpy as np
+import pytest
+
+BLOCKS = [16, 32, 64, 128, 256, 512]
+
+
+def hadamard(b):
+    i = np.arange(b)
+    pc = np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    return np.where(pc % 2 == 0, 1.0, -1.0)
+
+
+@pytest.mark.parametrize("B", BLOCKS)
+def test_fwht_unit_vector_kat(O, B):
+    c = np.float32(O.fwht_scale(B))
+    H = hadamard(B)
+    for j in [0, 1, B // 2 - 1, B - 1, 5 % B]:
+        e = np.zeros((1, B), np.float32)
+        e[0, j] = 1.0
+        y = O.fwht_rows(e, B)[0]
+        np.testing.assert_array_equal(y, (H[:, j] * c).astype(np.float32))
+
+
+def test_fwht_scale_constants(O):
+    assert O.fwht_scale(16) == 0.25
+    assert O.fwht_scale(64) == 0.125
+    assert O.fwht_scale(256) == 0.0625
+    for b in (32, 128, 512):
+        assert O.fwht_scale(b) == float(np.float32(1.0 / float(np.sqrt(np.float32(b)))))
+
+
+@pytest.mark.parametrize("B", BLOCKS)
+def test_fwht_closed_form_involution_parseval(O, B):
+    rng = np.random.default_rng(B)
+    x = rng.standard_normal((3, 2 * B)).astype(np.float32)
+    y = O.fwht_rows(x, B)
+    H = hadamard(B) / math.sqrt(B)
+    ref = np.concatenate([x[:, :B] @ H.T, x[:, B:] @ H.T], axis=1)
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max() * math.log2(B)
+    z = O.fwht_rows(y, B)
+    assert np.abs(z - x).max() <= 1e-5 * np.abs(x).max() * math.log2(B)
+    np.testing.assert_allclose(np.linalg.norm(y[:, :B], axis=1),
+                               np.linalg.norm(x[:, :B], axis=1), rtol=1e-5)
+
+
+def test_fwht_rejects_bad_block(O):
+    with pytest.raises(ValueError):
+        O.fwht_rows(np.zeros((1, 48), np.float32), 48)
+    with pytest.raises(ValueError):
+        O.fwht_rows(np.zeros((1, 96), np.float32), 64)
+
+
+def test_quant_kats(O):
+    q, s = O.quant_segment(np.array([127, 2.5, 3.5, -2.5, -0.5, 0.5, 1.5], np.float32), False)
+    np.testing.assert_array_equal(q, [127, 2, 4, -2, 0, 0, 2])
+    assert s == 127.0
+    q, s = O.quant_segment(np.zeros(64, np.float32), True)
+    assert (q == 0).all() and s == 0.0
+    x = np.array([0.5, -2.0, 1.0, 0.25], np.float32)
+    q, s = O.quant_segment(x, True)
+    assert s == np.float32(2.0) / np.float32(127.0)
+    np.testing.assert_array_equal(q, [32, -127, 64, 16])  # 31.75 -> 32, 63.5 -> 64 (even)
+
+
+def test_quant_random_matches_numpy(O):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(1000).astype(np.float32)
+    q, s = O.quant_segment(x, False)
+    amax = np.abs(x).max()
+    inv = np.float32(127.0) / amax
+    ref = np.clip(np.rint(x * inv), -128, 127).astype(np.int8)
+    np.testing.assert_array_equal(q, ref)
+    assert s == amax and np.abs(q).max() == 127
+
+
+def test_bf16_rne_matches_torch(O):
+    import torch
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 10.0 ** rng.integers(-8, 8, 4096),
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 0.0, -0.0,
+                                  3.0e38, 1e-40], np.float32)]).astype(np.float32)
+    mine = O.f32_to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(mine, ref)
+    c = np.array([O.lib().bqo_f32_to_bf16(float(v)) for v in x[:256]], np.uint16)
+    np.testing.assert_array_equal(c, mine[:256])
+
+
+@pytest.mark.parametrize("H", [2816, 4096, 2112, 128])
+def test_rms_reduce_row_f64(O, H):
+    x = O.synth_normal_bf16(3, 1.0, (H,))
+    ss = O.rms_reduce_row(x)
+    ref = float(np.sum(O.bf16_to_f32(x).astype(np.float64) ** 2))
+    assert abs(ss - ref) <= 1e-5 * ref
+
+
+@pytest.mark.parametrize("H,B", [(2816, 128), (4096, 128), (512, 64)])
+def test_norm_quant_f64_pipeline(O, H, B):
+    x = O.synth_normal_bf16(11, 1.0, (4, H))
+    g = O.f32_to_bf16(np.linspace(0.5, 1.5, H).astype(np.float32))
+    q, sa = O.norm_quant(x, g, B)
+    sqrt_n, n_eps = O.norm_consts(H)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    inv = sqrt_n / np.sqrt((xf ** 2).sum(1, keepdims=True) + n_eps)
+    w = xf * inv * O.bf16_to_f32(g)
+    Hm = hadamard(B) / math.sqrt(B)
+    w = (w.reshape(4, H // B, B) @ Hm.T).reshape(4, H)
+    amax = np.abs(w).max(1)
+    np.testing.assert_allclose(sa, amax, rtol=1e-5)
+    ref = np.clip(np.rint(w * 127.0 / amax[:, None]), -128, 127)
+    d = np.abs(q.astype(np.int64) - ref)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+
+
+def test_block_quant_f64_pipeline(O):
+    x = O.synth_normal_bf16(12, 1.0, (5, 704))
+    q, sa = O.block_quant(x, 64, True)
+    xf = O.bf16_to_f32(x).astype(np.float64).reshape(5, 11, 64) @ (hadamard(64) / 8.0).T
+    amax = np.abs(xf).max(2)
+    np.testing.assert_allclose(sa, amax, rtol=1e-5)
+    ref = np.clip(np.rint(xf * 127.0 / amax[:, :, None]), -128, 127).reshape(5, 704)
+    d = np.abs(q.astype(np.int64) - ref)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    # o_proj path: block = head_dim, no runtime FWHT (gemma_4_moe_bq.mojo:515-517)
+    x2 = O.synth_normal_bf16(13, 1.0, (3, 1024))
+    q2, sa2 = O.block_quant(x2, 256, False)
+    x2f = O.bf16_to_f32(x2).astype(np.float64).reshape(3, 4, 256)
+    np.testing.assert_array_equal(sa2, np.abs(x2f).max(2).astype(np.float32))
+    ref2 = np.clip(np.rint(x2f * 127.0 / np.abs(x2f).max(2, keepdims=True)), -128, 127)
+    assert np.abs(q2.astype(np.int64) - ref2.reshape(3, 1024)).max() <= 1
+    with pytest.raises(ValueError):
+        O.block_quant(x, 256, False)  # 704 is not a multiple of 256
+    with pytest.raises(ValueError):
+        O.block_quant(x, 48, True)
+
+
+def test_pack_positions_and_bijection(O):
+    rows, cols = 64, 128
+    w = (np.arange(rows * cols) % 251 - 125).astype(np.int8).reshape(rows, cols)
+    p, cs = O.pack_and_colsum(w)
+    # a 32x64 tile is two 16-row halves; each half is the 16x16 dword transpose
+    np.testing.assert_array_equal(p[0:4], w[0, 0:4])
+    np.testing.assert_array_equal(p[4:8], w[1, 0:4])
+    np.testing.assert_array_equal(p[60:64], w[15, 0:4])
+    np.testing.assert_array_equal(p[64:68], w[0, 4:8])
+    np.testing.assert_array_equal(p[1024:1028], w[16, 0:4])
+    np.testing.assert_array_equal(p[2048:2052], w[0, 64:68])
+    np.testing.assert_array_equal(p[32 * cols:32 * cols + 4], w[32, 0:4])
+    off = O.vnni_offsets(rows, cols)
+    assert np.unique(off).size == rows * cols and off.max() == rows * cols - 1
+    np.testing.assert_array_equal(p[off], w)
+    np.testing.assert_array_equal(cs, w.astype(np.int64).sum(1).astype(np.float32))
+    p2, cs2 = O.pack_and_colsum(w, 64, False)
+    np.testing.assert_array_equal(cs2.reshape(2, rows),
+                                  w.astype(np.int64).reshape(rows, 2, 64).sum(2).T)
+    with pytest.raises(ValueError):
+        O.pack_and_colsum(w[:48])
+
+
+def _quantized_linear(O, N, K, B, seed=0):
+    wf = O.bf16_to_f32(O.synth_normal_bf16(seed, 0.02, (N, K)))
+    q, s = O.rotate_and_quant(wf, B)
+    return q, s
+
+
+def test_rotate_and_quant_f64(O):
+    wf = O.bf16_to_f32(O.synth_normal_bf16(0, 0.02, (32, 256)))
+    q, s = O.rotate_and_quant(wf, 128)
+    rot = (wf.astype(np.float64).reshape(32, 2, 128) @ (hadamard(128) / math.sqrt(128)).T).reshape(32, 256)
+    np.testing.assert_allclose(s, np.abs(rot).max(1) / 127.0, rtol=1e-5)
+    d = np.abs(q - np.clip(np.rint(rot / (np.abs(rot).max(1, keepdims=True) / 127.0)), -128, 127))
+    assert d.max() <= 1
+    qb, sb = O.rotate_and_quant(wf, 64, per_block=True)
+    assert sb.shape == (32, 4)
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_linear_closed_form(O, M):
+    N, K = 64, 256
+    q, s = _quantized_linear(O, N, K, 128)
+    p, cs = O.pack_and_colsum(q)
+    x = O.synth_normal_bf16(1, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, 0x3F80, np.uint16))
+    ob, of = O.linear(xq, sa, p, s, cs, N)
+    acc = xq.astype(np.int64) @ q.astype(np.int64).T
+    np.testing.assert_array_equal(O.int_acc(xq, p, N), acc)
+    ref = acc * (sa[:, None].astype(np.float64) / 127.0) * s[None, :]
+    assert np.abs(of - ref).max() <= 4e-7 * np.abs(ref).max()
+    np.testing.assert_array_equal(ob, O.f32_to_bf16(of))
+    # VNNI u8 form == signed form whenever |sum (x+128) w| < 2^24
+    u8 = (xq.astype(np.int64) + 128) @ q.astype(np.int64).T
+    assert np.abs(u8).max() < 2 ** 24
+    sb, sf = O.signed_linear(xq, sa, p, s, N)
+    np.testing.assert_array_equal(sf, of)
+
+
+@pytest.mark.parametrize("B", [64, 256])
+def test_block_linear_closed_form(O, B):
+    N, K, M = 32, 512, 3
+    q, s = _quantized_linear(O, N, K, B)
+    p, cs = O.pack_and_colsum(q, B, False)
+    x = O.synth_normal_bf16(2, 1.0, (M, K))
+    xq, sa = O.block_quant(x, B, True)
+    ob, of = O.block_linear(xq, sa, p, s, cs, N, B)
+    nb = K // B
+    acc = np.einsum("mbk,nbk->mnb", xq.astype(np.int64).reshape(M, nb, B),
+                    q.astype(np.int64).reshape(N, nb, B))
+    ref = (acc * (sa[:, None, :].astype(np.float64) / 127.0)).sum(2) * s[None, :]
+    assert np.abs(of - ref).max() <= 1e-6 * np.abs(ref).max()
+    sb, sf = O.signed_block_linear(xq, sa, p, s, N, B)
+    np.testing.assert_array_equal(sf, of)
+
+
+def test_fast_math_bounds(O):
+    x = np.linspace(-87, 0, 20001).astype(np.float32)
+    e = O.exp_fast(x)
+    rel = np.abs(e.astype(np.float64) / np.exp(x.astype(np.float64)) - 1)
+    assert rel.max() < 4e-3
+    lib = O.lib()
+    xs = np.linspace(-12, 12, 4801).astype(np.float32)
+    t = np.array([lib.bqo_tanh_f32(float(v)) for v in xs])
+    assert np.abs(t - np.tanh(xs.astype(np.float64))).max() < 4e-3
+    assert lib.bqo_tanh_f32(-1.0) < 0 < lib.bqo_tanh_f32(1.0)
+    g = O.gelu_tanh(xs)
+    xd = xs.astype(np.float64)
+    exact = 0.5 * xd * (1 + np.tanh(math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    assert (np.abs(g - exact) <= 4e-3 * np.abs(xd) + 1e-6).all()
+    # the softmax exp is used on top-8 logit differences; away from f32
+    # underflow (x > -60) it is within 1% of exp
+    xs2 = np.linspace(-60, 0, 3001).astype(np.float32)
+    sb = np.array([lib.bqo_fast_exp_softmax_biased(float(v)) for v in xs2])
+    assert (np.abs(sb / np.exp(xs2.astype(np.float64)) - 1) < 1e-2).all()
+
+
+def test_route_topk_softmax(O):
+    logits = O.synth_normal_f32(2, 1.0, (64, 128))
+    logits[0, 5] = logits[0, 9] = 10.0  # tie -> lower expert first
+    idx, w = O.route_topk_softmax(logits, 8)
+    ref = np.argsort(-logits, axis=1, kind="stable")[:, :8]
+    np.testing.assert_array_equal(idx, ref)
+    assert idx[0, 0] == 5 and idx[0, 1] == 9
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=2e-6)
+    assert (np.diff(w, axis=1) <= 1e-7).all()
+
+
+def test_build_schedule_vs_sort(O):
+    rng = np.random.default_rng(4)
+    T, k, E = 37, 4, 16
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    eo, routes = O.build_schedule(idx, w, E)
+    order = sorted(((int(idx[t, j]), t, j) for t in range(T) for j in range(k)))
+    np.testing.assert_array_equal(routes["token"], [t for _, t, _ in order])
+    np.testing.assert_array_equal(routes["weight"], [w[t, j] for _, t, j in order])
+    counts = np.bincount(idx.ravel(), minlength=E)
+    np.testing.assert_array_equal(eo, np.concatenate([[0], np.cumsum(counts)]))
+
+
+def _moe_case(O, T=6, E=4, k=2, H=128, I=64, seed=5):
+    rng = np.random.default_rng(seed)
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    eo, routes = O.build_schedule(idx, w, E)
+    gu = O.bf16_to_f32(O.synth_normal_bf16(0, 0.02, (E * 2 * I, H)))
+    gq, gs = O.rotate_and_quant(gu, 128 if H % 128 == 0 else 64)
+    gp, gcs = O.pack_and_colsum(gq)
+    dn = O.bf16_to_f32(O.synth_normal_bf16(9, 0.02, (E * H, I)))
+    dq, ds = O.rotate_and_quant(dn, 64)
+    dp, dcs = O.pack_and_colsum(dq, 64, False)
+    x = O.synth_normal_bf16(1, 1.0, (T, H))
+    xq, xsa = O.norm_quant(x, np.full(H, 0x3F80, np.uint16), 64)
+    return dict(idx=idx, w=w, eo=eo, routes=routes, gq=gq, gs=gs, gp=gp, gcs=gcs, dq=dq, ds=ds,
+                dp=dp, dcs=dcs, xq=xq, xsa=xsa, T=T, E=E, k=k, H=H, I=I)
+
+
+def test_moe_phases_closed_form(O):
+    c = _moe_case(O)
+    T, E, H, I = c["T"], c["E"], c["H"], c["I"]
+    bucket = O.moe_phase1(c["xq"], c["xsa"], c["eo"], c["routes"], c["gp"], c["gs"], c["gcs"], I)
+    gq = c["gq"].astype(np.int64).reshape(E, 2 * I, H)
+    ref = np.zeros((len(c["routes"]), I))
+    for e in range(E):
+        for rec in range(c["eo"][e], c["eo"][e + 1]):
+            t = c["routes"]["token"][rec]
+            a = gq[e] @ c["xq"][t].astype(np.int64)
+            v = a * (c["xsa"][t] / 127.0) * c["gs"][e * 2 * I:(e + 1) * 2 * I]
+            g, u = v[:I], v[I:]
+            ref[rec] = 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3))) * u
+    got = O.bf16_to_f32(bucket).astype(np.float64)
+    assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+    bq_, bsa = O.block_quant(bucket, 64, True)
+    accum, out = O.moe_phase2(bq_, bsa, c["eo"], c["routes"], T, c["dp"], c["ds"], c["dcs"], H)
+    dq = c["dq"].astype(np.int64).reshape(E, H, I)
+    ref2 = np.zeros((T, H))
+    for e in range(E):
+        for rec in range(c["eo"][e], c["eo"][e + 1]):
+            t = c["routes"]["token"][rec]
+            acc = np.einsum("nbk,bk->nb", dq[e].reshape(H, I // 64, 64),
+                            bq_[rec].astype(np.int64).reshape(I // 64, 64))
+            y = (acc * (bsa[rec] / 127.0)).sum(1) * c["ds"][e * H:(e + 1) * H]
+            ref2[t] += y * c["routes"]["weight"][rec]
+    assert np.abs(accum - ref2).max() <= 1e-5 * np.abs(ref2).max()
+    np.testing.assert_array_equal(out, O.f32_to_bf16(accum))
+
+
+def test_synth_normal(O):
+    x = O.synth_normal_f32(0, 0.02, (200000,))
+    assert abs(x.mean()) < 2e-4 and abs(x.std() - 0.02) < 2e-4
+    b = O.synth_normal_bf16(0, 0.02, (1001,))
+    np.testing.assert_array_equal(b, O.f32_to_bf16(O.synth_normal_f32(0, 0.02, (1001,))))
