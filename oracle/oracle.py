@@ -84,9 +84,10 @@ ROUTE_DTYPE = np.dtype([("token", np.int32), ("weight", np.float32)])
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     """butterquant/convert.mojo:14-17 software RNE, vectorised in numpy
     (pinned against the C restatement in tests)."""
-    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    rne = (b + ((b >> 16) & 1) + 0x7FFF) & 0xFFFFFFFF
-    return (rne >> 16).astype(np.uint16)
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rne = b + ((b >> np.uint32(16)) & np.uint32(1))  # uint32 wraps like the reference's
+    rne += np.uint32(0x7FFF)
+    return (rne >> np.uint32(16)).astype(np.uint16)
 
 
 def bf16_to_f32(b: np.ndarray) -> np.ndarray:
