@@ -1,0 +1,405 @@
+"""Benchmark of the butterquant hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|...]
+
+Prints ONE JSON line.  Primary metric (value): decode GEMV HBM GB/s -- one
+step is one per-row quantized GEMV (M=1 token, K=N=4096, weights rotated over
+64 replicas = 1 GiB so every launch streams from HBM, not the 256 MB
+Infinity Cache).  The same line carries the other headline numbers of the
+metric: MoE-layer tokens/s at 32 and 2048 tokens, the prefill GEMM (M=512)
+TOP/s and MFMA fraction, and the batch-16 decoder-layer time.
+
+Kernel launches of each workload are captured once into a HIP graph
+(torch.cuda.CUDAGraph records libbq's launches on its capture stream) and
+replayed, so host launch overhead does not stretch the timed region.
+Timing uses HIP events on the stream the kernels run on, bracketed by
+device synchronizations.  Data: synthetic, bf16 N(0, 0.02) weights (seed 0)
+quantized by libbq's own encoder, bf16 N(0,1) activations (seed 1),
+N(0,1) router logits (seed 2).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mojo-gemma4-cpu_amd"))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, published (no sparsity)
+BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, published
+H, I, E, TOPK = 2816, 704, 128, 8   # Gemma-4-26B-A4B (modeling/gemma4_common.mojo)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (PMC calibration kernel)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+def graph_of(fn, n):
+    """Capture n calls fn(i) into one graph (after one eager warm call each)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, per_replay, steps, warmup):
+    """Replay graph g until >= steps calls were timed; -> (ms per call, wall s)."""
+    import torch
+    reps = max(1, -(-steps // per_replay))
+    wreps = max(1, -(-warmup // per_replay))
+    for _ in range(wreps):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / (reps * per_replay), wall, reps * per_replay
+
+
+def quantized(bq, torch, n, k, block, gen):
+    w = (torch.randn(n, k, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    codes, scales = bq.quantize_weight(w, block)
+    tiled = bq.retile(codes.view(-1), n, k)
+    return codes, scales, bq.ButterquantWeight(tiled, scales, n, k)
+
+
+# ---------------------------------------------------------------------------
+def bench_gemv(bq, torch, steps, warmup, reps=64):
+    N = K = 4096
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    codes, scales, W0 = quantized(bq, torch, N, K, 128, gen)
+    replicas = [W0] + [bq.ButterquantWeight(W0.data.clone(), scales.clone(), N, K)
+                       for _ in range(reps - 1)]
+    xg = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(1, K, generator=xg, device="cuda").to(torch.bfloat16)
+    gamma = torch.ones(K, dtype=torch.bfloat16, device="cuda")
+    xq, sa = bq.norm_quant(x, gamma, 128)
+    out = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    g = graph_of(lambda i: bq.linear(xq, sa, replicas[i], out=out), reps)
+    ms, wall, n = time_graph(g, reps, steps, warmup)
+    alg_bytes = N * K + N * 4 + K + 4 + N * 2       # W + sw + x_i8 + sa + y
+    # activation prep (norm-quant: RMS, FWHT128, int8) and the full decode linear
+    gq = graph_of(lambda i: bq.norm_quant(x, gamma, 128, out=(xq, sa)), 64)
+    ms_nq, _, _ = time_graph(gq, 64, 256, 64)
+    gl = graph_of(lambda i: (bq.norm_quant(x, gamma, 128, out=(xq, sa)),
+                             bq.linear(xq, sa, replicas[i], out=out)), reps)
+    ms_lin, _, _ = time_graph(gl, reps, 256, 64)
+    return dict(ms=ms, wall=wall, calls=n, alg_bytes=alg_bytes,
+                gbs=alg_bytes / (ms * 1e-3) / 1e9, norm_quant_us=ms_nq * 1e3,
+                linear_with_prep_us=ms_lin * 1e3, codes=codes, scales=scales)
+
+
+def bench_prefill(bq, torch, steps, warmup, reps=32):
+    M, N, K = 512, 4096, 4096
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    _, scales, W0 = quantized(bq, torch, N, K, 128, gen)
+    replicas = [W0] + [bq.ButterquantWeight(W0.data.clone(), scales, N, K) for _ in range(reps - 1)]
+    xg = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(M, K, generator=xg, device="cuda").to(torch.bfloat16)
+    xq, sa = bq.norm_quant(x, torch.ones(K, dtype=torch.bfloat16, device="cuda"), 128)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    g = graph_of(lambda i: bq.linear(xq, sa, replicas[i], out=out), reps)
+    ms, wall, n = time_graph(g, reps, max(64, steps // 8), max(32, warmup // 4))
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tops=tops, int8_frac=tops / INT8_PEAK_TOPS, bf16_frac=tops / BF16_PEAK_TFLOPS,
+                alg_bytes=N * K + N * 4 + M * K + M * 4 + M * N * 2)
+
+
+class MoeLayer:
+    """One quantized MoE expert layer: norm-quant -> CSR schedule -> phase 1
+    (gate/up + GELU) -> FWHT64 block-quant -> phase 2 (down + route-weighted,
+    expert-ordered combine)."""
+
+    def __init__(self, bq, torch, T, Wgu, Wd, gen_seed=1):
+        self.bq, self.T = bq, T
+        xg = torch.Generator(device="cuda").manual_seed(gen_seed)
+        self.x = torch.randn(T, H, generator=xg, device="cuda").to(torch.bfloat16)
+        lg = torch.Generator(device="cuda").manual_seed(2)
+        logits = torch.randn(T, E, generator=lg, device="cuda")
+        top, idx = torch.topk(logits, TOPK, dim=1)
+        self.idx = idx.to(torch.int32).contiguous()
+        self.w = torch.softmax(top, dim=1).contiguous()
+        self.gamma = torch.ones(H, dtype=torch.bfloat16, device="cuda")
+        self.Wgu, self.Wd = Wgu, Wd
+        d = "cuda"
+        self.xq = torch.empty(T, H, dtype=torch.int8, device=d)
+        self.xsa = torch.empty(T, dtype=torch.float32, device=d)
+        self.eo = torch.empty(E + 1, dtype=torch.int32, device=d)
+        self.routes = torch.zeros(T * TOPK, 2, dtype=torch.int32, device=d)
+        self.bucket = torch.empty(T * TOPK, I, dtype=torch.bfloat16, device=d)
+        self.bi8 = torch.empty(T * TOPK, I, dtype=torch.int8, device=d)
+        self.bsa = torch.empty(T * TOPK, I // 64, dtype=torch.float32, device=d)
+        self.ws = torch.empty(max(bq.moe_phase2_workspace_size(T, TOPK, H), 256),
+                              dtype=torch.uint8, device=d)
+        self.accum = torch.empty(T, H, dtype=torch.float32, device=d)
+        self.out = torch.empty(T, H, dtype=torch.bfloat16, device=d)
+
+    def __call__(self, _i=0):
+        bq, T = self.bq, self.T
+        bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
+        bq.build_schedule(self.idx, self.w, E, out=(self.eo, self.routes))
+        bq.moe_phase1(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I, out=self.bucket)
+        bq.block_quant(self.bucket, 64, True, out=(self.bi8, self.bsa))
+        bq.moe_phase2(self.bi8, self.bsa, self.eo, self.routes, self.Wd, E, T, TOPK, H,
+                      workspace=self.ws, out=(self.accum, self.out))
+
+
+def moe_weights(bq, torch):
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    _, _, Wgu = quantized(bq, torch, E * 2 * I, H, 128, gen)
+    _, _, Wd = quantized(bq, torch, E * H, I, 64, gen)
+    return Wgu, Wd
+
+
+def bench_moe(bq, torch, T, weights, steps):
+    """weights: list of (Wgu, Wd) replicas; consecutive steps alternate
+    between them so each step's ~0.7 GB of experts is not resident in the
+    256 MB Infinity Cache from the previous step."""
+    layers = [MoeLayer(bq, torch, T, Wgu, Wd) for Wgu, Wd in weights]
+    g = graph_of(lambda i: layers[i](), len(layers))
+    ms, wall, n = time_graph(g, len(layers), steps, max(3, steps // 8))
+    layer = layers[0]
+    eo = layer.eo.cpu().numpy()
+    touched = int((eo[1:] - eo[:-1] > 0).sum())
+    per_expert = 2 * I * H + 2 * I * 4 + H * I + H * 4
+    wbytes = touched * per_expert
+    return dict(T=T, ms=ms, tokens_per_s=T / (ms * 1e-3), experts_touched=touched,
+                weight_bytes=wbytes, hbm_gbs_weights=wbytes / (ms * 1e-3) / 1e9,
+                ops=2.0 * T * TOPK * (2 * I * H + H * I))
+
+
+def bench_layer16(bq, torch, Wgu, Wd, steps):
+    """All quantized projections of one decoder layer at decode batch 16:
+    sliding (q/k/v 4096/2048/2048, o B=256) and full (q 8192, k 1024, o
+    B=512) attention projections, dense MLP (gate/up 2112, down B=64) and the
+    128-expert MoE, each with its activation prep."""
+    T = 16
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    d = "cuda"
+    mk = lambda n, k, b: quantized(bq, torch, n, k, b, gen)[2]
+    sq, sk, sv, so = mk(4096, H, 128), mk(2048, H, 128), mk(2048, H, 128), mk(H, 4096, 256)
+    fq, fk, fo = mk(8192, H, 128), mk(1024, H, 128), mk(H, 8192, 512)
+    dg, du, dd = mk(2112, H, 128), mk(2112, H, 128), mk(H, 2112, 64)
+    xg = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(T, H, generator=xg, device=d).to(torch.bfloat16)
+    gamma = torch.ones(H, dtype=torch.bfloat16, device=d)
+    e = lambda *shape, dt=torch.bfloat16: torch.empty(*shape, dtype=dt, device=d)
+    xq, xsa = e(T, H, dt=torch.int8), e(T, dt=torch.float32)
+    # attention outputs feeding o_proj (the attention itself is not a bq op)
+    attn_s = torch.randn(T, 4096, generator=xg, device=d).to(torch.bfloat16)
+    attn_f = torch.randn(T, 8192, generator=xg, device=d).to(torch.bfloat16)
+    oq_s, osa_s = e(T, 4096, dt=torch.int8), e(T, 16, dt=torch.float32)
+    oq_f, osa_f = e(T, 8192, dt=torch.int8), e(T, 16, dt=torch.float32)
+    q_s, k_s, v_s = e(T, 4096), e(T, 2048), e(T, 2048)
+    q_f, k_f = e(T, 8192), e(T, 1024)
+    o = e(T, H)
+    gt, up = e(T, 2112), e(T, 2112)
+    gq_, gsa = e(T, 2112, dt=torch.int8), e(T, 2112 // 64, dt=torch.float32)
+    moe = MoeLayer(bq, torch, T, Wgu, Wd)
+
+    def dense_mlp():
+        bq.norm_quant(x, gamma, 128, out=(xq, xsa))
+        bq.linear(xq, xsa, dg, out=gt)
+        bq.linear(xq, xsa, du, out=up)
+        bq.block_quant(gt, 64, True, out=(gq_, gsa))   # GELU(gate)*up is elementwise (not a bq op)
+        bq.block_linear(gq_, gsa, dd, 64, out=o)
+
+    def sliding(_i=0):
+        bq.norm_quant(x, gamma, 128, out=(xq, xsa))
+        bq.qkv(xq, xsa, sq, sk, sv, outs=(q_s, k_s, v_s))
+        bq.block_quant(attn_s, 256, False, out=(oq_s, osa_s))
+        bq.block_linear(oq_s, osa_s, so, 256, out=o)
+        dense_mlp()
+        moe()
+
+    def full(_i=0):
+        bq.norm_quant(x, gamma, 128, out=(xq, xsa))
+        bq.linear(xq, xsa, fq, out=q_f)
+        bq.linear(xq, xsa, fk, out=k_f)               # k_eq_v: one projection for K and V
+        bq.block_quant(attn_f, 512, False, out=(oq_f, osa_f))
+        bq.block_linear(oq_f, osa_f, fo, 512, out=o)
+        dense_mlp()
+        moe()
+
+    gs_ = graph_of(sliding, 1)
+    ms_s, _, _ = time_graph(gs_, 1, steps, max(3, steps // 8))
+    gf_ = graph_of(full, 1)
+    ms_f, _, _ = time_graph(gf_, 1, steps, max(3, steps // 8))
+    gm_ = graph_of(moe, 1)
+    ms_m, _, _ = time_graph(gm_, 1, steps, max(3, steps // 8))
+    stack_ms = 25 * ms_s + 5 * ms_f
+    return dict(sliding_layer_ms=ms_s, full_layer_ms=ms_f, moe_ms=ms_m,
+                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3))
+
+
+# ---------------------------------------------------------------------------
+def cpu_baseline_gemv(codes, scales, seconds):
+    """The reference CPU path (VNNI u8 x i8, 32-row tiles over worker_range),
+    ported to C in oracle/cpu_baseline.c, on the host cores: the same decode
+    GEMV (M=1, K=N=4096), bounded to ~`seconds` of CPU work."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    lib = O.cpu()
+    q = codes.cpu().numpy()
+    s = scales.cpu().numpy().astype(np.float32)
+    N, K = q.shape
+    p, cs = O.pack_and_colsum(q)
+    xq = np.random.default_rng(1).integers(-127, 128, (1, K), dtype=np.int8)
+    sa = np.ones(1, np.float32)
+    out = np.empty((1, N), np.uint16)
+    nthreads = max(1, min(16, os.cpu_count() or 1))
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+
+    def call():
+        lib.bqcpu_linear(ptr(xq), ptr(sa), 1, ptr(p), ptr(s), ptr(cs), N, K, ptr(out), nthreads)
+
+    for _ in range(30):
+        call()
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(ts) < 600:
+        t0 = time.perf_counter()
+        call()
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    alg_bytes = N * K + N * 4 + K + 4 + N * 2
+    return dict(value=alg_bytes / med / 1e9, unit="GB/s", cores=nthreads, kind="port",
+                sample=f"decode GEMV M=1 K=N=4096, {len(ts)} calls after 30 warmups, median "
+                       f"{med * 1e6:.1f} us; ISA {lib.bqcpu_isa().decode()}")
+
+
+def calib_copy(torch):
+    """A plain device copy of 256 MiB (the PMC calibration kernel)."""
+    a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not built)"}))
+        sys.exit(2)
+    import torch
+    import bq
+    bq.init(0)
+    wl = args.workload
+    res = {}
+    if wl in ("all", "gemv"):
+        res["gemv"] = bench_gemv(bq, torch, args.steps, args.warmup)
+    if wl in ("all", "prefill"):
+        res["prefill"] = bench_prefill(bq, torch, args.steps, args.warmup)
+    if wl in ("all", "moe32", "moe2048", "layer16"):
+        Wgu, Wd = moe_weights(bq, torch)
+        reps = [(Wgu, Wd), tuple(bq.ButterquantWeight(w.data.clone(), w.scale, w.n_rows, w.k)
+                                 for w in (Wgu, Wd))]
+        if wl in ("all", "moe32"):
+            res["moe32"] = bench_moe(bq, torch, 32, reps, max(20, args.steps // 16))
+        if wl in ("all", "moe2048"):
+            res["moe2048"] = bench_moe(bq, torch, 2048, reps, max(10, args.steps // 32))
+        if wl in ("all", "layer16"):
+            res["layer16"] = bench_layer16(bq, torch, Wgu, Wd, max(10, args.steps // 32))
+    if args.calib_copy:
+        calib_copy(torch)
+
+    line = {
+        "metric": "bq GEMV HBM GB/s (% peak); MoE-layer tokens/s at 32 and 2048 tokens",
+        "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+    }
+    if "gemv" in res:
+        gv = res["gemv"]
+        line.update(value=round(gv["gbs"], 1), steps=gv["calls"], warmup=args.warmup,
+                    ms_per_step=gv["ms"],
+                    config={"workload": "decode GEMV: per-row butterquant linear, M=1 token, "
+                                        "K=4096, N=4096, int8 codes x int8 activation, "
+                                        "fp32 accumulate -> bf16; 64 weight replicas (1 GiB) "
+                                        "rotated", "global_batch": 1, "seq_len": 1,
+                            "parallelism": "single GPU"},
+                    pct_hbm_peak=round(100 * gv["gbs"] / HBM_PEAK_GBS, 1),
+                    roofline={"bound": "hbm", "achieved": round(gv["gbs"], 1),
+                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(gv["gbs"] / HBM_PEAK_GBS, 4),
+                              "traffic": _traffic()})
+        line["gemv_detail"] = {"kernel_us": round(gv["ms"] * 1e3, 3),
+                               "alg_bytes_per_launch": gv["alg_bytes"],
+                               "norm_quant_us": round(gv["norm_quant_us"], 3),
+                               "linear_with_prep_us": round(gv["linear_with_prep_us"], 3)}
+    else:
+        line.update(value=None, steps=args.steps, warmup=args.warmup, ms_per_step=None,
+                    config={"workload": wl})
+    if "prefill" in res:
+        p = res["prefill"]
+        line["prefill_gemm_m512"] = {"us": round(p["ms"] * 1e3, 2), "tops": round(p["tops"], 1),
+                                     "int8_mfma_frac": round(p["int8_frac"], 4),
+                                     "bf16_mfma_frac": round(p["bf16_frac"], 4)}
+    for key in ("moe32", "moe2048"):
+        if key in res:
+            m = res[key]
+            line[f"moe_layer_T{m['T']}"] = {
+                "tokens_per_s": round(m["tokens_per_s"], 1), "ms": round(m["ms"], 4),
+                "experts_touched": m["experts_touched"],
+                "weight_GBs": round(m["hbm_gbs_weights"], 1),
+                "hbm_frac_weights": round(m["hbm_gbs_weights"] / HBM_PEAK_GBS, 4),
+                "int8_tops": round(m["ops"] / (m["ms"] * 1e-3) / 1e12, 1)}
+    if "layer16" in res:
+        line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()}
+    if "gemv" in res and not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_gemv(res["gemv"]["codes"], res["gemv"]["scales"],
+                                                 args.cpu_seconds)
+    print(json.dumps(line))
+
+
+def _traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the plain-copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_decode_k4096_n4096_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
+if __name__ == "__main__":
+    main()

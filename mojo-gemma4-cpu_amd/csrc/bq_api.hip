@@ -111,6 +111,7 @@ int bq_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, floa
   if (hidden <= 0 || hidden % 64 || hidden % block)
     return fail(BQ_ERR_SHAPE, "bq_norm_quant: hidden %d must be a multiple of 64 and of block %d", hidden, block);
   if (hidden > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "bq_norm_quant: hidden %d > %d", hidden, kMaxRowLds);
+  if (!a16(src)) return fail(BQ_ERR_INVALID, "bq_norm_quant: src must be 16-byte aligned");
   return check_hip(bq::launch_norm_quant(src, gamma, x_i8, x_sa, seq_len, hidden, block, sqrt_n,
                                          n_eps, S(stream)), "norm_quant");
 }
@@ -231,6 +232,7 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
   if (top_k <= 0 || top_k > 16) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: top_k %d not in [1,16]", top_k);
   if (!pow2(block) || block < 64 || inter % block || inter % 64 || hidden % 16 || hidden <= 0)
     return fail(BQ_ERR_SHAPE, "bq_moe_phase2_down: need block a power of two >= 64 dividing inter, hidden %% 16 == 0");
+  if (inter / block > 64) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: inter/block = %d > 64", inter / block);
   if (!a16(bucket_i8) || !a16(w_down))
     return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: int8 operands must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(workspace) % 256)

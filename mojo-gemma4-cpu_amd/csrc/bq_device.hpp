@@ -148,12 +148,54 @@ __device__ inline void fwht_wave(float (&v)[R], int block) {
   }
 }
 
+// Workgroup barrier for LDS producer/consumer hand-offs: waits for this
+// wave's LDS operations only.  (__syncthreads() also carries a release fence,
+// which on gfx9 waits for every outstanding global load -- it would drain the
+// global-load prefetch pipeline at each stage.)  Global loads land in private
+// registers and are waited for by the compiler at their use.
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // 16-byte global loads/stores
 __device__ inline v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ inline void st16(int8_t* p, v4i v) { *reinterpret_cast<v4i*>(p) = v; }
 
 __device__ inline v4i mfma16x16x64(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Map a global m-tile index (BM records per tile, tiles of consecutive
+// experts concatenated) to (expert, first record, end record).  Every lane of
+// the calling wave gets the same answer.
+__device__ inline bool find_mtile(const int32_t* __restrict__ eo, int E, int BM, int mt,
+                                  int max_routes, int& e, int& r0, int& r1) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int ex = base + lane;
+    int tiles = 0;
+    if (ex < E) tiles = (eo[ex + 1] - eo[ex] + BM - 1) / BM;
+    int inc = tiles;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += y;
+    }
+    const int excl = inc - tiles;
+    const bool hit = tiles > 0 && mt >= carry + excl && mt < carry + inc;
+    const unsigned long long m = __ballot(hit);
+    if (m) {
+      const int l = __ffsll((long long)m) - 1;
+      e = base + l;
+      const int local = mt - carry - __shfl(excl, l, kWave);
+      r0 = eo[e] + local * BM;
+      r1 = min(min(eo[e + 1], r0 + BM), max_routes);
+      return r0 < r1;
+    }
+    carry += __shfl(inc, 63, kWave);
+  }
+  return false;
 }
 
 }  // namespace bq

@@ -48,6 +48,17 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st);
 
 struct Route { int32_t token; float weight; };
 
+hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStream_t st);
+hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
+                                    const Route* routes, const int8_t* w_gu, const float* gu_scale,
+                                    uint16_t* bucket, int experts, int max_routes, int hidden,
+                                    int inter, int bm, hipStream_t st);
+hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const int32_t* eo,
+                                 const Route* routes, const int8_t* w_d, const float* d_scale,
+                                 float* y, int experts, int max_routes, int hidden, int inter,
+                                 int block, int bm, hipStream_t st);
+int moe_tile_bm(int max_routes, int experts);
+
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);

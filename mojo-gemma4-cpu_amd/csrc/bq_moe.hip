@@ -16,6 +16,8 @@
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
+#include <stdlib.h>
+
 namespace bq {
 
 constexpr int kMaxExperts = 256;
@@ -84,39 +86,6 @@ __global__ __launch_bounds__(1024) void k_build_schedule(
   }
 }
 
-// Map a global m-tile index (BM records per tile, tiles of consecutive
-// experts concatenated) to (expert, first record, end record).  Every lane of
-// the calling wave gets the same answer.
-__device__ inline bool find_mtile(const int32_t* __restrict__ eo, int E, int BM, int mt,
-                                  int max_routes, int& e, int& r0, int& r1) {
-  const int lane = lane_id();
-  int carry = 0;
-  for (int base = 0; base < E; base += 64) {
-    const int ex = base + lane;
-    int tiles = 0;
-    if (ex < E) tiles = (eo[ex + 1] - eo[ex] + BM - 1) / BM;
-    int inc = tiles;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += y;
-    }
-    const int excl = inc - tiles;
-    const bool hit = tiles > 0 && mt >= carry + excl && mt < carry + inc;
-    const unsigned long long m = __ballot(hit);
-    if (m) {
-      const int l = __ffsll((long long)m) - 1;
-      e = base + l;
-      const int local = mt - carry - __shfl(excl, l, kWave);
-      r0 = eo[e] + local * BM;
-      r1 = min(min(eo[e + 1], r0 + BM), max_routes);
-      return r0 < r1;
-    }
-    carry += __shfl(inc, 63, kWave);
-  }
-  return false;
-}
-
 // Phase 1, 16-record m-tiles: blockIdx.y = m-tile, blockIdx.x = group of 4
 // intermediate 16-column subtiles (one per wave).
 template <int U>
@@ -137,7 +106,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   const int8_t* wu = we + (size_t)((inter >> 4) + isub) * K64 * 1024 + lane * 16;
   const int arow = r0 + (lane & 15);
   const bool aval = arow < r1;
-  const int8_t* ab = x_i8 + (size_t)(aval ? routes[arow].token : 0) * K + (lane >> 4) * 16;
+  const int8_t* ab = x_i8 + (size_t)routes[aval ? arow : r0].token * K + (lane >> 4) * 16;
   const v4i zero = {0, 0, 0, 0};
   v4i cg = zero, cu = zero;
   int kt = 0;
@@ -149,7 +118,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
       bu[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)(kt + u) * 1024));
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) af[u] = aval ? ld16(ab + (kt + u) * 64) : zero;
+    for (int u = 0; u < U; ++u) af[u] = ld16(ab + (kt + u) * 64);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       cg = mfma16x16x64(af[u], bg[u], cg);
@@ -159,7 +128,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   for (; kt < K64; ++kt) {
     const v4i bgf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wg + (size_t)kt * 1024));
     const v4i buf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)kt * 1024));
-    const v4i af = aval ? ld16(ab + kt * 64) : zero;
+    const v4i af = ld16(ab + kt * 64);
     cg = mfma16x16x64(af, bgf, cg);
     cu = mfma16x16x64(af, buf, cu);
   }
@@ -195,7 +164,7 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
   const int8_t* wb = w_d + (size_t)e * hidden * K + (size_t)nsub * K64 * 1024 + lane * 16;
   const int arow = r0 + (lane & 15);
   const bool aval = arow < r1;
-  const int8_t* ab = b_i8 + (size_t)(aval ? arow : 0) * K + (lane >> 4) * 16;
+  const int8_t* ab = b_i8 + (size_t)(aval ? arow : r0) * K + (lane >> 4) * 16;
   const v4i zero = {0, 0, 0, 0};
   float facc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   int rec4[4];
@@ -208,7 +177,7 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
     for (int u = 0; u < U; ++u)
       if (kt0 + u < K64) {
         bf[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)(kt0 + u) * 1024));
-        af[u] = aval ? ld16(ab + (kt0 + u) * 64) : zero;
+        af[u] = ld16(ab + (kt0 + u) * 64);
       }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -251,6 +220,26 @@ __global__ void k_token_lists(const int32_t* __restrict__ eo, int E, const Route
   if (t < 0 || t >= T) return;
   const int p = atomicAdd(&tok_cnt[t], 1);
   if (p < cap) tok_recs[(size_t)t * cap + p] = r;
+}
+
+// Same lists built by one workgroup with LDS counters (seq_len <= 16384):
+// no separate clearing pass over global memory.
+__global__ __launch_bounds__(1024) void k_token_lists_lds(
+    const int32_t* __restrict__ eo, int E, const Route* __restrict__ routes,
+    int32_t* __restrict__ tok_cnt, int32_t* __restrict__ tok_recs, int cap, int T,
+    int max_routes) {
+  extern __shared__ int cnt[];
+  for (int t = threadIdx.x; t < T; t += blockDim.x) cnt[t] = 0;
+  __syncthreads();
+  const int n = min(eo[E], max_routes);
+  for (int r = threadIdx.x; r < n; r += blockDim.x) {
+    const int t = routes[r].token;
+    if (t < 0 || t >= T) continue;
+    const int p = atomicAdd(&cnt[t], 1);
+    if (p < cap) tok_recs[(size_t)t * cap + p] = r;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += blockDim.x) tok_cnt[t] = cnt[t];
 }
 
 // accum[t, n] = (((0 + y[r1,n]) + y[r2,n]) + ...) over t's records in
@@ -296,11 +285,26 @@ static inline int mtile_bound(int max_routes, int experts, int bm) {
   return (int)b;
 }
 
+// m-tile height for the grouped kernels from the mean routes per expert:
+// 16-row skinny tiles while experts see a handful of tokens (decode), LDS-
+// tiled 64/128-row tiles once each expert's weights can be reused.
+int moe_tile_bm(int max_routes, int experts) {
+  if (const char* s = getenv("BQ_MOE_BM")) return atoi(s);
+  const int per = max_routes / (experts > 0 ? experts : 1);
+  if (per >= 96) return 128;
+  if (per >= 24) return 64;
+  return 16;
+}
+
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
                              const Route* routes, const int8_t* w_gu, const float* gu_scale,
                              uint16_t* bucket, int experts, int max_routes, int hidden,
                              int inter, hipStream_t st) {
   if (max_routes <= 0) return hipSuccess;
+  const int bm = moe_tile_bm(max_routes, experts);
+  if (bm >= 64 && inter % 64 == 0)
+    return launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket, experts,
+                                    max_routes, hidden, inter, bm, st);
   dim3 g((inter / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
   hipLaunchKernelGGL(k_moe_gate_up_skinny<4>, g, b, 0, st, x_i8, x_sa, eo, routes, w_gu,
                      gu_scale, bucket, experts, hidden, inter, max_routes);
@@ -329,13 +333,25 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
   float* y = (float*)ws;
   int32_t* tok_cnt = (int32_t*)(ws + align256((size_t)max_routes * hidden * sizeof(float)));
   int32_t* tok_recs = (int32_t*)((char*)tok_cnt + align256((size_t)seq_len * sizeof(int32_t)));
-  hipLaunchKernelGGL(k_fill_i32, dim3((seq_len + 255) / 256), dim3(256), 0, st, tok_cnt, seq_len, 0);
-  if (max_routes > 0) {
-    dim3 g((hidden / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
-    hipLaunchKernelGGL(k_moe_down_skinny<4>, g, b, 0, st, bucket_i8, bucket_sa, eo, routes, w_down,
-                       down_scale, y, experts, hidden, inter, block, max_routes);
+  if (seq_len <= 16384) {
+    hipLaunchKernelGGL(k_token_lists_lds, dim3(1), dim3(1024), (size_t)seq_len * sizeof(int), st,
+                       eo, experts, routes, tok_cnt, tok_recs, cap, seq_len, max_routes);
+  } else {
+    hipLaunchKernelGGL(k_fill_i32, dim3((seq_len + 255) / 256), dim3(256), 0, st, tok_cnt, seq_len, 0);
     hipLaunchKernelGGL(k_token_lists, dim3((max_routes + 255) / 256), dim3(256), 0, st, eo,
                        experts, routes, tok_cnt, tok_recs, cap, seq_len, max_routes);
+  }
+  if (max_routes > 0) {
+    const int bm = moe_tile_bm(max_routes, experts);
+    if (bm >= 64 && hidden % 128 == 0) {
+      hipError_t e = launch_moe_down_tiled(bucket_i8, bucket_sa, eo, routes, w_down, down_scale, y,
+                                           experts, max_routes, hidden, inter, block, bm, st);
+      if (e != hipSuccess) return e;
+    } else {
+      dim3 g((hidden / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
+      hipLaunchKernelGGL(k_moe_down_skinny<4>, g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
+                         w_down, down_scale, y, experts, hidden, inter, block, max_routes);
+    }
   }
   hipLaunchKernelGGL(k_combine, dim3((hidden + 255) / 256, seq_len), dim3(256), 0, st, y, tok_cnt,
                      tok_recs, cap, seq_len, hidden, accum, out);

@@ -1,0 +1,398 @@
+// bq_tiled.hip -- LDS-tiled v_mfma_i32_16x16x64_i8 GEMM for many rows:
+// dense prefill linears (butterquant/gemm.mojo:114-243 at large M) and the
+// grouped MoE projections at prefill (butterquant_kernels/moe.mojo:25-295).
+//
+// One template, three modes sharing the main loop:
+//   DENSE   : C = act[M,K] x W[N,K]^T, per-row or per-block epilogue
+//   GATE_UP : rows gathered by route token, B tile = 64 gate + 64 up rows of
+//             the expert, epilogue bucket = bf16(gelu(g) * u)
+//   DOWN    : rows = the expert's bucket records, per-block drains (B = 64),
+//             epilogue y[rec, n] = (facc * ws[n]) * route_w
+//
+// Pipeline: WM x WN waves, K advanced in stages of 64 bytes.
+// Operands move global -> LDS directly (global_load_lds_dwordx4, no VGPR
+// staging) into a ring of LDS stages: loads for the next ring-1 stages are
+// in flight while one stage is multiplied.  Every DMA instruction moves one 1 KiB
+// MFMA fragment (lane L's 16 bytes land at L*16): A fragments gather 16 rows
+// x 64 K of the activation, B fragments are contiguous 1 KiB runs of the
+// tile16x64 weight layout.
+#include "bq_device.hpp"
+#include "bq_kernels.hpp"
+
+#include <stdlib.h>
+
+namespace bq {
+
+enum { MODE_DENSE = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
+constexpr int kMaxBlocks = 64;  // K/block limit of the per-block path
+
+struct TiledArgs {
+  LinArgs lin;              // DENSE: segments, activation, scales, M, K, block
+  // MoE modes
+  const int8_t* a;          // GATE_UP: x_i8 [T, K]; DOWN: bucket_i8 [routes, K]
+  const float* a_scale;     // GATE_UP: x_sa [T];   DOWN: bucket_sa [routes, K/block]
+  const int32_t* eo;        // expert_offset [E+1]
+  const Route* routes;
+  const int8_t* w;          // expert weights, tile16x64, expert stride N*K
+  const float* ws;          // per-row weight scales, expert stride N
+  uint16_t* bucket;         // GATE_UP output [routes, inter]
+  float* y;                 // DOWN output [routes, N]
+  int E, max_routes, N, K, inter, block;
+  int gm, gn;               // DENSE grid decomposition
+};
+
+// Wait until at most `later` stages of this wave's fragment DMAs (D each)
+// are outstanding: s_waitcnt takes an immediate, so dispatch on the count.
+template <int D, int NBUF>
+__device__ inline void wait_dma(int later) {
+  static_assert((NBUF - 2) * D <= 63, "vmcnt field holds 6 bits");
+  switch (later) {
+#define BQ_WAIT_CASE(n) \
+    case n: if constexpr (n <= NBUF - 2) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(n * D) : "memory"); break; }
+    BQ_WAIT_CASE(7) BQ_WAIT_CASE(6) BQ_WAIT_CASE(5) BQ_WAIT_CASE(4)
+    BQ_WAIT_CASE(3) BQ_WAIT_CASE(2) BQ_WAIT_CASE(1)
+#undef BQ_WAIT_CASE
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
+// 32-bit LDS address of a __shared__ object (what M0 takes for LDS DMA)
+__device__ inline uint32_t lds_addr(const int8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
+}
+
+template <int MODE, int BM, int BN, int WM, int WN, bool PER_BLOCK, int NBUF>
+__global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
+  constexpr int KS = 1;
+  constexpr int NW = WM * WN, NT = 64 * NW;                 // waves, threads
+  constexpr int MI = BM / (16 * WM), NI = BN / (16 * WN);   // 16x16 tiles per wave
+  static_assert(MI >= 1 && NI >= 1 && (MODE != MODE_GATE_UP || NI % 2 == 0), "tile shape");
+  constexpr int FA = (BM / 16) * KS, FB = (BN / 16) * KS;  // 1 KiB fragments per stage
+  constexpr int D = (FA + FB + NW - 1) / NW;                // fragment DMAs per wave per stage
+  constexpr int REM = (FA + FB) % NW;  // when nonzero, waves >= REM issue D - 1
+  constexpr int A_STAGE = FA * 1024, B_STAGE = FB * 1024;
+  // ring of NBUF LDS stages (NBUF-1 stages of DMA in flight)
+  __shared__ __attribute__((aligned(16))) int8_t abuf_[NBUF][A_STAGE];
+  __shared__ __attribute__((aligned(16))) int8_t bbuf_[NBUF][B_STAGE];
+  // per-block activation scales of the tile's rows, times 1/127
+  __shared__ float lds_sa[PER_BLOCK ? BM * kMaxBlocks : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const bool full_d = REM == 0 || wave < REM;  // wave-uniform
+  const v4i zero = {0, 0, 0, 0};
+
+  // ---- work item -------------------------------------------------------
+  int K, n0 = 0, r0 = 0, r1 = 0, e = 0;
+  const LinSeg* seg = nullptr;
+  const int8_t* wbase;
+  if constexpr (MODE == MODE_DENSE) {
+    const int total = args.gm * args.gn;
+    int work = blockIdx.x;
+    if ((total & 7) == 0) work = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int mt = work % args.gm;
+    int nt_in = work / args.gm, s = 0;
+    for (int q = 0; q < args.lin.nseg; ++q) {
+      const int tiles = (args.lin.seg[q].n + BN - 1) / BN;
+      if (nt_in < tiles) { s = q; break; }
+      nt_in -= tiles;
+    }
+    seg = &args.lin.seg[s];
+    K = args.lin.K;
+    r0 = mt * BM;
+    r1 = min(args.lin.M, r0 + BM);
+    n0 = nt_in * BN;
+    wbase = seg->w;
+  } else {
+    if (!find_mtile(args.eo, args.E, BM, blockIdx.y, args.max_routes, e, r0, r1)) return;
+    K = args.K;
+    n0 = blockIdx.x * (MODE == MODE_GATE_UP ? BN / 2 : BN);
+    wbase = args.w + (size_t)e * args.N * K;
+  }
+  const int K64 = K >> 6;
+  const int blk = MODE == MODE_DENSE ? args.lin.block : args.block;
+  const int fpb = blk >> 6, nb = K / blk;
+  const int nstages = K64 / KS;  // launcher guarantees K64 % KS == 0
+
+  // ---- this wave's fragment DMAs: fragment wave + NW*d, d < D (or D - 1)
+  const int8_t* src[D];
+  int dst_off[D];
+  bool is_a[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int f = min(wave + NW * d, FA + FB - 1);  // the clamped slot is never issued
+    if (f < FA) {
+      const int ks = f / (BM / 16), msub = f % (BM / 16);
+      int row = r0 + msub * 16 + (lane & 15);
+      if (row >= r1) row = r0;  // rows past the tile end are never stored
+      const int8_t* rp;
+      if constexpr (MODE == MODE_DENSE) rp = args.lin.act + (size_t)row * K;
+      else if constexpr (MODE == MODE_GATE_UP) rp = args.a + (size_t)args.routes[row].token * K;
+      else rp = args.a + (size_t)row * K;
+      src[d] = rp + ks * 64 + (lane >> 4) * 16;
+      dst_off[d] = f * 1024;
+      is_a[d] = true;
+    } else {
+      const int g = f - FA;
+      const int ks = g / (BN / 16), nsub = g % (BN / 16);
+      int wrow;
+      bool ok;
+      if constexpr (MODE == MODE_GATE_UP) {
+        const int half = BN / 32;
+        wrow = nsub < half ? n0 + nsub * 16 : args.inter + n0 + (nsub - half) * 16;
+        ok = (n0 + (nsub % half) * 16) < args.inter;
+      } else if constexpr (MODE == MODE_DENSE) {
+        wrow = n0 + nsub * 16;
+        ok = wrow < seg->n;
+      } else {
+        wrow = n0 + nsub * 16;
+        ok = wrow < args.N;
+      }
+      if (!ok) wrow = 0;  // subtiles past N are never stored
+      src[d] = wbase + ((size_t)(wrow >> 4) * K64 + ks) * 1024 + lane * 16;
+      dst_off[d] = g * 1024;
+      is_a[d] = false;
+    }
+  }
+
+  if constexpr (PER_BLOCK) {
+    const float* sc = MODE == MODE_DENSE ? args.lin.sa : args.a_scale;
+    for (int i = tid; i < BM * nb; i += NT) {
+      const int m = i / nb, b = i % nb;
+      lds_sa[i] = r0 + m < r1 ? sc[(size_t)(r0 + m) * nb + b] * kInv127 : 0.0f;
+    }
+  }
+
+  // The DMA is issued from inline asm so the compiler does not track it:
+  // the only waits are the explicit vmcnt waits of the main loop (the
+  // compiler would otherwise wait for every DMA before any LDS read).
+  auto issue = [&](int8_t* abuf, int8_t* bbuf, int st) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (d == D - 1 && !full_d) break;
+      const int8_t* g = src[d] + (is_a[d] ? (size_t)st * KS * 64 : (size_t)st * KS * 1024);
+      const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr((is_a[d] ? abuf : bbuf) + dst_off[d]));
+      // M0 holds the LDS destination; one wait state separates its write from
+      // the DMA (the M0 -> LDS-DMA hazard).  These kernels use M0 for nothing
+      // else, so clobbering it is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                   :: "s"(l), "v"(g) : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+  };
+
+  int bsub[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    if constexpr (MODE == MODE_GATE_UP) {
+      const int half = BN / 32, hn = NI / 2;  // gate subtiles [0, half), up [half, 2*half)
+      bsub[ni] = ni < hn ? wn * hn + ni : half + wn * hn + (ni - hn);
+    } else {
+      bsub[ni] = wn * NI + ni;
+    }
+  }
+
+  v4i acc[MI][NI];
+  float facc[MI][NI][4];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      acc[mi][ni] = zero;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) facc[mi][ni][v] = 0.0f;
+    }
+
+  auto row_of = [&](int mi, int v) { return r0 + (wm * MI + mi) * 16 + 4 * (lane >> 4) + v; };
+
+  auto compute = [&](const int8_t* abuf, const int8_t* bbuf, int st) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      v4i a[MI], b[NI];
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+        a[mi] = *reinterpret_cast<const v4i*>(&abuf[(ks * (BM / 16) + wm * MI + mi) * 1024 + lane * 16]);
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        b[ni] = *reinterpret_cast<const v4i*>(&bbuf[(ks * (BN / 16) + bsub[ni]) * 1024 + lane * 16]);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma16x16x64(a[mi], b[ni], acc[mi][ni]);
+      if constexpr (PER_BLOCK) {
+        const int kt = st * KS + ks;
+        if (((kt + 1) & (fpb - 1)) == 0) {
+          const int b_idx = kt / fpb;
+#pragma unroll
+          for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int m = (wm * MI + mi) * 16 + 4 * (lane >> 4) + v;
+              const float adv = lds_sa[m * nb + b_idx];
+#pragma unroll
+              for (int ni = 0; ni < NI; ++ni)
+                facc[mi][ni][v] = fmaf((float)acc[mi][ni][v], adv, facc[mi][ni][v]);
+            }
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = zero;
+          }
+        }
+      }
+    }
+  };
+
+  // ---- main loop: a ring of NBUF LDS stages, NBUF-1 in flight -------------
+  // iteration s: wait for this wave's DMAs of stage s (those of the later
+  // stages already issued may stay outstanding), barrier (all waves' stage-s
+  // data has landed and every wave has finished reading stage s-1), refill
+  // stage s-1's buffer with stage s+NBUF-1, multiply stage s.  The ring is
+  // unrolled NBUF times so every buffer index is a compile-time constant.
+  for (int p = 0; p < NBUF - 1 && p < nstages; ++p) issue(abuf_[p], bbuf_[p], p);
+  for (int s0 = 0; s0 < nstages; s0 += NBUF) {
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) {
+      const int s = s0 + i;
+      if (s >= nstages) break;
+      const int later = min(NBUF - 2, nstages - 1 - s);
+      if (full_d) wait_dma<D, NBUF>(later);
+      else wait_dma<D - 1, NBUF>(later);
+      lds_barrier();
+      if (s + NBUF - 1 < nstages) issue(abuf_[(i + NBUF - 1) % NBUF], bbuf_[(i + NBUF - 1) % NBUF], s + NBUF - 1);
+      compute(abuf_[i], bbuf_[i], s);
+    }
+  }
+
+  // ---- epilogue ----------------------------------------------------------
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = row_of(mi, v);
+      if (row >= r1) continue;
+      if constexpr (MODE == MODE_DENSE) {
+        const float ad = PER_BLOCK ? 0.0f : args.lin.sa[row] * kInv127;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int col = n0 + bsub[ni] * 16 + (lane & 15);
+          if (col >= seg->n) continue;
+          const float y = PER_BLOCK ? facc[mi][ni][v] * seg->ws[col]
+                                    : (float)acc[mi][ni][v] * ad * seg->ws[col];
+          seg->out[(size_t)row * seg->n + col] = f32_to_bf16(y);
+          if (seg->out_f32) seg->out_f32[(size_t)row * seg->n + col] = y;
+        }
+      } else if constexpr (MODE == MODE_GATE_UP) {
+        const float ad = args.a_scale[args.routes[row].token] * kInv127;
+        const float* ws = args.ws + (size_t)e * args.N;
+        constexpr int hn = NI / 2;
+#pragma unroll
+        for (int j = 0; j < hn; ++j) {
+          const int col = n0 + (wn * hn + j) * 16 + (lane & 15);
+          if (col >= args.inter) continue;
+          const float g = (float)acc[mi][j][v] * ad * ws[col];
+          const float u = (float)acc[mi][hn + j][v] * ad * ws[args.inter + col];
+          args.bucket[(size_t)row * args.inter + col] = f32_to_bf16(gelu_tanh_f32(g) * u);
+        }
+      } else {
+        const float rw = args.routes[row].weight;
+        const float* ws = args.ws + (size_t)e * args.N;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int col = n0 + bsub[ni] * 16 + (lane & 15);
+          if (col >= args.N) continue;
+          args.y[(size_t)row * args.N + col] = facc[mi][ni][v] * ws[col] * rw;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile configuration: BM x BN output tile, NBUF-stage LDS ring.  Smaller
+// rings leave room for several workgroups per CU (more waves to overlap the
+// LDS-read -> MFMA -> barrier chain of each); overrides BQ_TILE_BN and
+// BQ_RING exist for tuning sweeps.
+static int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : dflt;
+}
+
+template <int MODE, int BM, int BN, int WM, int WN, bool PB>
+static void launch_cfg(int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
+  const dim3 b(64 * WM * WN);
+  if (nbuf >= 6) hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 6>), g, b, 0, st, t);
+  else if (nbuf >= 4) hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 4>), g, b, 0, st, t);
+  else hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 3>), g, b, 0, st, t);
+}
+
+// 8 waves (2 x 4) per workgroup: two waves per SIMD keep the MFMA pipe and
+// the LDS reads overlapped (one wave per SIMD leaves every latency exposed).
+template <int MODE, int BM, bool PB>
+static void launch_bn(int bn, int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
+  if (bn >= 128) launch_cfg<MODE, BM, 128, 2, 4, PB>(nbuf, g, st, t);
+  else launch_cfg<MODE, BM, 64, 2, 2, PB>(nbuf, g, st, t);
+}
+
+template <int MODE, bool PB>
+static void launch_bm(int bm, int bn, int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
+  if (bm >= 128) launch_bn<MODE, 128, PB>(bn, nbuf, g, st, t);
+  else if (bm >= 64) launch_bn<MODE, 64, PB>(bn, nbuf, g, st, t);
+  else launch_bn<MODE, 32, PB>(bn, nbuf, g, st, t);
+}
+
+hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStream_t st) {
+  const int bn = env_int("BQ_TILE_BN", 128);
+  const int nbuf = env_int("BQ_RING", 4);
+  TiledArgs t{};
+  t.lin = a;
+  int gn = 0;
+  for (int q = 0; q < a.nseg; ++q) gn += (a.seg[q].n + bn - 1) / bn;
+  const int bmv = bm >= 128 ? 128 : bm >= 64 ? 64 : 32;
+  t.gm = (a.M + bmv - 1) / bmv;
+  t.gn = gn;
+  dim3 g(t.gm * t.gn);
+  if (per_block) launch_bm<MODE_DENSE, true>(bm, bn, nbuf, g, st, t);
+  else launch_bm<MODE_DENSE, false>(bm, bn, nbuf, g, st, t);
+  return hipGetLastError();
+}
+
+static inline int mtile_bound(int max_routes, int experts, int bm) {
+  return (max_routes + bm - 1) / bm + experts;
+}
+
+hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
+                                    const Route* routes, const int8_t* w_gu,
+                                    const float* gu_scale, uint16_t* bucket, int experts,
+                                    int max_routes, int hidden, int inter, int bm,
+                                    hipStream_t st) {
+  TiledArgs t{};
+  t.a = x_i8; t.a_scale = x_sa; t.eo = eo; t.routes = routes; t.w = w_gu; t.ws = gu_scale;
+  t.bucket = bucket; t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
+  t.inter = inter; t.block = hidden;
+  const int bn = env_int("BQ_TILE_BN", 128);  // weight rows per tile: bn/2 gate + bn/2 up
+  const int nbuf = env_int("BQ_RING", 3);
+  const int bmv = bm >= 128 ? 128 : 64;
+  dim3 g((inter + bn / 2 - 1) / (bn / 2), mtile_bound(max_routes, experts, bmv));
+  launch_bm<MODE_GATE_UP, false>(bmv, bn, nbuf, g, st, t);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const int32_t* eo,
+                                 const Route* routes, const int8_t* w_d, const float* d_scale,
+                                 float* y, int experts, int max_routes, int hidden, int inter,
+                                 int block, int bm, hipStream_t st) {
+  TiledArgs t{};
+  t.a = b_i8; t.a_scale = b_sa; t.eo = eo; t.routes = routes; t.w = w_d; t.ws = d_scale; t.y = y;
+  t.E = experts; t.max_routes = max_routes; t.N = hidden; t.K = inter; t.inter = inter;
+  t.block = block;
+  const int bn = env_int("BQ_TILE_BN", 128);
+  const int nbuf = env_int("BQ_RING", 3);
+  const int bmv = bm >= 128 ? 128 : 64;
+  dim3 g((hidden + bn - 1) / bn, mtile_bound(max_routes, experts, bmv));
+  launch_bm<MODE_DOWN, true>(bmv, bn, nbuf, g, st, t);
+  return hipGetLastError();
+}
+
+}  // namespace bq

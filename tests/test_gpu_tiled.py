@@ -1,0 +1,86 @@
+"""GPU parity of the LDS-tiled MFMA paths (prefill linears and the grouped MoE
+kernels) for every tile height, against the CPU oracle, bit-exact.  Tile
+heights are forced through the library's BQ_TILE_BM / BQ_MOE_BM overrides."""
+import numpy as np
+import pytest
+
+from test_gpu_parity import dev, host, tol_check
+
+pytestmark = pytest.mark.gpu
+ONE = 0x3F80
+
+
+@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("M,K,B", [(200, 512, None), (77, 2816, None), (150, 1024, 256),
+                                   (96, 704, 64), (130, 2112, 64)])
+def test_dense_tiles(gpu, O, monkeypatch, bm, M, K, B):
+    monkeypatch.setenv("BQ_TILE_BM", str(bm))
+    N = 384  # three 128-wide n-tiles; N=2816 tails are covered in test_gpu_parity
+    wf = O.bf16_to_f32(O.synth_normal_bf16(3, 0.02, (N, K)))
+    q, s = O.rotate_and_quant(wf, B or 128)
+    W = gpu.ButterquantWeight(gpu.retile(dev(q.reshape(-1)), N, K), dev(s), N, K)
+    x = O.synth_normal_bf16(4, 1.0, (M, K))
+    if B is None:
+        xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128 if K % 128 == 0 else 64)
+        ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+        p, cs = O.pack_and_colsum(q)
+        rb, rf = O.linear(xq, sa, p, s, cs, N)
+    else:
+        xq, sa = O.block_quant(x, B, B == 64)
+        ob, of = gpu.block_linear(dev(xq), dev(sa), W, B, want_f32=True)
+        p, cs = O.pack_and_colsum(q, B, False)
+        rb, rf = O.block_linear(xq, sa, p, s, cs, N, B)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
+def test_dense_qkv_tiled(gpu, O):
+    K, M = 512, 100
+    Ws, qs = [], []
+    for n, seed in ((256, 1), (128, 2), (128, 3)):
+        wf = O.bf16_to_f32(O.synth_normal_bf16(seed, 0.02, (n, K)))
+        q, s = O.rotate_and_quant(wf, 128)
+        Ws.append(gpu.ButterquantWeight(gpu.retile(dev(q.reshape(-1)), n, K), dev(s), n, K))
+    x = O.synth_normal_bf16(6, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    outs = gpu.qkv(dev(xq), dev(sa), *Ws)
+    for o, W in zip(outs, Ws):
+        np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
+
+
+def _tiny_moe(O, gpu, T, E=4, k=2, H=128, I=64, seed=5):
+    logits = O.synth_normal_f32(seed, 1.0, (T, E))
+    idx, w = O.route_topk_softmax(logits, k)
+    gu = O.bf16_to_f32(O.synth_normal_bf16(6, 0.02, (E * 2 * I, H)))
+    gq, gs = O.rotate_and_quant(gu, 128)
+    dn = O.bf16_to_f32(O.synth_normal_bf16(7, 0.02, (E * H, I)))
+    dq, ds = O.rotate_and_quant(dn, 64)
+    x = O.synth_normal_bf16(8, 1.0, (T, H))
+    xq, xsa = O.norm_quant(x, np.full(H, ONE, np.uint16), 128)
+    Wgu = gpu.ButterquantWeight(gpu.retile(dev(gq.reshape(-1)), E * 2 * I, H), dev(gs), E * 2 * I, H)
+    Wd = gpu.ButterquantWeight(gpu.retile(dev(dq.reshape(-1)), E * H, I), dev(ds), E * H, I)
+    return dict(idx=idx, w=w, gq=gq, gs=gs, dq=dq, ds=ds, xq=xq, xsa=xsa, Wgu=Wgu, Wd=Wd,
+                T=T, E=E, k=k, H=H, I=I)
+
+
+@pytest.mark.parametrize("T,bm", [(64, None), (256, None), (64, 128), (256, 64), (256, 16),
+                                  (300, 128), (33, 64)])
+def test_moe_tiled(gpu, O, monkeypatch, T, bm):
+    if bm is not None:
+        monkeypatch.setenv("BQ_MOE_BM", str(bm))
+    c = _tiny_moe(O, gpu, T)
+    E, H, I, k = c["E"], c["H"], c["I"], c["k"]
+    eo, routes = gpu.build_schedule(dev(c["idx"]), dev(c["w"]), E)
+    bucket = gpu.moe_phase1(dev(c["xq"]), dev(c["xsa"]), eo, routes, c["Wgu"], E, T, k, I)
+    bi8, bsa = gpu.block_quant(bucket, 64, True)
+    accum, out = gpu.moe_phase2(bi8, bsa, eo, routes, c["Wd"], E, T, k, H)
+    reo, rroutes = O.build_schedule(c["idx"], c["w"], E)
+    gp, gcs = O.pack_and_colsum(c["gq"])
+    rb = O.moe_phase1(c["xq"], c["xsa"], reo, rroutes, gp, c["gs"], gcs, I)
+    np.testing.assert_array_equal(host(bucket), rb)
+    rbq, rbsa = O.block_quant(rb, 64, True)
+    dp, dcs = O.pack_and_colsum(c["dq"], 64, False)
+    racc, rout = O.moe_phase2(rbq, rbsa, reo, rroutes, T, dp, c["ds"], dcs, H)
+    np.testing.assert_array_equal(host(accum), racc)
+    np.testing.assert_array_equal(host(out), rout)
+    tol_check(host(accum), racc)
