@@ -102,7 +102,8 @@ int bq_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, floa
 
 /* dispatch_bq_block_quant[block, apply_fwht] (linear.mojo:182-205 ->
  * runtime.mojo:62-80): bf16 [seq_len, cols] -> [FWHT(block)] -> per-block int8,
- * x_sa [seq_len, cols/block] = block amax.  cols % 64 == 0, cols % block == 0. */
+ * x_sa [seq_len, cols/block] = block amax.  cols % 64 == 0, cols % block == 0;
+ * src and x_i8 16-byte aligned. */
 int bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa, int cols, int seq_len,
                    int block, int apply_fwht, void* stream);
 
@@ -153,8 +154,8 @@ int bq_moe_phase1_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* 
                           const float* gate_up_scale, uint16_t* bucket, int experts_per_rank,
                           int seq_len, int top_k, int hidden, int inter, void* stream);
 
-/* Bytes of device workspace bq_moe_phase2_down needs (per-route f32 results
- * and per-token route lists). */
+/* Bytes of device workspace bq_moe_phase2_down needs (the per-route f32
+ * down-projection rows, seq_len*top_k x hidden). */
 size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden);
 
 /* dispatch_bq_phase2_down[hidden, inter] (moe.mojo:298-335): per-block
@@ -162,7 +163,11 @@ size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden);
  * and accumulated per token in ascending expert order into moe_accum
  * f32 [seq_len, hidden]; moe_out = bf16(moe_accum).  w_down rows are
  * [experts_per_rank*hidden, inter] (expert stride hidden*inter).
- * workspace: >= bq_moe_phase2_workspace_size() bytes, 256-byte aligned. */
+ * Each expert's route records must be in ascending token order (the order
+ * bq_moe_build_schedule and the reference's schedule produce), and a token
+ * appears at most once per expert; top_k <= 16.
+ * workspace: >= bq_moe_phase2_workspace_size() bytes, 256-byte aligned;
+ * moe_accum and moe_out 16-byte aligned. */
 int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                        const int32_t* expert_offset, const bq_route* routes, const int8_t* w_down,
                        const float* down_scale, float* moe_accum, uint16_t* moe_out,

@@ -161,14 +161,12 @@ __global__ __launch_bounds__(1024) void k_norm_quant_reg(
     }
   }
   for (int st = 1; st < block && st < kWave; st <<= 1) {
+    const XlaneStage x(st);
 #pragma unroll
     for (int q = 0; q < MAXSEG; ++q) {
       if (wave + q * nw >= nseg) continue;
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const float p = __shfl_xor(v[q][i], st, kWave);
-        v[q][i] = (lane & st) ? (p - v[q][i]) : (v[q][i] + p);
-      }
+      for (int i = 0; i < R; ++i) v[q][i] = x(v[q][i]);
     }
   }
 #pragma unroll
@@ -209,42 +207,192 @@ __global__ __launch_bounds__(1024) void k_norm_quant_reg(
   if (tid == 0) sa[t] = amax;
 }
 
-// Each wave owns segments of S = R*64 values (one block when B >= 64, or
-// 64/B blocks when B < 64) of one row; grid-stride over all segments.
-template <int R>
+// Long sequences: one wave per token, four tokens per workgroup.  The row
+// is staged in the wave's own LDS slice (the gain once per workgroup); the
+// sum of squares keeps the rms_reduce_row order of k_norm_quant (chain c =
+// p*16+j over pairs c + i*pu*16; lane-wise sum over p; 16-lane halving tree),
+// and FWHT / quantization run on registers, value q*S + r*64 + lane of
+// segment q.  Every one of the NSEG segments is processed without branches
+// (segments past nseg read a clamped position and are zeroed): per-segment
+// guards would split the shuffles into separate blocks and serialize them.
+template <int R, int NSEG>
+__global__ __launch_bounds__(256) void k_norm_quant_wave(
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int T, int hidden, int block, int pu,
+    float sqrt_n, float n_eps, float fwht_scale) {
+  extern __shared__ uint32_t lds_rows[];  // [gain | row of wave 0..3], bf16 pairs
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int t = blockIdx.x * 4 + wave;
+  constexpr int S = R * kWave;
+  const int nseg = hidden / S, nchunk = hidden / 8;
+  uint32_t* gs = lds_rows;
+  // the row's loads go out before the gain's barrier so both latencies overlap
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(src + (size_t)min(t, T - 1) * hidden);
+  constexpr int CH = (NSEG * R + 7) / 8;  // 16-byte chunks per lane (NSEG*R*64 values)
+  v4i raw[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) raw[i] = ld16(xrow + (size_t)min(lane + 64 * i, nchunk - 1) * 16);
+  for (int c = threadIdx.x; c < nchunk; c += blockDim.x)
+    reinterpret_cast<v4i*>(gs)[c] = ld16(reinterpret_cast<const int8_t*>(gamma) + (size_t)c * 16);
+  __syncthreads();
+  if (t >= T) return;  // whole waves only; nothing below synchronizes the block
+  uint32_t* xs = lds_rows + (size_t)(wave + 1) * (hidden / 2);
+#pragma unroll
+  for (int i = 0; i < CH; ++i)
+    if (lane + 64 * i < nchunk) reinterpret_cast<v4i*>(xs)[lane + 64 * i] = raw[i];
+
+  // chains c0 = lane and c1 = lane + 64 (pu*16 <= 128 chains), interleaved
+  const int chains = pu * 16;  // also the pair stride of a chain
+  const int iters = hidden / (pu * 32);
+  const int c1 = min(lane + 64, chains - 1);
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+  for (int i = 0; i < iters; ++i) {
+    const uint32_t p0 = xs[i * chains + min(lane, chains - 1)], p1 = xs[i * chains + c1];
+    a0 = fmaf(__uint_as_float(p0 & 0xFFFF0000u), __uint_as_float(p0 & 0xFFFF0000u), a0);
+    a0 = fmaf(__uint_as_float(p0 << 16), __uint_as_float(p0 << 16), a0);
+    a1 = fmaf(__uint_as_float(p1 & 0xFFFF0000u), __uint_as_float(p1 & 0xFFFF0000u), a1);
+    a1 = fmaf(__uint_as_float(p1 << 16), __uint_as_float(p1 << 16), a1);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int c = p * 16 + (lane & 15);
+    const float v0 = __shfl(a0, c & 63, kWave);
+    const float v1 = __shfl(a1, c & 63, kWave);
+    if (p < pu) sum = sum + (c < 64 ? v0 : v1);
+  }
+#pragma unroll
+  for (int h = 8; h >= 1; h >>= 1) sum = sum + __shfl_down(sum, h, 16);
+  const float total = __shfl(sum, 0, kWave);
+  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+
+  float v[NSEG][R];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = min(q, nseg - 1) * S + r * kWave + lane;
+      const uint32_t w = xs[k >> 1], gw = gs[k >> 1];
+      const float xv = __uint_as_float((k & 1) ? (w & 0xFFFF0000u) : (w << 16));
+      const float g = __uint_as_float((k & 1) ? (gw & 0xFFFF0000u) : (gw << 16));
+      const float val = xv * inv_rms * g;
+      v[q][r] = q < nseg ? val : 0.0f;
+    }
+  for (int st = 1; st < block && st < kWave; st <<= 1) {
+    const XlaneStage x(st);
+#pragma unroll
+    for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[q][r] = x(v[q][r]);
+  }
+#pragma unroll
+  for (int rs = 1; rs < R; rs <<= 1) {
+    if (rs * kWave >= block) continue;
+#pragma unroll
+    for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (r & rs) continue;
+        const float a = v[q][r], b = v[q][r + rs];
+        v[q][r] = a + b;
+        v[q][r + rs] = a - b;
+      }
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      v[q][r] = v[q][r] * fwht_scale;
+      m = fmaxf(m, fabsf(v[q][r]));
+    }
+  const float amax = wave_max(m);
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int8_t* qrow = xq + (size_t)t * hidden;
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (q < nseg) qrow[q * S + r * kWave + lane] = quantize_i8(v[q][r], inv);
+  if (lane == 0) sa[t] = amax;
+}
+
+template <int R, int NSEG>
+static void launch_nq_wave(dim3 g, size_t lds, hipStream_t st, const uint16_t* src,
+                           const uint16_t* gamma, int8_t* xq, float* sa, int T, int hidden,
+                           int block, int pu, float sqrt_n, float n_eps, float sc) {
+  hipLaunchKernelGGL((k_norm_quant_wave<R, NSEG>), g, dim3(256), lds, st, src, gamma, xq, sa, T,
+                     hidden, block, pu, sqrt_n, n_eps, sc);
+}
+
+// smallest instance holding nseg segments of R*64 values (hidden <= 4096)
+static bool launch_norm_quant_wave(int R, int nseg, const uint16_t* src, const uint16_t* gamma,
+                                   int8_t* xq, float* sa, int T, int hidden, int block, int pu,
+                                   float sqrt_n, float n_eps, float sc, hipStream_t st) {
+  const dim3 g((T + 3) / 4);
+  const size_t lds = (size_t)5 * hidden * 2;  // gain + four rows
+#define BQ_NQW(RR, NS) \
+  if (R == RR && nseg <= NS) { launch_nq_wave<RR, NS>(g, lds, st, src, gamma, xq, sa, T, hidden, block, pu, sqrt_n, n_eps, sc); return true; }
+  BQ_NQW(1, 16) BQ_NQW(1, 32) BQ_NQW(1, 44) BQ_NQW(1, 64)
+  BQ_NQW(2, 8) BQ_NQW(2, 16) BQ_NQW(2, 22) BQ_NQW(2, 32)
+  BQ_NQW(4, 4) BQ_NQW(4, 8) BQ_NQW(4, 11) BQ_NQW(4, 16)
+  BQ_NQW(8, 2) BQ_NQW(8, 4) BQ_NQW(8, 6) BQ_NQW(8, 8)
+#undef BQ_NQW
+  return false;
+}
+
+// Flat over the whole [rows, cols] matrix: lane i owns the 8 consecutive
+// values [8i, 8i+8); a block of B values spans LPB = B/8 aligned lanes and
+// blocks never straddle rows (cols % B == 0), so block b's scale lands at
+// sa[b] = sa[row * cols/B + col/B].  FWHT strides 1, 2, 4 run inside the lane,
+// strides 8 ... B/2 across lanes, in the reference's ascending stage order.
+template <int LPB>
 __global__ __launch_bounds__(256) void k_block_quant(
     const uint16_t* __restrict__ src, int8_t* __restrict__ xq, float* __restrict__ sa,
-    int rows, int cols, int block, int apply_fwht, float fwht_scale) {
+    size_t nchunks, int apply_fwht, float fwht_scale) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t c = i < nchunks ? i : nchunks - 1;  // whole LPB groups are in or out
   const int lane = lane_id();
-  const int S = R * kWave;
-  const int segs_per_row = cols / S;
-  const int nb = cols / block;
-  const size_t total = (size_t)rows * segs_per_row;
-  const size_t wave_id = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const size_t nwaves = ((size_t)gridDim.x * blockDim.x) >> 6;
-  for (size_t g = wave_id; g < total; g += nwaves) {
-    const int r = (int)(g / segs_per_row), sg = (int)(g % segs_per_row);
-    const size_t base = (size_t)r * cols + (size_t)sg * S;
-    float v[R];
+  const v4i raw = *reinterpret_cast<const v4i*>(src + c * 8);
+  float v[8];
 #pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = bf16_to_f32(src[base + i * kWave + lane]);
-    if (apply_fwht) {
-      fwht_wave<R>(v, block);
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float((uint32_t)raw[j] << 16);
+    v[2 * j + 1] = __uint_as_float((uint32_t)raw[j] & 0xFFFF0000u);
+  }
+  if (apply_fwht) {
 #pragma unroll
-      for (int i = 0; i < R; ++i) v[i] = v[i] * fwht_scale;
+    for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j & s) continue;
+        const float a = v[j], b = v[j + s];
+        v[j] = a + b;
+        v[j + s] = a - b;
+      }
+#pragma unroll
+    for (int s = 1; s < LPB; s <<= 1) {
+      const XlaneStage x(s);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = x(v[j]);
     }
-    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < R; ++i) m = fmaxf(m, fabsf(v[i]));
-    const float bm = block >= kWave ? wave_max(m) : group_max(m, block);
-    const float inv = bm > 0.0f ? 127.0f / bm : 0.0f;
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * fwht_scale;
+  }
+  float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < R; ++i) xq[base + i * kWave + lane] = quantize_i8(v[i], inv);
-    if (block >= kWave) {
-      if (lane == 0) sa[(size_t)r * nb + (size_t)sg * S / block] = bm;
-    } else if ((lane % block) == 0) {
-      sa[(size_t)r * nb + ((size_t)sg * S + lane) / block] = bm;
-    }
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+#pragma unroll
+  for (int s = 1; s < LPB; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, kWave));
+  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j >> 2] |= (uint32_t)(uint8_t)quantize_i8(v[j], inv) << (8 * (j & 3));
+  if (i < nchunks) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(xq + c * 8) = u2{w[0], w[1]};
+    if ((lane & (LPB - 1)) == 0) sa[c / LPB] = m;
   }
 }
 
@@ -267,6 +415,10 @@ hipError_t launch_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t*
   const int nseg = hidden / (R * 64);
   constexpr int MAXSEG = 4;
   const int waves = (nseg + MAXSEG - 1) / MAXSEG;
+  if (seq_len >= 256 && hidden <= 4096 &&
+      launch_norm_quant_wave(R, nseg, src, gamma, xq, sa, seq_len, hidden, block, pu, sqrt_n,
+                             n_eps, sc, st))
+    return hipGetLastError();
   if (waves <= 16) {
     const int threads = 64 * (waves < 4 ? 4 : waves);
     const size_t lds = (size_t)hidden * 2;
@@ -296,16 +448,15 @@ hipError_t launch_block_quant(const uint16_t* src, int8_t* xq, float* sa, int ro
                               int block, int apply_fwht, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
   const float sc = fwht_scale_host(block);
-  const int R = block < 64 ? 1 : block / 64;
-  const size_t segs = (size_t)rows * (cols / (R * 64));
-  size_t blocks = (segs + 3) / 4;
-  if (blocks > 8192) blocks = 8192;
-  dim3 g((unsigned)blocks), b(256);
-  switch (R) {
-    case 1: hipLaunchKernelGGL(k_block_quant<1>, g, b, 0, st, src, xq, sa, rows, cols, block, apply_fwht, sc); break;
-    case 2: hipLaunchKernelGGL(k_block_quant<2>, g, b, 0, st, src, xq, sa, rows, cols, block, apply_fwht, sc); break;
-    case 4: hipLaunchKernelGGL(k_block_quant<4>, g, b, 0, st, src, xq, sa, rows, cols, block, apply_fwht, sc); break;
-    case 8: hipLaunchKernelGGL(k_block_quant<8>, g, b, 0, st, src, xq, sa, rows, cols, block, apply_fwht, sc); break;
+  const size_t nchunks = (size_t)rows * cols / 8;
+  dim3 g((unsigned)((nchunks + 255) / 256)), b(256);
+  switch (block) {
+    case 16: hipLaunchKernelGGL(k_block_quant<2>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
+    case 32: hipLaunchKernelGGL(k_block_quant<4>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
+    case 64: hipLaunchKernelGGL(k_block_quant<8>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
+    case 128: hipLaunchKernelGGL(k_block_quant<16>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
+    case 256: hipLaunchKernelGGL(k_block_quant<32>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
+    case 512: hipLaunchKernelGGL(k_block_quant<64>, g, b, 0, st, src, xq, sa, nchunks, apply_fwht, sc); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

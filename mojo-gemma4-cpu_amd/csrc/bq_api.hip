@@ -124,6 +124,8 @@ int bq_block_quant(const uint16_t* src, int8_t* x_i8, float* x_sa, int cols, int
     return fail(BQ_ERR_SHAPE, "bq_block_quant: unsupported block %d", block);
   if (cols <= 0 || cols % 64 || cols % block)  // runtime.mojo:68-70
     return fail(BQ_ERR_SHAPE, "bq_block_quant: cols %d must be a multiple of 64 and of block %d", cols, block);
+  if (!a16(src) || !a16(x_i8))
+    return fail(BQ_ERR_INVALID, "bq_block_quant: src and x_i8 must be 16-byte aligned");
   return check_hip(bq::launch_block_quant(src, x_i8, x_sa, seq_len, cols, block, apply_fwht,
                                           S(stream)), "block_quant");
 }
@@ -233,8 +235,8 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
   if (!pow2(block) || block < 64 || inter % block || inter % 64 || hidden % 16 || hidden <= 0)
     return fail(BQ_ERR_SHAPE, "bq_moe_phase2_down: need block a power of two >= 64 dividing inter, hidden %% 16 == 0");
   if (inter / block > 64) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: inter/block = %d > 64", inter / block);
-  if (!a16(bucket_i8) || !a16(w_down))
-    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: int8 operands must be 16-byte aligned");
+  if (!a16(bucket_i8) || !a16(w_down) || !a16(moe_accum) || !a16(moe_out))
+    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: int8 operands, moe_accum and moe_out must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: workspace must be 256-byte aligned");
   const size_t need = bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);

@@ -120,6 +120,24 @@ __device__ inline float group_max(float v, int width) {
   return v;
 }
 
+// One element of a cross-lane FWHT stage of stride st: the lane with bit st
+// clear holds a and gets a + b, its partner holds b and gets a - b.  Computed
+// as fmaf(s, v, p) with s = +1 / -1 and p the partner's value: s*v is exact,
+// so the one rounding gives exactly v + p (= a + b) or p - v (= a - b).
+struct XlaneStage {
+  int addr;  // byte address of the partner lane for ds_bpermute
+  float s;
+  __device__ explicit XlaneStage(int st) {
+    const int lane = (int)(threadIdx.x & 63);
+    addr = (lane ^ st) << 2;
+    s = (lane & st) ? -1.0f : 1.0f;
+  }
+  __device__ float operator()(float v) const {
+    const float p = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v)));
+    return fmaf(s, v, p);
+  }
+};
+
 // In-wave FWHT of one segment of S = R*64 values (R = max(1, B/64)), value
 // index r*64 + lane.  For B < 64 the wave holds 64/B independent blocks (one
 // value per lane, block = lane / B).  Every (a, b) pair of a stage is
@@ -129,11 +147,9 @@ template <int R>
 __device__ inline void fwht_wave(float (&v)[R], int block) {
   const int lane = lane_id();
   for (int s = 1; s < block && s < kWave; s <<= 1) {
+    const XlaneStage x(s);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float p = __shfl_xor(v[r], s, kWave);
-      v[r] = (lane & s) ? (p - v[r]) : (v[r] + p);
-    }
+    for (int r = 0; r < R; ++r) v[r] = x(v[r]);
   }
 #pragma unroll
   for (int rs = 1; rs < R; rs <<= 1) {

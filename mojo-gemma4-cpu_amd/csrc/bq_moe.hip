@@ -2,9 +2,8 @@
 // and its CSR schedule (kernels/moe_router.mojo:60-106).
 //
 // Schedule: expert_offset[E+1] (exclusive prefix of per-expert route counts)
-//   and routes[] sorted by (expert, token, k) -- the reference's order -- built
-//   by one workgroup with LDS counters and per-expert token bitmasks (a route's
-//   rank = number of earlier tokens routed to the same expert).
+//   and routes[] sorted by (expert, token, k) -- the reference's order -- one
+//   workgroup per expert, ranks from a block scan over route slots.
 // Phase 1 (moe.mojo:25-164): grouped GEMM over (expert m-tile, intermediate
 //   tile); each wave accumulates the gate and up 16x16 tiles of the same
 //   intermediate columns, so the epilogue bucket = bf16(gelu(g)*u) is
@@ -13,6 +12,8 @@
 //   per-route f32 results y = (facc*ws)*route_w, then a combine that adds each
 //   token's routes in ascending expert order -- the reference's accumulation
 //   order (experts ascending, moe.mojo:259-282) -- so accum is bit-identical.
+//   The combine relies on each expert's records being in ascending token
+//   order, as the schedule (and the reference's) produces them.
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
@@ -22,67 +23,93 @@ namespace bq {
 
 constexpr int kMaxExperts = 256;
 
-__global__ __launch_bounds__(1024) void k_build_schedule(
-    const int32_t* __restrict__ route_idx, const float* __restrict__ route_w, int T, int top_k,
-    int ebase, int E, int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
-  __shared__ int cnt[kMaxExperts];
-  __shared__ int running[kMaxExperts];
-  __shared__ uint32_t bits[kMaxExperts][32];
-  __shared__ int wpre[kMaxExperts][32];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();
-  const int slots = T * top_k;
-  for (int s = tid; s < slots; s += blockDim.x) {
-    const int e = route_idx[s] - ebase;
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+// One workgroup per expert e.  Because each token's top-k experts are
+// distinct, the (expert, token, k) order puts route slot s = t*top_k + kk of
+// expert e at expert_offset[e] + (number of earlier slots routed to e), and
+// expert_offset[e] = number of slots routed to experts below e.  Both counts
+// come from scanning route_idx: a chunk of kRows x 1024 slots is read
+// coalesced (thread tid takes slots j*1024 + tid, row j = 0..kRows-1), so
+// slot order is (row, wave, lane): per-row wave ballots plus one exclusive
+// scan over the kRows x 16 (row, wave) counts give every hit its rank.
+constexpr int kSchedThreads = 1024, kSchedWaves = kSchedThreads / 64, kRows = 16;
+
+__global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
+    const int32_t* __restrict__ route_idx, const float* __restrict__ route_w, int slots,
+    int top_k, int ebase, int E, int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
+  __shared__ int cnt[kRows * kSchedWaves];  // per (row, wave) counts, then their exclusive prefix
+  __shared__ int red[2 * kSchedWaves];
+  __shared__ int chunk_total;
+  const int e = blockIdx.x, target = ebase + e, tid = threadIdx.x;
+  const int lane = lane_id(), wave = tid >> 6;
+  constexpr int kChunk = kRows * kSchedThreads;
+  // pass 1: slots routed to experts below e, and to e
+  int below = 0, mine = 0;
+  for (int c0 = 0; c0 < slots; c0 += kChunk) {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const int s = c0 + j * kSchedThreads + tid;
+      const int x = route_idx[min(s, slots - 1)];  // unmasked: loads stay batched
+      below += (s < slots && x >= ebase && x < target) ? 1 : 0;
+      mine += (s < slots && x == target) ? 1 : 0;
+    }
   }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    below += __shfl_xor(below, o, kWave);
+    mine += __shfl_xor(mine, o, kWave);
+  }
+  if (lane == 0) { red[wave] = below; red[kSchedWaves + wave] = mine; }
   __syncthreads();
+  int offset = 0, count = 0;
+#pragma unroll
+  for (int w = 0; w < kSchedWaves; ++w) { offset += red[w]; count += red[kSchedWaves + w]; }
   if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      expert_offset[e] = run;
-      running[e] = run;
-      run += cnt[e];
-    }
-    expert_offset[E] = run;
+    expert_offset[e] = offset;
+    if (e == E - 1) expert_offset[E] = offset + count;
   }
-  __syncthreads();
-  for (int c0 = 0; c0 < T; c0 += 1024) {
-    for (int i = tid; i < E * 32; i += blockDim.x) bits[i >> 5][i & 31] = 0u;
-    __syncthreads();
-    const int t = c0 + tid;
-    if (t < T) {
-      for (int kk = 0; kk < top_k; ++kk) {
-        const int e = route_idx[(size_t)t * top_k + kk] - ebase;
-        if (e >= 0 && e < E) atomicOr(&bits[e][tid >> 5], 1u << (tid & 31));
-      }
+  // pass 2: ranks in slot order
+  int run = offset;
+  for (int c0 = 0; c0 < slots; c0 += kChunk) {
+    unsigned long long m[kRows];
+    float wts[kRows];
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const int s = c0 + j * kSchedThreads + tid;
+      const int sc = min(s, slots - 1);
+      const int x = route_idx[sc];
+      wts[j] = route_w[sc];
+      m[j] = __ballot(s < slots && x == target);
+      if (lane == 0) cnt[j * kSchedWaves + wave] = __popcll(m[j]);
     }
     __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) {
-      int run = 0;
-      for (int w = 0; w < 32; ++w) {
-        wpre[e][w] = run;
-        run += __popc(bits[e][w]);
+    if (wave == 0) {  // exclusive scan of the kRows*16 (row, wave) counts, 4 per lane
+      int v[4], sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { v[i] = cnt[lane * 4 + i]; sum += v[i]; }
+      int inc = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += y;
       }
+      int ex = inc - sum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { cnt[lane * 4 + i] = ex; ex += v[i]; }
+      if (lane == 63) chunk_total = inc;
     }
     __syncthreads();
-    if (t < T) {
-      const int w = tid >> 5;
-      const uint32_t below = (1u << (tid & 31)) - 1u;
-      for (int kk = 0; kk < top_k; ++kk) {
-        const size_t slot = (size_t)t * top_k + kk;
-        const int e = route_idx[slot] - ebase;
-        if (e >= 0 && e < E) {
-          const int pos = running[e] + wpre[e][w] + __popc(bits[e][w] & below);
-          routes[pos].token = t;
-          routes[pos].weight = route_w[slot];
-        }
+    const unsigned long long below_lane = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      if ((m[j] >> lane) & 1ull) {
+        const int pos = run + cnt[j * kSchedWaves + wave] + __popcll(m[j] & below_lane);
+        const int s = c0 + j * kSchedThreads + tid;
+        routes[pos].token = s / top_k;
+        routes[pos].weight = wts[j];
       }
     }
-    __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) running[e] += wpre[e][31] + __popc(bits[e][31]);
-    __syncthreads();
+    run += chunk_total;
+    __syncthreads();  // cnt / chunk_total are rewritten by the next chunk
   }
 }
 
@@ -205,65 +232,68 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
   }
 }
 
-__global__ void k_fill_i32(int32_t* p, int n, int v) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
+// Ordered combine, one workgroup per token t: accum[t, :] = (((0 + y[r1]) +
+// y[r2]) + ...) over t's records in ascending expert order (moe.mojo:259-282),
+// out = bf16(accum).  t's record in expert e's segment is found by binary
+// search (segments are in ascending token order); a ballot over experts
+// lists the records in ascending expert order.  At most kMaxTopK records.
+constexpr int kMaxTopK = 16;
 
-// per-token record lists (unordered; the combine sorts them)
-__global__ void k_token_lists(const int32_t* __restrict__ eo, int E, const Route* __restrict__ routes,
-                              int32_t* __restrict__ tok_cnt, int32_t* __restrict__ tok_recs,
-                              int cap, int T, int max_routes) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= eo[E] || r >= max_routes) return;
-  const int t = routes[r].token;
-  if (t < 0 || t >= T) return;
-  const int p = atomicAdd(&tok_cnt[t], 1);
-  if (p < cap) tok_recs[(size_t)t * cap + p] = r;
-}
-
-// Same lists built by one workgroup with LDS counters (seq_len <= 16384):
-// no separate clearing pass over global memory.
-__global__ __launch_bounds__(1024) void k_token_lists_lds(
-    const int32_t* __restrict__ eo, int E, const Route* __restrict__ routes,
-    int32_t* __restrict__ tok_cnt, int32_t* __restrict__ tok_recs, int cap, int T,
-    int max_routes) {
-  extern __shared__ int cnt[];
-  for (int t = threadIdx.x; t < T; t += blockDim.x) cnt[t] = 0;
-  __syncthreads();
-  const int n = min(eo[E], max_routes);
-  for (int r = threadIdx.x; r < n; r += blockDim.x) {
-    const int t = routes[r].token;
-    if (t < 0 || t >= T) continue;
-    const int p = atomicAdd(&cnt[t], 1);
-    if (p < cap) tok_recs[(size_t)t * cap + p] = r;
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) tok_cnt[t] = cnt[t];
-}
-
-// accum[t, n] = (((0 + y[r1,n]) + y[r2,n]) + ...) over t's records in
-// ascending record order (= ascending expert order); out = bf16(accum).
 __global__ __launch_bounds__(256) void k_combine(
-    const float* __restrict__ y, const int32_t* __restrict__ tok_cnt,
-    const int32_t* __restrict__ tok_recs, int cap, int T, int hidden,
-    float* __restrict__ accum, uint16_t* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= hidden) return;
-  int recs[16];
-  int cnt = tok_cnt[t];
-  cnt = cnt < cap ? cnt : cap;
-  for (int j = 0; j < cnt; ++j) {
-    const int r = tok_recs[(size_t)t * cap + j];
-    int p = j;
-    while (p > 0 && recs[p - 1] > r) { recs[p] = recs[p - 1]; --p; }
-    recs[p] = r;
+    const float* __restrict__ y, const int32_t* __restrict__ eo, const Route* __restrict__ routes,
+    int E, int max_routes, int hidden, float* __restrict__ accum, uint16_t* __restrict__ out) {
+  __shared__ int recs[kMaxTopK];
+  __shared__ int wsum[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  int cnt = 0;
+  for (int e0 = 0; e0 < E; e0 += 256) {
+    const int e = e0 + tid;
+    int found = -1;
+    if (e < E) {
+      const int lo0 = max(0, min(eo[e], max_routes)), hi0 = max(0, min(eo[e + 1], max_routes));
+      int lo = lo0, hi = hi0;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (routes[mid].token < t) lo = mid + 1; else hi = mid;
+      }
+      if (lo < hi0 && routes[lo].token == t) found = lo;
+    }
+    const unsigned long long m = __ballot(found >= 0);
+    if (lane == 0) wsum[wave] = __popcll(m);
+    __syncthreads();
+    int base = cnt, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      base += w < wave ? wsum[w] : 0;
+      total += wsum[w];
+    }
+    if (found >= 0) {
+      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+      if (pos < kMaxTopK) recs[pos] = found;
+    }
+    cnt += total;
+    __syncthreads();
   }
-  float acc = 0.0f;
-  for (int j = 0; j < cnt; ++j) acc = acc + y[(size_t)recs[j] * hidden + n];
-  accum[(size_t)t * hidden + n] = acc;
-  out[(size_t)t * hidden + n] = f32_to_bf16(acc);
+  cnt = min(cnt, kMaxTopK);
+  int rr[kMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) rr[j] = j < cnt ? recs[j] : 0;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  for (int c = tid * 4; c < hidden; c += 1024) {
+    f4 v[kMaxTopK];
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+      if (j < cnt) v[j] = *reinterpret_cast<const f4*>(y + (size_t)rr[j] * hidden + c);
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+      if (j < cnt) acc = acc + v[j];
+    *reinterpret_cast<f4*>(accum + (size_t)t * hidden + c) = acc;
+    const uint32_t lo = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(out + (size_t)t * hidden + c) = u2{lo, hi};
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -274,8 +304,8 @@ hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w,
                                  Route* routes, hipStream_t st) {
   if (seq_len <= 0) return hipSuccess;
   if (experts > kMaxExperts) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_build_schedule, dim3(1), dim3(1024), 0, st, route_idx, route_w, seq_len,
-                     top_k, expert_base, experts, expert_offset, routes);
+  hipLaunchKernelGGL(k_build_schedule, dim3(experts), dim3(kSchedThreads), 0, st, route_idx,
+                     route_w, seq_len * top_k, top_k, expert_base, experts, expert_offset, routes);
   return hipGetLastError();
 }
 
@@ -287,13 +317,18 @@ static inline int mtile_bound(int max_routes, int experts, int bm) {
 
 // m-tile height for the grouped kernels from the mean routes per expert:
 // 16-row skinny tiles while experts see a handful of tokens (decode), LDS-
-// tiled 64/128-row tiles once each expert's weights can be reused.
+// tiled tiles once each expert's weights can be reused.  The tile is sized
+// so that nearly every expert fits in one m-tile (mean + 4 standard
+// deviations of a binomial count): then each expert's weights stream from
+// HBM once instead of once per m-tile.
 int moe_tile_bm(int max_routes, int experts) {
   if (const char* s = getenv("BQ_MOE_BM")) return atoi(s);
   const int per = max_routes / (experts > 0 ? experts : 1);
-  if (per >= 96) return 128;
-  if (per >= 24) return 64;
-  return 16;
+  if (per < 24) return 16;
+  const double hi = per + 4.0 * __builtin_sqrt((double)per);
+  if (hi > 128.0) return 256;
+  if (hi > 64.0) return 128;
+  return 64;
 }
 
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
@@ -315,10 +350,7 @@ static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t moe_phase2_workspace(int max_routes, int seq_len, int hidden) {
   if (seq_len <= 0) return 0;
-  const size_t cap = ((size_t)max_routes + seq_len - 1) / seq_len;
-  return align256((size_t)max_routes * hidden * sizeof(float)) +
-         align256((size_t)seq_len * sizeof(int32_t)) +
-         align256((size_t)seq_len * cap * sizeof(int32_t));
+  return align256((size_t)max_routes * hidden * sizeof(float));
 }
 
 hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, const int32_t* eo,
@@ -327,25 +359,13 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                              int max_routes, int hidden, int inter, int block, void* workspace,
                              hipStream_t st) {
   if (seq_len <= 0) return hipSuccess;
-  const int cap = (max_routes + seq_len - 1) / seq_len;
-  if (cap > 16) return hipErrorInvalidValue;
-  char* ws = (char*)workspace;
-  float* y = (float*)ws;
-  int32_t* tok_cnt = (int32_t*)(ws + align256((size_t)max_routes * hidden * sizeof(float)));
-  int32_t* tok_recs = (int32_t*)((char*)tok_cnt + align256((size_t)seq_len * sizeof(int32_t)));
-  if (seq_len <= 16384) {
-    hipLaunchKernelGGL(k_token_lists_lds, dim3(1), dim3(1024), (size_t)seq_len * sizeof(int), st,
-                       eo, experts, routes, tok_cnt, tok_recs, cap, seq_len, max_routes);
-  } else {
-    hipLaunchKernelGGL(k_fill_i32, dim3((seq_len + 255) / 256), dim3(256), 0, st, tok_cnt, seq_len, 0);
-    hipLaunchKernelGGL(k_token_lists, dim3((max_routes + 255) / 256), dim3(256), 0, st, eo,
-                       experts, routes, tok_cnt, tok_recs, cap, seq_len, max_routes);
-  }
+  float* y = (float*)workspace;
   if (max_routes > 0) {
     const int bm = moe_tile_bm(max_routes, experts);
     if (bm >= 64 && hidden % 128 == 0) {
+      const int bm_down = getenv("BQ_MOE_BM") ? bm : 64;  // see launch_moe_down_tiled
       hipError_t e = launch_moe_down_tiled(bucket_i8, bucket_sa, eo, routes, w_down, down_scale, y,
-                                           experts, max_routes, hidden, inter, block, bm, st);
+                                           experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
       dim3 g((hidden / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
@@ -353,8 +373,8 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                          w_down, down_scale, y, experts, hidden, inter, block, max_routes);
     }
   }
-  hipLaunchKernelGGL(k_combine, dim3((hidden + 255) / 256, seq_len), dim3(256), 0, st, y, tok_cnt,
-                     tok_recs, cap, seq_len, hidden, accum, out);
+  hipLaunchKernelGGL(k_combine, dim3(seq_len), dim3(256), 0, st, y, eo, routes, experts,
+                     max_routes, hidden, accum, out);
   return hipGetLastError();
 }
 

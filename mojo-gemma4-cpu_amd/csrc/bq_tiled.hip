@@ -24,7 +24,6 @@
 namespace bq {
 
 enum { MODE_DENSE = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
-constexpr int kMaxBlocks = 64;  // K/block limit of the per-block path
 
 struct TiledArgs {
   LinArgs lin;              // DENSE: segments, activation, scales, M, K, block
@@ -38,7 +37,8 @@ struct TiledArgs {
   uint16_t* bucket;         // GATE_UP output [routes, inter]
   float* y;                 // DOWN output [routes, N]
   int E, max_routes, N, K, inter, block;
-  int gm, gn;               // DENSE grid decomposition
+  int gm, gn;               // grid decomposition: m-tiles, n-tiles
+  int order;                // MoE work order (0: n-tile fastest, 1: XCD ranges, 2: m-tile per XCD)
 };
 
 // Wait until at most `later` stages of this wave's fragment DMAs (D each)
@@ -49,6 +49,7 @@ __device__ inline void wait_dma(int later) {
   switch (later) {
 #define BQ_WAIT_CASE(n) \
     case n: if constexpr (n <= NBUF - 2) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(n * D) : "memory"); break; }
+    BQ_WAIT_CASE(12) BQ_WAIT_CASE(11) BQ_WAIT_CASE(10) BQ_WAIT_CASE(9) BQ_WAIT_CASE(8)
     BQ_WAIT_CASE(7) BQ_WAIT_CASE(6) BQ_WAIT_CASE(5) BQ_WAIT_CASE(4)
     BQ_WAIT_CASE(3) BQ_WAIT_CASE(2) BQ_WAIT_CASE(1)
 #undef BQ_WAIT_CASE
@@ -61,21 +62,32 @@ __device__ inline uint32_t lds_addr(const int8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
 }
 
+// A stage covers 128 bytes of K (two MFMA k-steps of 64).
+//   A: BM/8 DMAs, each 8 rows x 128 B, so every DMA reads whole 128-byte
+//      lines (a DMA of 16 rows x 64 B -- the raw MFMA fragment -- moves a
+//      third as fast).  Inside a 1 KiB block (rows 8b..8b+7) the 16-byte
+//      chunk c of row r sits at slot r*8 + (c ^ r ^ (b & 1)): the swizzle
+//      keeps the MFMA operand reads (16 rows x one chunk) free of LDS bank
+//      conflicts.
+//   B: two contiguous 1 KiB tile16x64 fragments per 16-row strip.
+// When K/64 is odd the last stage holds one k-step; its second-half DMAs are
+// pointed at the first half (valid memory, never read).
 template <int MODE, int BM, int BN, int WM, int WN, bool PER_BLOCK, int NBUF>
 __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
-  constexpr int KS = 1;
+  constexpr int KS = 2;                                     // k-steps per stage
   constexpr int NW = WM * WN, NT = 64 * NW;                 // waves, threads
   constexpr int MI = BM / (16 * WM), NI = BN / (16 * WN);   // 16x16 tiles per wave
   static_assert(MI >= 1 && NI >= 1 && (MODE != MODE_GATE_UP || NI % 2 == 0), "tile shape");
-  constexpr int FA = (BM / 16) * KS, FB = (BN / 16) * KS;  // 1 KiB fragments per stage
-  constexpr int D = (FA + FB + NW - 1) / NW;                // fragment DMAs per wave per stage
+  constexpr int FA = BM / 8, FB = (BN / 16) * KS;           // 1 KiB DMAs per stage
+  constexpr int D = (FA + FB + NW - 1) / NW;                // DMAs per wave per stage
   constexpr int REM = (FA + FB) % NW;  // when nonzero, waves >= REM issue D - 1
   constexpr int A_STAGE = FA * 1024, B_STAGE = FB * 1024;
   // ring of NBUF LDS stages (NBUF-1 stages of DMA in flight)
   __shared__ __attribute__((aligned(16))) int8_t abuf_[NBUF][A_STAGE];
   __shared__ __attribute__((aligned(16))) int8_t bbuf_[NBUF][B_STAGE];
-  // per-block activation scales of the tile's rows, times 1/127
-  __shared__ float lds_sa[PER_BLOCK ? BM * kMaxBlocks : 1];
+  // per-block activation scales of the tile's rows, times 1/127 (dynamic
+  // LDS of BM * K/block floats, sized at launch)
+  extern __shared__ float lds_sa[];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -105,37 +117,61 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
     n0 = nt_in * BN;
     wbase = seg->w;
   } else {
-    if (!find_mtile(args.eo, args.E, BM, blockIdx.y, args.max_routes, e, r0, r1)) return;
+    // XCD-aware order: hardware places workgroup b on XCD b % 8, so XCD x
+    // takes the contiguous work range [x*G/8, (x+1)*G/8) of (m-tile major,
+    // n-tile minor) items.  The n-tiles sharing one gathered activation tile,
+    // and the consecutive m-tiles of one expert sharing its weight tiles, then
+    // meet in the same L2.
+    const int total = args.gm * args.gn, per_xcd = (int)gridDim.x >> 3;
+    int mt, nt;
+    if (args.order == 1) {
+      const int work = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+      if (work >= total) return;
+      mt = work / args.gn; nt = work % args.gn;
+    } else if (args.order == 2) {
+      // m-tile's n-tiles on one XCD, consecutive m-tiles on different XCDs
+      const int xcd = (int)(blockIdx.x & 7), k = (int)(blockIdx.x >> 3);
+      mt = xcd + 8 * (k / args.gn); nt = k % args.gn;
+      if (mt >= args.gm) return;
+    } else {
+      const int work = (int)blockIdx.x;
+      if (work >= total) return;
+      mt = work / args.gn; nt = work % args.gn;
+    }
+    if (!find_mtile(args.eo, args.E, BM, mt, args.max_routes, e, r0, r1)) return;
     K = args.K;
-    n0 = blockIdx.x * (MODE == MODE_GATE_UP ? BN / 2 : BN);
+    n0 = nt * (MODE == MODE_GATE_UP ? BN / 2 : BN);
     wbase = args.w + (size_t)e * args.N * K;
   }
   const int K64 = K >> 6;
   const int blk = MODE == MODE_DENSE ? args.lin.block : args.block;
   const int fpb = blk >> 6, nb = K / blk;
-  const int nstages = K64 / KS;  // launcher guarantees K64 % KS == 0
+  const int nstages = (K64 + 1) / 2;
+  const int tail = nstages - 1;  // the stage that may hold one k-step
+  const bool odd = K64 & 1;
 
-  // ---- this wave's fragment DMAs: fragment wave + NW*d, d < D (or D - 1)
+  // ---- this wave's DMAs: DMA wave + NW*d, d < D (or D - 1) ---------------
   const int8_t* src[D];
   int dst_off[D];
-  bool is_a[D];
+  bool is_a[D], hi[D];  // hi: reads the second k-step of the stage
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int f = min(wave + NW * d, FA + FB - 1);  // the clamped slot is never issued
     if (f < FA) {
-      const int ks = f / (BM / 16), msub = f % (BM / 16);
-      int row = r0 + msub * 16 + (lane & 15);
+      const int r = lane >> 3, c = (lane & 7) ^ r ^ (f & 1);  // this lane's row, chunk
+      int row = r0 + f * 8 + r;
       if (row >= r1) row = r0;  // rows past the tile end are never stored
       const int8_t* rp;
       if constexpr (MODE == MODE_DENSE) rp = args.lin.act + (size_t)row * K;
       else if constexpr (MODE == MODE_GATE_UP) rp = args.a + (size_t)args.routes[row].token * K;
       else rp = args.a + (size_t)row * K;
-      src[d] = rp + ks * 64 + (lane >> 4) * 16;
+      src[d] = rp + c * 16;
       dst_off[d] = f * 1024;
       is_a[d] = true;
+      hi[d] = c >= 4;
     } else {
       const int g = f - FA;
-      const int ks = g / (BN / 16), nsub = g % (BN / 16);
+      const int ks = g & 1, nsub = g >> 1;
       int wrow;
       bool ok;
       if constexpr (MODE == MODE_GATE_UP) {
@@ -153,6 +189,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
       src[d] = wbase + ((size_t)(wrow >> 4) * K64 + ks) * 1024 + lane * 16;
       dst_off[d] = g * 1024;
       is_a[d] = false;
+      hi[d] = ks == 1;
     }
   }
 
@@ -171,7 +208,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       if (d == D - 1 && !full_d) break;
-      const int8_t* g = src[d] + (is_a[d] ? (size_t)st * KS * 64 : (size_t)st * KS * 1024);
+      // stage st starts at K byte 128*st (A) / fragment 2*st (B); in a
+      // one-step tail stage the second-half reads fall back to the first half
+      const int back = (odd && st == tail && hi[d]) ? (is_a[d] ? 64 : 1024) : 0;
+      const int8_t* g = src[d] + (is_a[d] ? (size_t)st * 128 : (size_t)st * 2048) - back;
       const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr((is_a[d] ? abuf : bbuf) + dst_off[d]));
       // M0 holds the LDS destination; one wait state separates its write from
       // the DMA (the M0 -> LDS-DMA hazard).  These kernels use M0 for nothing
@@ -195,6 +235,33 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
     }
   }
 
+  // ---- epilogue operands, fetched now so their (dependent) loads are long
+  // done at the epilogue: per output row an activation scale (x 1/127) or a
+  // route weight, per output column the weight scale
+  float ep_row[MI][4], ep_col[NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      int row = r0 + (wm * MI + mi) * 16 + 4 * (lane >> 4) + v;
+      row = row < r1 ? row : r0;
+      if constexpr (MODE == MODE_DENSE) ep_row[mi][v] = PER_BLOCK ? 0.0f : args.lin.sa[row] * kInv127;
+      else if constexpr (MODE == MODE_GATE_UP) ep_row[mi][v] = args.a_scale[args.routes[row].token] * kInv127;
+      else ep_row[mi][v] = args.routes[row].weight;
+    }
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    if constexpr (MODE == MODE_GATE_UP) {
+      constexpr int hn = NI / 2;
+      const int col = min(n0 + (wn * hn + (ni % hn)) * 16 + (lane & 15), args.inter - 1);
+      ep_col[ni] = args.ws[(size_t)e * args.N + (ni < hn ? col : args.inter + col)];
+    } else if constexpr (MODE == MODE_DENSE) {
+      ep_col[ni] = seg->ws[min(n0 + bsub[ni] * 16 + (lane & 15), seg->n - 1)];
+    } else {
+      ep_col[ni] = args.ws[(size_t)e * args.N + min(n0 + bsub[ni] * 16 + (lane & 15), args.N - 1)];
+    }
+  }
+
   v4i acc[MI][NI];
   float facc[MI][NI][4];
 #pragma unroll
@@ -208,16 +275,29 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
 
   auto row_of = [&](int mi, int v) { return r0 + (wm * MI + mi) * 16 + 4 * (lane >> 4) + v; };
 
+  // LDS offset of this lane's A operand (row m = (wm*MI+mi)*16 + lane%16,
+  // chunk ks*4 + lane/16) under the block swizzle
+  int a_off[MI][KS];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int m = (wm * MI + mi) * 16 + (lane & 15);
+      const int b = m >> 3, r = m & 7, c = ks * 4 + (lane >> 4);
+      a_off[mi][ks] = b * 1024 + r * 128 + ((c ^ r ^ (b & 1)) * 16);
+    }
+
   auto compute = [&](const int8_t* abuf, const int8_t* bbuf, int st) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      if (ks == 1 && odd && st == tail) break;
       v4i a[MI], b[NI];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
-        a[mi] = *reinterpret_cast<const v4i*>(&abuf[(ks * (BM / 16) + wm * MI + mi) * 1024 + lane * 16]);
+        a[mi] = *reinterpret_cast<const v4i*>(&abuf[a_off[mi][ks]]);
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        b[ni] = *reinterpret_cast<const v4i*>(&bbuf[(ks * (BN / 16) + bsub[ni]) * 1024 + lane * 16]);
+        b[ni] = *reinterpret_cast<const v4i*>(&bbuf[(bsub[ni] * 2 + ks) * 1024 + lane * 16]);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -273,36 +353,34 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
       const int row = row_of(mi, v);
       if (row >= r1) continue;
       if constexpr (MODE == MODE_DENSE) {
-        const float ad = PER_BLOCK ? 0.0f : args.lin.sa[row] * kInv127;
+        const float ad = ep_row[mi][v];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + bsub[ni] * 16 + (lane & 15);
           if (col >= seg->n) continue;
-          const float y = PER_BLOCK ? facc[mi][ni][v] * seg->ws[col]
-                                    : (float)acc[mi][ni][v] * ad * seg->ws[col];
+          const float y = PER_BLOCK ? facc[mi][ni][v] * ep_col[ni]
+                                    : (float)acc[mi][ni][v] * ad * ep_col[ni];
           seg->out[(size_t)row * seg->n + col] = f32_to_bf16(y);
           if (seg->out_f32) seg->out_f32[(size_t)row * seg->n + col] = y;
         }
       } else if constexpr (MODE == MODE_GATE_UP) {
-        const float ad = args.a_scale[args.routes[row].token] * kInv127;
-        const float* ws = args.ws + (size_t)e * args.N;
+        const float ad = ep_row[mi][v];
         constexpr int hn = NI / 2;
 #pragma unroll
         for (int j = 0; j < hn; ++j) {
           const int col = n0 + (wn * hn + j) * 16 + (lane & 15);
           if (col >= args.inter) continue;
-          const float g = (float)acc[mi][j][v] * ad * ws[col];
-          const float u = (float)acc[mi][hn + j][v] * ad * ws[args.inter + col];
+          const float g = (float)acc[mi][j][v] * ad * ep_col[j];
+          const float u = (float)acc[mi][hn + j][v] * ad * ep_col[hn + j];
           args.bucket[(size_t)row * args.inter + col] = f32_to_bf16(gelu_tanh_f32(g) * u);
         }
       } else {
-        const float rw = args.routes[row].weight;
-        const float* ws = args.ws + (size_t)e * args.N;
+        const float rw = ep_row[mi][v];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + bsub[ni] * 16 + (lane & 15);
           if (col >= args.N) continue;
-          args.y[(size_t)row * args.N + col] = facc[mi][ni][v] * ws[col] * rw;
+          args.y[(size_t)row * args.N + col] = facc[mi][ni][v] * ep_col[ni] * rw;
         }
       }
     }
@@ -319,32 +397,63 @@ static int env_int(const char* name, int dflt) {
   return s ? atoi(s) : dflt;
 }
 
-template <int MODE, int BM, int BN, int WM, int WN, bool PB>
-static void launch_cfg(int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
-  const dim3 b(64 * WM * WN);
-  if (nbuf >= 6) hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 6>), g, b, 0, st, t);
-  else if (nbuf >= 4) hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 4>), g, b, 0, st, t);
-  else hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, 3>), g, b, 0, st, t);
+constexpr size_t kLdsBytes = 160 * 1024;
+
+template <int MODE, int BM, int BN, int WM, int WN, bool PB, int NBUF>
+static bool try_launch(dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
+  constexpr size_t ring = (size_t)NBUF * (BM + BN) * 128;  // 128 bytes of K per stage
+  if constexpr (ring > kLdsBytes) {
+    return false;  // never instantiated: the ring alone exceeds LDS
+  } else {
+    if (ring + dyn > kLdsBytes) return false;
+    hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, NBUF>), g, dim3(64 * WM * WN), dyn, st, t);
+    return true;
+  }
 }
 
-// 8 waves (2 x 4) per workgroup: two waves per SIMD keep the MFMA pipe and
-// the LDS reads overlapped (one wave per SIMD leaves every latency exposed).
+// NBUF-stage ring: the largest of {6, 4, 3, 2} stages (at most `nbuf`) that
+// fits in LDS next to the per-block scales.  The bytes in flight per CU
+// ((NBUF-1) stages) must cover the L2/HBM latency at the MFMA's pace.
+template <int MODE, int BM, int BN, int WM, int WN, bool PB>
+static void launch_cfg(int nbuf, dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
+  if (nbuf >= 6 && try_launch<MODE, BM, BN, WM, WN, PB, 6>(g, dyn, st, t)) return;
+  if (nbuf >= 4 && try_launch<MODE, BM, BN, WM, WN, PB, 4>(g, dyn, st, t)) return;
+  if (nbuf >= 3 && try_launch<MODE, BM, BN, WM, WN, PB, 3>(g, dyn, st, t)) return;
+  try_launch<MODE, BM, BN, WM, WN, PB, 2>(g, dyn, st, t);
+}
+
+// 8 waves (2 x 4) per workgroup for 128/256-wide tiles: each wave owns a
+// (BM/2) x (BN/4) block; two waves per SIMD keep MFMA and LDS reads
+// overlapped (one wave per SIMD leaves every latency exposed).
 template <int MODE, int BM, bool PB>
-static void launch_bn(int bn, int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
-  if (bn >= 128) launch_cfg<MODE, BM, 128, 2, 4, PB>(nbuf, g, st, t);
-  else launch_cfg<MODE, BM, 64, 2, 2, PB>(nbuf, g, st, t);
+static void launch_bn(int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
+  if (bn >= 256) launch_cfg<MODE, BM, 256, 2, 4, PB>(nbuf, g, dyn, st, t);
+  else launch_cfg<MODE, BM, 128, 2, 4, PB>(nbuf, g, dyn, st, t);
 }
 
 template <int MODE, bool PB>
-static void launch_bm(int bm, int bn, int nbuf, dim3 g, hipStream_t st, const TiledArgs& t) {
-  if (bm >= 128) launch_bn<MODE, 128, PB>(bn, nbuf, g, st, t);
-  else if (bm >= 64) launch_bn<MODE, 64, PB>(bn, nbuf, g, st, t);
-  else launch_bn<MODE, 32, PB>(bn, nbuf, g, st, t);
+static void launch_bm(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st,
+                      const TiledArgs& t) {
+  // 256-record m-tiles (MoE): 4 x 2 waves of 64 x 64, one tile per expert for
+  // up to 256 routes, so each expert's weights stream from HBM once
+  if (bm >= 256) {
+    // 256 x 256 (4 x 2 waves of 64 x 128) halves the operand traffic again;
+    // the per-block drains' f32 accumulators would not fit next to it
+    if constexpr (!PB) {
+      if (bn >= 256) { launch_cfg<MODE, 256, 256, 4, 2, PB>(nbuf, g, dyn, st, t); return; }
+    }
+    launch_cfg<MODE, 256, 128, 4, 2, PB>(nbuf, g, dyn, st, t);
+  }
+  else if (bm >= 128) launch_bn<MODE, 128, PB>(bn, nbuf, g, dyn, st, t);
+  else if (bm >= 64) launch_bn<MODE, 64, PB>(bn, nbuf, g, dyn, st, t);
+  else launch_bn<MODE, 32, PB>(bn, nbuf, g, dyn, st, t);
 }
 
+static inline int tile_bn(int bn) { return bn >= 256 ? 256 : 128; }
+
 hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStream_t st) {
-  const int bn = env_int("BQ_TILE_BN", 128);
-  const int nbuf = env_int("BQ_RING", 4);
+  const int bn = tile_bn(env_int("BQ_TILE_BN", 128));
+  const int nbuf = env_int("BQ_RING", 3);
   TiledArgs t{};
   t.lin = a;
   int gn = 0;
@@ -353,9 +462,15 @@ hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStrea
   t.gm = (a.M + bmv - 1) / bmv;
   t.gn = gn;
   dim3 g(t.gm * t.gn);
-  if (per_block) launch_bm<MODE_DENSE, true>(bm, bn, nbuf, g, st, t);
-  else launch_bm<MODE_DENSE, false>(bm, bn, nbuf, g, st, t);
+  const size_t dyn = per_block ? (size_t)bmv * (a.K / a.block) * sizeof(float) : 0;
+  if (per_block) launch_bm<MODE_DENSE, true>(bm, bn, nbuf, g, dyn, st, t);
+  else launch_bm<MODE_DENSE, false>(bm, bn, nbuf, g, dyn, st, t);
   return hipGetLastError();
+}
+
+static unsigned moe_grid(const TiledArgs& t) {
+  if (t.order == 2) return (unsigned)(8 * ((t.gm + 7) / 8) * t.gn);
+  return (unsigned)((t.gm * t.gn + 7) / 8 * 8);
 }
 
 static inline int mtile_bound(int max_routes, int experts, int bm) {
@@ -371,11 +486,17 @@ hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const
   t.a = x_i8; t.a_scale = x_sa; t.eo = eo; t.routes = routes; t.w = w_gu; t.ws = gu_scale;
   t.bucket = bucket; t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
   t.inter = inter; t.block = hidden;
-  const int bn = env_int("BQ_TILE_BN", 128);  // weight rows per tile: bn/2 gate + bn/2 up
-  const int nbuf = env_int("BQ_RING", 3);
-  const int bmv = bm >= 128 ? 128 : 64;
-  dim3 g((inter + bn / 2 - 1) / (bn / 2), mtile_bound(max_routes, experts, bmv));
-  launch_bm<MODE_GATE_UP, false>(bmv, bn, nbuf, g, st, t);
+  const int bmv = bm >= 256 ? 256 : bm >= 128 ? 128 : 64;
+  // weight rows per tile: bn/2 gate + bn/2 up.  256-record tiles pair with
+  // 256 weight rows: each expert's weights and each activation tile then
+  // stream the fewest times (measured best at 2048 tokens x 128 experts).
+  const int bn = tile_bn(env_int("BQ_TILE_BN", bmv == 256 ? 256 : 128));
+  const int nbuf = env_int("BQ_RING", 2);
+  t.gn = (inter + bn / 2 - 1) / (bn / 2);
+  t.gm = mtile_bound(max_routes, experts, bmv);
+  t.order = env_int("BQ_MOE_ORDER", 0);
+  const dim3 g(moe_grid(t));
+  launch_bm<MODE_GATE_UP, false>(bmv, bn, nbuf, g, 0, st, t);
   return hipGetLastError();
 }
 
@@ -387,11 +508,18 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
   t.a = b_i8; t.a_scale = b_sa; t.eo = eo; t.routes = routes; t.w = w_d; t.ws = d_scale; t.y = y;
   t.E = experts; t.max_routes = max_routes; t.N = hidden; t.K = inter; t.inter = inter;
   t.block = block;
-  const int bn = env_int("BQ_TILE_BN", 128);
-  const int nbuf = env_int("BQ_RING", 3);
-  const int bmv = bm >= 128 ? 128 : 64;
-  dim3 g((hidden + bn - 1) / bn, mtile_bound(max_routes, experts, bmv));
-  launch_bm<MODE_DOWN, true>(bmv, bn, nbuf, g, st, t);
+  // the down projection's K (= inter) is short, and its per-block drains
+  // keep f32 accumulators: 64-record tiles with a double-buffered stage run
+  // fastest (more workgroups in flight per CU)
+  const int bmv = bm >= 256 ? 256 : bm >= 128 ? 128 : 64;
+  const int bn = tile_bn(env_int("BQ_TILE_BN", 128));
+  const int nbuf = env_int("BQ_RING", 2);
+  t.gn = (hidden + bn - 1) / bn;
+  t.gm = mtile_bound(max_routes, experts, bmv);
+  t.order = env_int("BQ_MOE_ORDER", 0);
+  const dim3 g(moe_grid(t));
+  const size_t dyn = (size_t)bmv * (inter / block) * sizeof(float);
+  launch_bm<MODE_DOWN, true>(bmv, bn, nbuf, g, dyn, st, t);
   return hipGetLastError();
 }
 

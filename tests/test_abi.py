@@ -80,8 +80,8 @@ def test_empty_batches_are_noops(L):
 
 
 def test_workspace_size(L):
-    # per-route f32 results + per-token counters + per-token route lists
+    # per-route f32 down-projection rows
     T, k, H = 32, 8, 2816
     n = L.bq_moe_phase2_workspace_size(T, k, H)
-    assert n >= T * k * H * 4 + T * 4 + T * k * 4
+    assert n >= T * k * H * 4 and n % 256 == 0
     assert L.bq_moe_phase2_workspace_size(0, 8, H) == 0

@@ -124,6 +124,18 @@ def test_norm_quant(gpu, O, H, B):
     np.testing.assert_array_equal(host(q), rq)
 
 
+@pytest.mark.parametrize("H,B", [(2816, 128), (4096, 128), (2112, 64), (512, 16), (4096, 512),
+                                 (1024, 32), (768, 256), (1536, 512)])
+def test_norm_quant_long(gpu, O, H, B):
+    # seq_len >= 256 takes the one-wave-per-token kernel; 259 leaves a partial workgroup
+    x = O.synth_normal_bf16(11, 1.0, (259, H))
+    g = O.f32_to_bf16(O.synth_normal_f32(12, 0.3, (H,)) + 1.0)
+    q, sa = gpu.norm_quant(dev(x), dev(g), B)
+    rq, rsa = O.norm_quant(x, g, B)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(q), rq)
+
+
 def test_norm_quant_golden(gpu, G):
     q, sa = gpu.norm_quant(dev(G["nq_x"]), dev(G["nq_gamma"]), 128)
     np.testing.assert_array_equal(host(q), G["nq_codes"])
@@ -146,6 +158,19 @@ def test_block_quant(gpu, O, cols, B, fwht):
     x = O.synth_normal_bf16(2, 1.0, (37, cols))
     q, sa = gpu.block_quant(dev(x), B, fwht)
     rq, rsa = O.block_quant(x, B, fwht)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(q), rq)
+
+
+@pytest.mark.parametrize("B", [16, 32, 64, 128, 256, 512])
+@pytest.mark.parametrize("fwht", [True, False])
+def test_block_quant_blocks(gpu, O, B, fwht):
+    # every block size of the flat kernel; 3 rows x 1024 columns, plus zero blocks
+    x = O.synth_normal_bf16(5, 1.0, (3, 1024))
+    x[1, :B] = 0
+    q, sa = gpu.block_quant(dev(x), B, fwht)
+    rq, rsa = O.block_quant(x, B, fwht)
+    assert rsa.reshape(-1)[1024 // B] == 0.0
     np.testing.assert_array_equal(host(sa), rsa)
     np.testing.assert_array_equal(host(q), rq)
 

@@ -10,12 +10,14 @@ pytestmark = pytest.mark.gpu
 ONE = 0x3F80
 
 
+@pytest.mark.parametrize("bn", [64, 128, 256])
 @pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("M,K,B", [(200, 512, None), (77, 2816, None), (150, 1024, 256),
-                                   (96, 704, 64), (130, 2112, 64)])
-def test_dense_tiles(gpu, O, monkeypatch, bm, M, K, B):
+                                   (96, 704, 64), (130, 2112, 64), (40, 4096, 64)])
+def test_dense_tiles(gpu, O, monkeypatch, bm, bn, M, K, B):
     monkeypatch.setenv("BQ_TILE_BM", str(bm))
-    N = 384  # three 128-wide n-tiles; N=2816 tails are covered in test_gpu_parity
+    monkeypatch.setenv("BQ_TILE_BN", str(bn))
+    N = 384  # 1.5 n-tiles at bn=256; N=2816 tails are covered in test_gpu_parity
     wf = O.bf16_to_f32(O.synth_normal_bf16(3, 0.02, (N, K)))
     q, s = O.rotate_and_quant(wf, B or 128)
     W = gpu.ButterquantWeight(gpu.retile(dev(q.reshape(-1)), N, K), dev(s), N, K)
@@ -63,11 +65,17 @@ def _tiny_moe(O, gpu, T, E=4, k=2, H=128, I=64, seed=5):
                 T=T, E=E, k=k, H=H, I=I)
 
 
-@pytest.mark.parametrize("T,bm", [(64, None), (256, None), (64, 128), (256, 64), (256, 16),
-                                  (300, 128), (33, 64)])
-def test_moe_tiled(gpu, O, monkeypatch, T, bm):
+@pytest.mark.parametrize("T,bm,bn", [(64, None, None), (256, None, None), (64, 128, None),
+                                     (256, 64, None), (256, 16, None), (300, 128, None),
+                                     (33, 64, None), (256, 128, 128), (256, 64, 64),
+                                     (300, 128, 256), (300, 64, 256), (300, 256, None),
+                                     (64, 256, None), (600, 256, None), (600, 256, 256),
+                                     (300, 256, 256)])
+def test_moe_tiled(gpu, O, monkeypatch, T, bm, bn):
     if bm is not None:
         monkeypatch.setenv("BQ_MOE_BM", str(bm))
+    if bn is not None:
+        monkeypatch.setenv("BQ_TILE_BN", str(bn))
     c = _tiny_moe(O, gpu, T)
     E, H, I, k = c["E"], c["H"], c["I"], c["k"]
     eo, routes = gpu.build_schedule(dev(c["idx"]), dev(c["w"]), E)
