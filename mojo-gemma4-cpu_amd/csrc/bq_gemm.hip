@@ -38,7 +38,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
   int nt;
   const LinSeg& seg = pick_seg(args, blockIdx.x, nt);
   const int K = args.K, K64 = K >> 6, M = args.M;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fpb = args.block >> 6;  // fragments per K block (power of two)
   const int nb = K / args.block;
   int kt0, kt1;
@@ -52,16 +52,28 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
     kt0 = min(K64, wave * per);
     kt1 = min(K64, kt0 + per);
   }
-  // epilogue operands are fetched up front so their latency hides under the
-  // weight stream (thread t < 256 owns accumulator element t of the tile)
+  const int8_t* wb = seg.w + (size_t)nt * K64 * 1024 + lane * 16;
+  // the weight stream goes out first: a K slice of at most U fragments per
+  // wave (K <= 64*U*WAVES) is requested before anything else
+  v4i bf0[U];
+  const bool one_shot = kt1 - kt0 <= U;
+  if (one_shot) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      bf0[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const v4i*>(wb + (size_t)min(kt0 + u, max(kt1 - 1, 0)) * 1024));
+  }
+  // epilogue operands, fetched before the weights arrive (thread t < 256
+  // owns accumulator element t of the tile)
   const int t = threadIdx.x;
   const int ev = (t & 255) >> 6, eL = t & 63;
   const int ei = 4 * (eL >> 4) + ev;
   const int en = nt * 16 + (eL & 15);
   const bool eact = t < 256 && ei < M;
-  const float ews = eact ? seg.ws[en] : 0.0f;
-  const float ead = (eact && !PER_BLOCK) ? args.sa[ei] * kInv127 : 0.0f;
-  const int8_t* wb = seg.w + (size_t)nt * K64 * 1024 + lane * 16;
+  // unmasked loads (clamped index): a masked load would make the compiler
+  // wait for the whole weight stream at the branch join
+  const float ews = seg.ws[en];
+  const float ead = PER_BLOCK ? 0.0f : args.sa[min(ei, M - 1)] * kInv127;
   // rows >= M load row 0 instead: accumulator row i depends only on A row i
   // and rows >= M are never stored, so the loads need no mask (a branch
   // around them would force the compiler to wait for every outstanding load)
@@ -71,6 +83,40 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
   v4i c = zero;
 
   int kt = kt0;
+  if (one_shot) {
+    v4i af[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) af[u] = ld16(ab + min(kt0 + u, max(kt1 - 1, 0)) * 64);
+    if constexpr (!PER_BLOCK) {
+      // two independent accumulator chains (exact int32 sums, added at the end)
+      v4i c1 = zero;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kt0 + u < kt1) {
+          if (u & 1) c1 = mfma16x16x64(af[u], bf0[u], c1);
+          else c = mfma16x16x64(af[u], bf0[u], c);
+        }
+      }
+      c += c1;
+    } else {
+      // one chain, drained at block ends
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kt0 + u < kt1) {
+          c = mfma16x16x64(af[u], bf0[u], c);
+          if (((kt0 + u + 1) & (fpb - 1)) == 0) {
+            const int b = (kt0 + u) / fpb;
+            lds[b * 256 + 0 * 64 + lane] = c.x;
+            lds[b * 256 + 1 * 64 + lane] = c.y;
+            lds[b * 256 + 2 * 64 + lane] = c.z;
+            lds[b * 256 + 3 * 64 + lane] = c.w;
+            c = zero;
+          }
+        }
+      }
+    }
+    kt = kt1;
+  }
   for (; kt + U <= kt1; kt += U) {
     v4i bf[U], af[U];
 #pragma unroll
@@ -145,12 +191,22 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     // 8 waves split K so that each wave's whole slice (<= 8 fragments for
     // K <= 4096) is requested at once: the full weight is in flight within
     // the first memory latency.
-    constexpr int WAVES = 8;
+    const int waves = getenv("BQ_GEMV_WAVES") ? atoi(getenv("BQ_GEMV_WAVES")) : 8;
     const int nb = a.K / a.block;
-    const size_t lds = (size_t)(per_block ? nb : WAVES) * 256 * sizeof(int);
-    dim3 g(tiles), b(WAVES * 64);
-    if (per_block) hipLaunchKernelGGL((k_linear_skinny<WAVES, true, 8>), g, b, lds, st, a);
-    else hipLaunchKernelGGL((k_linear_skinny<WAVES, false, 8>), g, b, lds, st, a);
+    dim3 g(tiles);
+    if (waves >= 16) {
+      const size_t lds = (size_t)(per_block ? nb : 16) * 256 * sizeof(int);
+      if (per_block) hipLaunchKernelGGL((k_linear_skinny<16, true, 4>), g, dim3(1024), lds, st, a);
+      else hipLaunchKernelGGL((k_linear_skinny<16, false, 4>), g, dim3(1024), lds, st, a);
+    } else if (waves <= 4) {
+      const size_t lds = (size_t)(per_block ? nb : 4) * 256 * sizeof(int);
+      if (per_block) hipLaunchKernelGGL((k_linear_skinny<4, true, 16>), g, dim3(256), lds, st, a);
+      else hipLaunchKernelGGL((k_linear_skinny<4, false, 16>), g, dim3(256), lds, st, a);
+    } else {
+      const size_t lds = (size_t)(per_block ? nb : 8) * 256 * sizeof(int);
+      if (per_block) hipLaunchKernelGGL((k_linear_skinny<8, true, 8>), g, dim3(512), lds, st, a);
+      else hipLaunchKernelGGL((k_linear_skinny<8, false, 8>), g, dim3(512), lds, st, a);
+    }
     return hipGetLastError();
   }
   // prefer the largest M tile that still yields >= 256 workgroups (one per CU)

@@ -113,8 +113,14 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
   }
 }
 
-// Phase 1, 16-record m-tiles: blockIdx.y = m-tile, blockIdx.x = group of 4
-// intermediate 16-column subtiles (one per wave).
+// Skinny (16-record m-tile) kernels for decode-sized batches.  Each wave owns
+// one 16-column output subtile and streams its weight rows in chunks of U
+// k-steps through two register slots: chunk c+1's loads are in flight while
+// chunk c is multiplied.  Loads are never masked (indices are clamped, work
+// past K is skipped by a uniform test), and every epilogue operand is loaded
+// at kernel start.
+
+// Phase 1: blockIdx.y = m-tile, blockIdx.x = group of 4 intermediate subtiles.
 template <int U>
 __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
     const int8_t* __restrict__ x_i8, const float* __restrict__ x_sa,
@@ -123,7 +129,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
     uint16_t* __restrict__ bucket, int E, int hidden, int inter, int max_routes) {
   int e, r0, r1;
   if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;
-  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
   const int isub = blockIdx.x * 4 + wave;
   if (isub * 16 >= inter) return;
   const int K = hidden, K64 = K >> 6;
@@ -132,103 +138,134 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   const int8_t* wg = we + (size_t)isub * K64 * 1024 + lane * 16;
   const int8_t* wu = we + (size_t)((inter >> 4) + isub) * K64 * 1024 + lane * 16;
   const int arow = r0 + (lane & 15);
-  const bool aval = arow < r1;
-  const int8_t* ab = x_i8 + (size_t)routes[aval ? arow : r0].token * K + (lane >> 4) * 16;
-  const v4i zero = {0, 0, 0, 0};
-  v4i cg = zero, cu = zero;
-  int kt = 0;
-  for (; kt + U <= K64; kt += U) {
-    v4i bg[U], bu[U], af[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      bg[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wg + (size_t)(kt + u) * 1024));
-      bu[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)(kt + u) * 1024));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) af[u] = ld16(ab + (kt + u) * 64);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      cg = mfma16x16x64(af[u], bg[u], cg);
-      cu = mfma16x16x64(af[u], bu[u], cu);
-    }
-  }
-  for (; kt < K64; ++kt) {
-    const v4i bgf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wg + (size_t)kt * 1024));
-    const v4i buf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)kt * 1024));
-    const v4i af = ld16(ab + kt * 64);
-    cg = mfma16x16x64(af, bgf, cg);
-    cu = mfma16x16x64(af, buf, cu);
-  }
+  const int8_t* ab = x_i8 + (size_t)routes[arow < r1 ? arow : r0].token * K + (lane >> 4) * 16;
+  // epilogue operands
   const float* ws = gu_scale + (size_t)e * gate_up;
   const int col = isub * 16 + (lane & 15);
+  const float wsg = ws[col], wsu = ws[inter + col];
+  float ad[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int rec = r0 + 4 * (lane >> 4) + v;
+    ad[v] = x_sa[routes[rec < r1 ? rec : r0].token] * kInv127;
+  }
+  const v4i zero = {0, 0, 0, 0};
+  v4i cg = zero, cu = zero;
+  v4i bg[2][U], bu[2][U], af[2][U];
+  auto load = [&](int s, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = min(c * U + u, K64 - 1);
+      bg[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wg + (size_t)kt * 1024));
+      bu[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)kt * 1024));
+      af[s][u] = ld16(ab + kt * 64);
+    }
+  };
+  auto mul = [&](int s, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c * U + u < K64) {
+        cg = mfma16x16x64(af[s][u], bg[s][u], cg);
+        cu = mfma16x16x64(af[s][u], bu[s][u], cu);
+      }
+  };
+  const int nch = (K64 + U - 1) / U;
+  load(0, 0);
+  for (int c = 0; c < nch; c += 2) {
+    if (c + 1 < nch) load(1, c + 1);
+    mul(0, c);
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) load(0, c + 2);
+    mul(1, c + 1);
+  }
   const int g4[4] = {cg.x, cg.y, cg.z, cg.w};
   const int u4[4] = {cu.x, cu.y, cu.z, cu.w};
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int rec = r0 + 4 * (lane >> 4) + v;
     if (rec >= r1) continue;
-    const float ad = x_sa[routes[rec].token] * kInv127;
-    const float gv = (float)g4[v] * ad * ws[col];
-    const float uv = (float)u4[v] * ad * ws[inter + col];
+    const float gv = (float)g4[v] * ad[v] * wsg;
+    const float uv = (float)u4[v] * ad[v] * wsu;
     bucket[(size_t)rec * inter + col] = f32_to_bf16(gelu_tanh_f32(gv) * uv);
   }
 }
 
-// Phase 2 GEMM, 16-record m-tiles: y[rec, n] = (facc * ws[n]) * route_w[rec]
-// with facc the fma chain over K blocks (moe.mojo:198-223).
+// Phase 2 GEMM: y[rec, n] = (facc * ws[n]) * route_w[rec] with facc the fma
+// chain over K blocks (moe.mojo:198-223).  The m-tile's per-block activation
+// scales (16 records x K/block <= 64) are staged in LDS up front.
 template <int U>
 __global__ __launch_bounds__(256) void k_moe_down_skinny(
     const int8_t* __restrict__ b_i8, const float* __restrict__ b_sa,
     const int32_t* __restrict__ eo, const Route* __restrict__ routes,
     const int8_t* __restrict__ w_d, const float* __restrict__ d_scale, float* __restrict__ y,
     int E, int hidden, int inter, int block, int max_routes) {
+  __shared__ float s_sa[16 * 64];
   int e, r0, r1;
-  if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;
-  const int wave = threadIdx.x >> 6, lane = lane_id();
+  if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;  // whole workgroup
+  const int K = inter, K64 = K >> 6, fpb = block >> 6, nb = K / block;
+  for (int i = threadIdx.x; i < 16 * nb; i += blockDim.x) {
+    const int row = r0 + i / nb;
+    s_sa[i] = b_sa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
+  }
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
   const int nsub = blockIdx.x * 4 + wave;
   if (nsub * 16 >= hidden) return;
-  const int K = inter, K64 = K >> 6, fpb = block >> 6, nb = K / block;
   const int8_t* wb = w_d + (size_t)e * hidden * K + (size_t)nsub * K64 * 1024 + lane * 16;
   const int arow = r0 + (lane & 15);
-  const bool aval = arow < r1;
-  const int8_t* ab = b_i8 + (size_t)(aval ? arow : r0) * K + (lane >> 4) * 16;
-  const v4i zero = {0, 0, 0, 0};
-  float facc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  int rec4[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) rec4[v] = r0 + 4 * (lane >> 4) + v;
-  v4i c = zero;
-  for (int kt0 = 0; kt0 < K64; kt0 += U) {
-    v4i bf[U], af[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (kt0 + u < K64) {
-        bf[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)(kt0 + u) * 1024));
-        af[u] = ld16(ab + (kt0 + u) * 64);
-      }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kt = kt0 + u;
-      if (kt >= K64) break;
-      c = mfma16x16x64(af[u], bf[u], c);
-      if (((kt + 1) & (fpb - 1)) == 0) {
-        const int b = kt / fpb;
-        const int cc[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float adv = rec4[v] < r1 ? b_sa[(size_t)rec4[v] * nb + b] * kInv127 : 0.0f;
-          facc[v] = fmaf((float)cc[v], adv, facc[v]);
-        }
-        c = zero;
-      }
-    }
-  }
-  const float* ws = d_scale + (size_t)e * hidden;
+  const int8_t* ab = b_i8 + (size_t)(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
+  // epilogue operands and per-block scales
   const int col = nsub * 16 + (lane & 15);
+  const float wsc = d_scale[(size_t)e * hidden + col];
+  float rw[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    if (rec4[v] >= r1) continue;
-    y[(size_t)rec4[v] * hidden + col] = facc[v] * ws[col] * routes[rec4[v]].weight;
+    const int rec = r0 + 4 * (lane >> 4) + v;
+    rw[v] = routes[rec < r1 ? rec : r0].weight;
+  }
+  const v4i zero = {0, 0, 0, 0};
+  float facc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4i c = zero;
+  v4i bf[2][U], af[2][U];
+  auto load = [&](int s, int ch) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = min(ch * U + u, K64 - 1);
+      bf[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)kt * 1024));
+      af[s][u] = ld16(ab + kt * 64);
+    }
+  };
+  auto mul = [&](int s, int ch) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = ch * U + u;
+      if (kt < K64) {
+        c = mfma16x16x64(af[s][u], bf[s][u], c);
+        if (((kt + 1) & (fpb - 1)) == 0) {
+          const int b = kt / fpb;
+          const int cc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            facc[v] = fmaf((float)cc[v], s_sa[(4 * (lane >> 4) + v) * nb + b], facc[v]);
+          c = zero;
+        }
+      }
+    }
+  };
+  const int nch = (K64 + U - 1) / U;
+  load(0, 0);
+  for (int ch = 0; ch < nch; ch += 2) {
+    if (ch + 1 < nch) load(1, ch + 1);
+    mul(0, ch);
+    if (ch + 1 >= nch) break;
+    if (ch + 2 < nch) load(0, ch + 2);
+    mul(1, ch + 1);
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int rec = r0 + 4 * (lane >> 4) + v;
+    if (rec >= r1) continue;
+    y[(size_t)rec * hidden + col] = facc[v] * wsc * rw[v];
   }
 }
 
