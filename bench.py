@@ -137,22 +137,23 @@ def bench_prefill(bq, torch, steps, warmup, reps=32):
 
 
 class MoeLayer:
-    """One quantized MoE expert layer: norm-quant -> CSR schedule -> phase 1
-    (gate/up + GELU) -> FWHT64 block-quant -> phase 2 (down + route-weighted,
-    expert-ordered combine)."""
+    """One quantized MoE expert layer from router logits: top-8 + softmax
+    routing -> norm-quant -> CSR schedule -> phase 1 (gate/up + GELU) ->
+    FWHT64 block-quant -> phase 2 (down + route-weighted, expert-ordered
+    combine)."""
 
     def __init__(self, bq, torch, T, Wgu, Wd, gen_seed=1):
         self.bq, self.T = bq, T
         xg = torch.Generator(device="cuda").manual_seed(gen_seed)
         self.x = torch.randn(T, H, generator=xg, device="cuda").to(torch.bfloat16)
         lg = torch.Generator(device="cuda").manual_seed(2)
-        logits = torch.randn(T, E, generator=lg, device="cuda")
-        top, idx = torch.topk(logits, TOPK, dim=1)
-        self.idx = idx.to(torch.int32).contiguous()
-        self.w = torch.softmax(top, dim=1).contiguous()
+        self.logits = torch.randn(T, E, generator=lg, device="cuda")
+        self.pes = torch.ones(E, dtype=torch.bfloat16, device="cuda")  # per_expert_scale = 1
         self.gamma = torch.ones(H, dtype=torch.bfloat16, device="cuda")
         self.Wgu, self.Wd = Wgu, Wd
         d = "cuda"
+        self.idx = torch.empty(T, TOPK, dtype=torch.int32, device=d)
+        self.w = torch.empty(T, TOPK, dtype=torch.float32, device=d)
         self.xq = torch.empty(T, H, dtype=torch.int8, device=d)
         self.xsa = torch.empty(T, dtype=torch.float32, device=d)
         self.eo = torch.empty(E + 1, dtype=torch.int32, device=d)
@@ -167,6 +168,7 @@ class MoeLayer:
 
     def __call__(self, _i=0):
         bq, T = self.bq, self.T
+        bq.route_topk(self.logits, TOPK, self.pes, out=(self.idx, self.w))
         bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
         bq.build_schedule(self.idx, self.w, E, out=(self.eo, self.routes))
         bq.moe_phase1(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I, out=self.bucket)

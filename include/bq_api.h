@@ -134,6 +134,29 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
 
 /* ---- MoE ---------------------------------------------------------------- */
 
+/* RouterExpertKernel (kernels/moe_router.mojo:149-193, dispatch_router_expert
+ * :206-245; called at gemma_4_moe_bq.mojo:666-671)
+ * up to the candidate insert, for all experts:
+ * inv_rms = sqrt_n / sqrt(rms_reduce_row(x) + n_eps), scaled = (x *
+ * router_scale) * inv_rms, logits[t, e] = dot_to_scalar(scaled,
+ * router_proj[e]) in the reference's accumulator order (PU x 16 fma chains,
+ * pairwise tree, 16-lane halving reduce), f32 [seq_len, experts].
+ * x [seq_len, hidden], router_proj [experts, hidden], router_scale [hidden]
+ * bf16, 4-byte aligned; hidden % 64 == 0. */
+int bq_moe_router_logits(const uint16_t* x, const uint16_t* router_proj,
+                         const uint16_t* router_scale, float* logits, int seq_len, int hidden,
+                         int experts, float sqrt_n, float n_eps, void* stream);
+
+/* insert_candidate top-k (kernels/moe_router.mojo:43-57) + the softmax of
+ * RouterMergeKernel (:248-293; dispatch_merge_router_candidates, :333-389):
+ * per token the top_k experts by (logit descending, lower expert first on
+ * ties) among logits > -1e30, padded with {expert 0, logit -1e30};
+ * w = fast_exp_softmax_biased(logit - max) * (1/sum) * f32(scale[expert]).
+ * per_expert_scale: bf16 [experts], or NULL for scale 1.
+ * experts <= 1024, top_k <= 16. */
+int bq_moe_route_topk(const float* logits, const uint16_t* per_expert_scale, int seq_len,
+                      int experts, int top_k, int32_t* route_idx, float* route_w, void* stream);
+
 /* dispatch_build_expert_schedules (kernels/moe_router.mojo:60-145): routes
  * of experts [expert_base, expert_base+experts) into expert_offset[experts+1]
  * and routes[] sorted by (expert, token, k).  Each token's top_k experts must

@@ -41,6 +41,8 @@ SIGNATURES = {
     "bq_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "bq_block_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "bq_qkv": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_moe_router_logits": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
+    "bq_moe_route_topk": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_phase1_gate_up": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "bq_moe_phase2_workspace_size": [_i, _i, _i],
@@ -244,6 +246,40 @@ def qkv(x_i8, x_sa, q: ButterquantWeight, k: ButterquantWeight, v: ButterquantWe
 # --------------------------------------------------------------------------
 # MoE
 # --------------------------------------------------------------------------
+
+def router_logits(x: torch.Tensor, router_proj: torch.Tensor, router_scale: torch.Tensor,
+                  sqrt_n=None, n_eps=None, out=None):
+    """bf16 x [T,H], router_proj [E,H], router_scale [H] -> f32 logits [T,E]."""
+    _dev(x, torch.bfloat16)
+    _dev(router_proj, torch.bfloat16)
+    _dev(router_scale, torch.bfloat16)
+    t, h = x.shape
+    e = router_proj.shape[0]
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    if out is None:
+        out = torch.empty((t, e), dtype=torch.float32, device=x.device)
+    _check(_lib.bq_moe_router_logits(_p(x), _p(router_proj), _p(router_scale), _p(out), t, h, e,
+                                     sqrt_n, n_eps, _stream()))
+    return out
+
+
+def route_topk(logits: torch.Tensor, top_k: int, per_expert_scale: torch.Tensor | None = None,
+               out=None):
+    """f32 logits [T,E] -> (route_idx int32 [T,k], route_w f32 [T,k])."""
+    _dev(logits, torch.float32)
+    if per_expert_scale is not None:
+        _dev(per_expert_scale, torch.bfloat16)
+    t, e = logits.shape
+    if out is None:
+        idx = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+        w = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    else:
+        idx, w = out
+    _check(_lib.bq_moe_route_topk(_p(logits), _p(per_expert_scale), t, e, top_k, _p(idx), _p(w),
+                                  _stream()))
+    return idx, w
+
 
 def build_schedule(route_idx: torch.Tensor, route_w: torch.Tensor, experts: int,
                    expert_base: int = 0, out=None):

@@ -186,6 +186,35 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
   return check_hip(bq::launch_linear(a, 0, S(stream)), "qkv");
 }
 
+int bq_moe_router_logits(const uint16_t* x, const uint16_t* router_proj,
+                         const uint16_t* router_scale, float* logits, int seq_len, int hidden,
+                         int experts, float sqrt_n, float n_eps, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x || !router_proj || !router_scale || !logits)
+    return fail(BQ_ERR_INVALID, "bq_moe_router_logits: null pointer");
+  if (hidden <= 0 || hidden % 64 || experts <= 0)
+    return fail(BQ_ERR_SHAPE, "bq_moe_router_logits: need hidden %% 64 == 0 and experts > 0");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_proj) |
+       reinterpret_cast<uintptr_t>(router_scale)) & 3u)
+    return fail(BQ_ERR_INVALID, "bq_moe_router_logits: bf16 operands must be 4-byte aligned");
+  return check_hip(bq::launch_router_logits(x, router_proj, router_scale, logits, seq_len, hidden,
+                                            experts, sqrt_n, n_eps, S(stream)),
+                   "router_logits");
+}
+
+int bq_moe_route_topk(const float* logits, const uint16_t* per_expert_scale, int seq_len,
+                      int experts, int top_k, int32_t* route_idx, float* route_w, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!logits || !route_idx || !route_w) return fail(BQ_ERR_INVALID, "bq_moe_route_topk: null pointer");
+  if (experts <= 0 || top_k <= 0) return fail(BQ_ERR_SHAPE, "bq_moe_route_topk: bad top_k/experts");
+  if (experts > 1024 || top_k > 16)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_moe_route_topk: experts %d > 1024 or top_k %d > 16", experts,
+                top_k);
+  return check_hip(bq::launch_route_topk(logits, per_expert_scale, seq_len, experts, top_k,
+                                         route_idx, route_w, S(stream)),
+                   "route_topk");
+}
+
 int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
                           int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
                           void* stream) {

@@ -103,6 +103,26 @@ __device__ inline float gelu_tanh_f32(float x) {
   return 0.5f * x * (1.0f + t);
 }
 
+// simd_math/exponential.mojo:178-194, the router softmax's exp: a bit-level
+// 2^(x/ln2) with a quadratic mantissa correction.  The f32 -> i32 truncation
+// is the one of the x86 build the reference runs on: NaN and values outside
+// [-2^31, 2^31) give INT32_MIN (so x near -1e30 returns -0.0), where
+// v_cvt_i32_f32 alone would saturate positive values and map NaN to 0.
+__device__ inline float fast_exp_softmax_biased(float x) {
+  const float A_MAGIC = 12102203.16156148f;
+  const float BIAS_F = 1059208216.0f;
+  const float INV_TWO23 = 1.0f / (float)(1 << 23);
+  const float QC_A = 1.6501418352127075f;
+  const float QC_B = -0.37554836273193359f;
+  const float QC_C = 0.38696467876434326f;
+  const float v = A_MAGIC * x + BIAS_F;
+  const int32_t i = (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;
+  const uint32_t u = (uint32_t)i;
+  const float k = __uint_as_float(u);
+  const float f = (float)(u & 0x7FFFFFu) * INV_TWO23;
+  return k * (QC_A + f * (QC_B + f * QC_C));
+}
+
 // ---------------------------------------------------------------------------
 // wave helpers
 // ---------------------------------------------------------------------------
@@ -145,7 +165,6 @@ struct XlaneStage {
 // reference's stage loop, so the result is bit-identical to it.
 template <int R>
 __device__ inline void fwht_wave(float (&v)[R], int block) {
-  const int lane = lane_id();
   for (int s = 1; s < block && s < kWave; s <<= 1) {
     const XlaneStage x(s);
 #pragma unroll

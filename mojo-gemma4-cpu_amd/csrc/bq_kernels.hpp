@@ -59,6 +59,11 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
                                  int block, int bm, hipStream_t st);
 int moe_tile_bm(int max_routes, int experts);
 
+hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const uint16_t* rscale,
+                                float* logits, int T, int H, int E, float sqrt_n, float n_eps,
+                                hipStream_t st);
+hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,
+                             int32_t* route_idx, float* route_w, hipStream_t st);
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);

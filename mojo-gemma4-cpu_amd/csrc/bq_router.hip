@@ -1,0 +1,291 @@
+// bq_router.hip -- the MoE router ahead of the expert schedule
+// (kernels/moe_router.mojo:148-298): router logits, top-k with the
+// reference's candidate order, and the softmax merge.
+//
+// Logits (RouterExpertKernel, moe_router.mojo:164-187): every logit is an f32
+//   dot product whose rounding the reference fixes through its SIMD
+//   accumulator order, so each one is computed in exactly that order: chain
+//   c = p*16 + j (PU accumulators of 16 lanes) is an fma chain over elements
+//   i*PU*16 + c; lanes own adjacent chains, the chains of a logit are merged
+//   with cross-lane adds in the reference's tree order.  Vector fp32 (an MFMA
+//   would reassociate the sums).
+// Top-k + softmax (insert_candidate :43-57 and RouterMergeKernel :248-293):
+//   one wave per token.  insert_candidate keeps the k best candidates under
+//   a strict total order (logit descending, lower expert first on ties)
+//   among logits above the sentinel -1e30, padding with {expert 0, -1e30}.
+//   The wave takes k successive maxima of a 64-bit key that encodes that
+//   order, so the selected list is the reference's list entry for entry.
+#include "bq_device.hpp"
+#include "bq_kernels.hpp"
+
+namespace bq {
+
+constexpr float kRouterSentinel = -1.0e30f;
+
+// Sum of squares of a bf16 row in the order of rms_reduce_row (rmsnorm.mojo:
+// 16-17 -> dot_products.mojo:144-191): chain c = p*16 + j (p < pu) takes the
+// bf16 pairs c + i*pu*16, odd element first; s_j = sum_p chain(p, j) in p
+// order; then a 16-lane halving tree.  Wave-uniform result.
+__device__ inline float wave_row_ssq(const uint32_t* __restrict__ pairs, int hidden, int pu) {
+  const int lane = lane_id();
+  const int chains = pu * 16;
+  const int iters = hidden / (pu * 32);
+  const int c0 = min(lane, chains - 1), c1 = min(lane + 64, chains - 1);
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+  for (int i = 0; i < iters; ++i) {
+    const uint32_t p0 = pairs[i * chains + c0], p1 = pairs[i * chains + c1];
+    a0 = fmaf(__uint_as_float(p0 & 0xFFFF0000u), __uint_as_float(p0 & 0xFFFF0000u), a0);
+    a0 = fmaf(__uint_as_float(p0 << 16), __uint_as_float(p0 << 16), a0);
+    a1 = fmaf(__uint_as_float(p1 & 0xFFFF0000u), __uint_as_float(p1 & 0xFFFF0000u), a1);
+    a1 = fmaf(__uint_as_float(p1 << 16), __uint_as_float(p1 << 16), a1);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int c = p * 16 + (lane & 15);
+    const float v0 = __shfl(a0, c & 63, kWave);
+    const float v1 = __shfl(a1, c & 63, kWave);
+    if (p < pu) sum = sum + (c < 64 ? v0 : v1);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sum = sum + __shfl_down(sum, 8 >> q, 16);
+  return __shfl(sum, 0, kWave);
+}
+
+// A workgroup computes TT tokens x (4 waves x EE experts).  Lane l owns the
+// CPL adjacent chains c = l*CPL + r of the PU = CPL*4 accumulator bank
+// (64*CPL chains); per step i it scales its TT x values on the fly
+// ((x * router_scale) * inv_rms, :177-181) and runs TT*EE*CPL fma chains.
+template <int TT, int EE, int CPL>
+__global__ __launch_bounds__(256) void k_router_logits(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ proj,
+    const uint16_t* __restrict__ rscale, float* __restrict__ logits, int T, int H, int E,
+    int pu_bf16, float sqrt_n, float n_eps) {
+  __shared__ float s_inv[TT];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int t0 = blockIdx.x * TT, e0 = (blockIdx.y * 4 + wave) * EE;
+  for (int tt = wave; tt < TT; tt += 4) {
+    const int t = min(t0 + tt, T - 1);
+    const float ssq =
+        wave_row_ssq(reinterpret_cast<const uint32_t*>(x + (size_t)t * H), H, pu_bf16);
+    if (lane == 0) s_inv[tt] = sqrt_n / __builtin_sqrtf(ssq + n_eps);
+  }
+  __syncthreads();
+  float inv[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) inv[tt] = s_inv[tt];
+
+  const uint16_t* xr[TT];
+  const uint16_t* wr[EE];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) xr[tt] = x + (size_t)min(t0 + tt, T - 1) * H;
+#pragma unroll
+  for (int ee = 0; ee < EE; ++ee) wr[ee] = proj + (size_t)min(e0 + ee, E - 1) * H;
+
+  constexpr int C = 64 * CPL;  // chains = PU*16 elements per step
+  float acc[TT][EE][CPL];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int ee = 0; ee < EE; ++ee)
+#pragma unroll
+      for (int r = 0; r < CPL; ++r) acc[tt][ee][r] = 0.0f;
+
+  const int iters = H / C;
+  for (int i = 0; i < iters; ++i) {
+    const int off = i * C + lane * CPL;
+    float sv[CPL], xs[TT][CPL], wv[EE][CPL];
+    if constexpr (CPL == 2) {
+      const uint32_t s2 = *reinterpret_cast<const uint32_t*>(rscale + off);
+      sv[0] = __uint_as_float(s2 << 16);
+      sv[1] = __uint_as_float(s2 & 0xFFFF0000u);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(xr[tt] + off);
+        xs[tt][0] = __uint_as_float(v << 16);
+        xs[tt][1] = __uint_as_float(v & 0xFFFF0000u);
+      }
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(wr[ee] + off);
+        wv[ee][0] = __uint_as_float(v << 16);
+        wv[ee][1] = __uint_as_float(v & 0xFFFF0000u);
+      }
+    } else {
+      sv[0] = bf16_to_f32(rscale[off]);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) xs[tt][0] = bf16_to_f32(xr[tt][off]);
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee) wv[ee][0] = bf16_to_f32(wr[ee][off]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int r = 0; r < CPL; ++r) xs[tt][r] = xs[tt][r] * sv[r] * inv[tt];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int ee = 0; ee < EE; ++ee)
+#pragma unroll
+        for (int r = 0; r < CPL; ++r) acc[tt][ee][r] = fmaf(xs[tt][r], wv[ee][r], acc[tt][ee][r]);
+  }
+
+  // chain c = l*CPL + r is (p, j) = (c >> 4, c & 15).  tree_merge_accs
+  // (simd_math/matrixops.mojo:265-283): acc[p] += acc[p + s] for s = 1, 2,
+  // 4 -> partner lane + s*16/CPL; then the 16-lane halving reduce_add: lane
+  // + h/CPL for h >= CPL, in-lane r + 1 for h = 1 < CPL.  Lane 0, r = 0 ends
+  // with the logit; lane tt*EE + ee stores it.
+  constexpr int PU = 4 * CPL;
+  float mine = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int ee = 0; ee < EE; ++ee) {
+      float v[CPL];
+#pragma unroll
+      for (int r = 0; r < CPL; ++r) v[r] = acc[tt][ee][r];
+#pragma unroll
+      for (int q = 0; (1 << q) < PU; ++q)
+#pragma unroll
+        for (int r = 0; r < CPL; ++r) v[r] = v[r] + __shfl_down(v[r], (16 << q) / CPL, kWave);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int h = 8 >> q;
+        if (h >= CPL) {
+#pragma unroll
+          for (int r = 0; r < CPL; ++r) v[r] = v[r] + __shfl_down(v[r], h / CPL, kWave);
+        } else if constexpr (CPL == 2) {
+          v[0] = v[0] + v[1];
+        }
+      }
+      const float total = __shfl(v[0], 0, kWave);
+      if (lane == tt * EE + ee) mine = total;
+    }
+  static_assert(TT * EE <= 64, "one logit per lane");
+  const int tt = lane / EE, ee = lane % EE;
+  if (lane < TT * EE && t0 + tt < T && e0 + ee < E) logits[(size_t)(t0 + tt) * E + e0 + ee] = mine;
+}
+
+// 64-bit key ordering candidates like insert_candidate: high word = the
+// logit mapped to an unsigned order (-0.0 taken as +0.0, since the reference
+// compares floats), low word = (1023 - expert) << 1 so lower experts win
+// ties, plus bit 0 remembering a -0.0 logit.  Candidates at or below the
+// sentinel (and NaN) get key 0 and are never selected.
+__device__ inline uint64_t cand_key(float lg, int e) {
+  const uint32_t b = __float_as_uint(lg);
+  const uint32_t negzero = (b == 0x80000000u) ? 1u : 0u;
+  const uint32_t cb = negzero ? 0u : b;
+  const uint32_t ord = (cb & 0x80000000u) ? ~cb : (cb | 0x80000000u);
+  return ((uint64_t)ord << 32) | ((uint32_t)(1023 - e) << 1) | negzero;
+}
+
+__device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int NE>
+__global__ __launch_bounds__(256) void k_route_topk(
+    const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
+    int32_t* __restrict__ route_idx, float* __restrict__ route_w) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;  // whole waves; no block synchronization below
+  const float* row = logits + (size_t)t * E;
+  uint64_t key[NE];
+#pragma unroll
+  for (int q = 0; q < NE; ++q) {
+    const int e = lane + 64 * q;
+    const float lg = row[min(e, E - 1)];
+    key[q] = (e < E && lg > kRouterSentinel) ? cand_key(lg, e) : 0ull;
+  }
+  uint64_t local = key[0];
+#pragma unroll
+  for (int q = 1; q < NE; ++q) local = umax64(local, key[q]);
+
+  float mx = 0.0f, sum = 0.0f, my_ev = 0.0f;
+  int my_e = 0;
+  for (int k = 0; k < top_k; ++k) {
+    uint64_t best = local;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t lo = __shfl_xor((uint32_t)best, o, kWave);
+      const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), o, kWave);
+      best = umax64(best, ((uint64_t)hi << 32) | lo);
+    }
+    float lg = kRouterSentinel;
+    int e = 0;
+    if (best != 0ull) {
+      const uint32_t hi = (uint32_t)(best >> 32), lo = (uint32_t)best;
+      e = 1023 - (int)(lo >> 1);
+      const uint32_t b = (hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi;
+      lg = __uint_as_float((lo & 1u) ? 0x80000000u : b);
+#pragma unroll
+      for (int q = 0; q < NE; ++q) key[q] = key[q] == best ? 0ull : key[q];
+      local = key[0];
+#pragma unroll
+      for (int q = 1; q < NE; ++q) local = umax64(local, key[q]);
+    }
+    // RouterMergeKernel (:276-293): max = merged[0].logit, exp of the
+    // difference, sum in slot order
+    if (k == 0) mx = lg;
+    const float ev = fast_exp_softmax_biased(lg - mx);
+    sum = sum + ev;
+    if (lane == k) {
+      my_ev = ev;
+      my_e = e;
+    }
+  }
+  const float inv_sum = 1.0f / sum;
+  if (lane < top_k) {
+    const float sc = pes ? bf16_to_f32(pes[my_e]) : 1.0f;
+    route_idx[(size_t)t * top_k + lane] = my_e;
+    route_w[(size_t)t * top_k + lane] = my_ev * inv_sum * sc;
+  }
+}
+
+static int pick_port_unroll(int width, int cols) {
+  if (cols % (8 * width) == 0) return 8;
+  if (cols % (4 * width) == 0) return 4;
+  if (cols % (2 * width) == 0) return 2;
+  return 1;
+}
+
+template <int TT, int EE>
+static hipError_t launch_logits_tile(const uint16_t* x, const uint16_t* proj,
+                                     const uint16_t* rscale, float* logits, int T, int H, int E,
+                                     float sqrt_n, float n_eps, hipStream_t st) {
+  const dim3 grid((T + TT - 1) / TT, (E + 4 * EE - 1) / (4 * EE));
+  const int pu_bf16 = pick_port_unroll(32, H);
+  if (pick_port_unroll(16, H) == 8)
+    hipLaunchKernelGGL((k_router_logits<TT, EE, 2>), grid, dim3(256), 0, st, x, proj, rscale,
+                       logits, T, H, E, pu_bf16, sqrt_n, n_eps);
+  else
+    hipLaunchKernelGGL((k_router_logits<TT, EE, 1>), grid, dim3(256), 0, st, x, proj, rscale,
+                       logits, T, H, E, pu_bf16, sqrt_n, n_eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const uint16_t* rscale,
+                                float* logits, int T, int H, int E, float sqrt_n, float n_eps,
+                                hipStream_t st) {
+  if (T >= 256) return launch_logits_tile<8, 8>(x, proj, rscale, logits, T, H, E, sqrt_n, n_eps, st);
+  return launch_logits_tile<2, 4>(x, proj, rscale, logits, T, H, E, sqrt_n, n_eps, st);
+}
+
+hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,
+                             int32_t* route_idx, float* route_w, hipStream_t st) {
+  const dim3 grid((T + 3) / 4), block(256);
+  const int ne = (E + 63) / 64;
+  if (ne <= 1)
+    hipLaunchKernelGGL(k_route_topk<1>, grid, block, 0, st, logits, pes, T, E, top_k, route_idx, route_w);
+  else if (ne <= 2)
+    hipLaunchKernelGGL(k_route_topk<2>, grid, block, 0, st, logits, pes, T, E, top_k, route_idx, route_w);
+  else if (ne <= 4)
+    hipLaunchKernelGGL(k_route_topk<4>, grid, block, 0, st, logits, pes, T, E, top_k, route_idx, route_w);
+  else if (ne <= 8)
+    hipLaunchKernelGGL(k_route_topk<8>, grid, block, 0, st, logits, pes, T, E, top_k, route_idx, route_w);
+  else
+    hipLaunchKernelGGL(k_route_topk<16>, grid, block, 0, st, logits, pes, T, E, top_k, route_idx, route_w);
+  return hipGetLastError();
+}
+
+}  // namespace bq

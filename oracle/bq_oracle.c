@@ -417,21 +417,74 @@ float bqo_fast_exp_softmax_biased(float x) {
     const float QC_A = 1.6501418352127075f;
     const float QC_B = -0.37554836273193359f;
     const float QC_C = 0.38696467876434326f;
-    int32_t i = (int32_t)(A_MAGIC * x + BIAS_F);
+    float v = A_MAGIC * x + BIAS_F;
+    /* the f32 -> i32 truncation of the x86 build the reference runs on
+     * (cvttps2dq): NaN and values outside [-2^31, 2^31) give INT32_MIN, so
+     * a sentinel candidate's x near -1e30 yields -0.0 */
+    int32_t i = (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;
     uint32_t u = (uint32_t)i;
     float k = u2f(u);
     float f = (float)(u & 0x7FFFFFu) * INV_TWO23;
     return k * (QC_A + f * (QC_B + f * QC_C));
 }
 
-/* moe_router.mojo:43-57 insert_candidate + :276-293 softmax merge */
+/* dot_to_scalar[cols](x f32, w bf16) (dot_products.mojo:195-205): PU =
+ * pick_port_unroll(W=16, cols) accumulators of 16 f32 lanes; accumulator p
+ * lane j is an fma chain over elements i*PU*16 + p*16 + j, i ascending
+ * (dot_f32_bf16_into_accs, :162-178); then tree_merge_accs (pairwise:
+ * acc[i] += acc[i+stride] for stride 1, 2, 4; simd_math/matrixops.mojo:265-
+ * 283) and a 16-lane halving-tree reduce_add. */
+static float dot_f32_bf16(const float* x, const uint16_t* w, int cols) {
+    enum { W = 16 };
+    int pu = pick_port_unroll(W, cols);
+    float acc[8][W];
+    memset(acc, 0, sizeof(acc));
+    for (int i = 0; i < cols / (pu * W); ++i)
+        for (int p = 0; p < pu; ++p)
+            for (int j = 0; j < W; ++j) {
+                size_t off = (size_t)i * pu * W + (size_t)p * W + j;
+                acc[p][j] = fmaf(x[off], bqo_bf16_to_f32(w[off]), acc[p][j]);
+            }
+    for (int stride = 1; stride < pu; stride *= 2)
+        for (int i = 0; i < pu; i += 2 * stride)
+            for (int j = 0; j < W; ++j) acc[i][j] = acc[i][j] + acc[i + stride][j];
+    for (int half = W / 2; half >= 1; half /= 2)
+        for (int j = 0; j < half; ++j) acc[0][j] = acc[0][j] + acc[0][j + half];
+    return acc[0][0];
+}
+
+/* RouterExpertKernel.execute (kernels/moe_router.mojo:164-187) up to the
+ * candidate insert: inv_rms = sqrt_n / sqrt(rms_reduce_row(x) + n_eps);
+ * scaled[j] = (x[j] * router_scale[j]) * inv_rms; logit[e] =
+ * dot_to_scalar(scaled, router_proj[e]).  logits [T, E] f32. */
+void bqo_router_logits(const uint16_t* x, const uint16_t* router_proj,
+                       const uint16_t* router_scale, int T, int H, int E, float sqrt_n,
+                       float n_eps, float* logits) {
+    float* scaled = (float*)malloc(sizeof(float) * H);
+    for (int t = 0; t < T; ++t) {
+        const uint16_t* xr = x + (size_t)t * H;
+        float inv_rms = sqrt_n / sqrtf(bqo_rms_reduce_row(xr, H) + n_eps);
+        for (int j = 0; j < H; ++j)
+            scaled[j] = bqo_bf16_to_f32(xr[j]) * bqo_bf16_to_f32(router_scale[j]) * inv_rms;
+        for (int e = 0; e < E; ++e)
+            logits[(size_t)t * E + e] = dot_f32_bf16(scaled, router_proj + (size_t)e * H, H);
+    }
+    free(scaled);
+}
+
+/* kernels/moe_router.mojo:43-57 insert_candidate (candidates start as the
+ * sentinel {expert 0, logit -1e30}; a logit enters at the first slot it beats,
+ * ties going to the lower expert) + :276-293 the merge's softmax over the k:
+ * ev = fast_exp_softmax_biased(logit - max), sum in slot order, w = ev *
+ * (1/sum) * f32(per_expert_scale[expert]) (scale 1 when NULL). */
 void bqo_route_topk_softmax(const float* logits, int T, int E, int top_k,
-                            int32_t* route_idx, float* route_w) {
+                            const uint16_t* per_expert_scale, int32_t* route_idx,
+                            float* route_w) {
     int32_t* ce = (int32_t*)malloc(sizeof(int32_t) * top_k);
     float* cl = (float*)malloc(sizeof(float) * top_k);
     float* ev = (float*)malloc(sizeof(float) * top_k);
     for (int t = 0; t < T; ++t) {
-        for (int k = 0; k < top_k; ++k) { ce[k] = -1; cl[k] = -INFINITY; }
+        for (int k = 0; k < top_k; ++k) { ce[k] = 0; cl[k] = -1.0e30f; }
         const float* row = logits + (size_t)t * E;
         for (int e = 0; e < E; ++e) {
             float lg = row[e];
@@ -447,8 +500,9 @@ void bqo_route_topk_softmax(const float* logits, int T, int E, int top_k,
         for (int k = 0; k < top_k; ++k) { ev[k] = bqo_fast_exp_softmax_biased(cl[k] - mx); sum += ev[k]; }
         float inv_sum = 1.0f / sum;
         for (int k = 0; k < top_k; ++k) {
+            const float sc = per_expert_scale ? bqo_bf16_to_f32(per_expert_scale[ce[k]]) : 1.0f;
             route_idx[(size_t)t * top_k + k] = ce[k];
-            route_w[(size_t)t * top_k + k] = ev[k] * inv_sum * 1.0f;
+            route_w[(size_t)t * top_k + k] = ev[k] * inv_sum * sc;
         }
     }
     free(ce); free(cl); free(ev);

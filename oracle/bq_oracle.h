@@ -95,8 +95,12 @@ float bqo_gelu_tanh_f32(float x);                /* simd_math/ops.mojo:145-156 *
 float bqo_fast_exp_softmax_biased(float x);      /* simd_math/exponential.mojo:178-194 */
 /* top-k (ties -> lower expert, moe_router.mojo:43-57) + softmax over the k
  * (moe_router.mojo:276-293) with per_expert_scale = 1. logits [T,E]. */
+void bqo_router_logits(const uint16_t* x, const uint16_t* router_proj,
+                       const uint16_t* router_scale, int T, int H, int E, float sqrt_n,
+                       float n_eps, float* logits);   /* moe_router.mojo:164-187 */
 void bqo_route_topk_softmax(const float* logits, int T, int E, int top_k,
-                            int32_t* route_idx, float* route_w);
+                            const uint16_t* per_expert_scale, int32_t* route_idx,
+                            float* route_w);
 /* kernels/moe_router.mojo:60-106 (experts [0,E)) */
 void bqo_build_schedule(const int32_t* route_idx, const float* route_w, int T,
                         int top_k, int E, int32_t* expert_offset,

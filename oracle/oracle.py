@@ -301,13 +301,36 @@ def exp_fast(x):
     return np.array([f(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))
 
 
-def route_topk_softmax(logits: np.ndarray, top_k: int = 8):
-    """Top-k (moe_router.mojo:43-57) + softmax over the k (:276-293)."""
+def router_logits(x_bf16: np.ndarray, router_proj_bf16: np.ndarray, router_scale_bf16: np.ndarray,
+                  sqrt_n=None, n_eps=None) -> np.ndarray:
+    """RouterExpertKernel up to the candidate insert (kernels/moe_router.mojo:
+    164-187): bf16 x [T,H], router_proj [E,H], router_scale [H] -> f32 [T,E]."""
+    x = _c(x_bf16, np.uint16)
+    rp = _c(router_proj_bf16, np.uint16)
+    rs = _c(router_scale_bf16, np.uint16)
+    T, H = x.shape
+    E = rp.shape[0]
+    assert rp.shape == (E, H) and rs.shape == (H,)
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(H)
+    out = np.empty((T, E), np.float32)
+    f = lib().bqo_router_logits
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float,
+                  C.c_float, C.c_void_p]
+    f(_p(x), _p(rp), _p(rs), T, H, E, sqrt_n, n_eps, _p(out))
+    return out
+
+
+def route_topk_softmax(logits: np.ndarray, top_k: int = 8, per_expert_scale=None):
+    """Top-k (moe_router.mojo:43-57) + softmax over the k (:276-293); optional
+    bf16 [E] per-expert scale."""
     lg = _c(logits, np.float32)
     T, E = lg.shape
     idx = np.empty((T, top_k), np.int32)
     w = np.empty((T, top_k), np.float32)
-    lib().bqo_route_topk_softmax(_p(lg), T, E, top_k, _p(idx), _p(w))
+    sc = None if per_expert_scale is None else _c(per_expert_scale, np.uint16)
+    lib().bqo_route_topk_softmax(_p(lg), T, E, top_k, _p(sc) if sc is not None else None,
+                                 _p(idx), _p(w))
     return idx, w
 
 

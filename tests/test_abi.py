@@ -63,6 +63,14 @@ def test_validation_errors(L):
     assert L.bq_norm_quant(P, P, P, P, 1, 2880, 128, C.c_float(1), C.c_float(1), None) == 2
     assert L.bq_block_quant(P, P, P, 704, 1, 256, 0, None) == 2
     assert L.bq_moe_build_schedule(P, P, 4, 8, 0, 512, P, P, None) == 4
+    assert L.bq_moe_route_topk(P, None, 4, 128, 17, P, P, None) == 4
+    assert L.bq_moe_route_topk(P, None, 4, 2048, 8, P, P, None) == 4
+    assert L.bq_moe_route_topk(P, None, 4, 128, 0, P, P, None) == 2
+    assert L.bq_moe_route_topk(None, None, 4, 128, 8, P, P, None) == 1
+    assert L.bq_moe_router_logits(P, P, P, P, 4, 2880 + 32, 128, C.c_float(1), C.c_float(1),
+                                  None) == 2
+    assert L.bq_moe_router_logits(P, C.c_void_p(18), P, P, 4, 2816, 128, C.c_float(1),
+                                  C.c_float(1), None) == 1
     assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
                                 C.c_void_p(256), 0, None) == 2
     assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
@@ -75,6 +83,9 @@ def test_empty_batches_are_noops(L):
     assert L.bq_block_linear(None, None, None, None, None, None, 64, 256, 0, 64, None) == 0
     assert L.bq_norm_quant(None, None, None, None, 0, 2816, 128, C.c_float(1), C.c_float(1), None) == 0
     assert L.bq_block_quant(None, None, None, 704, -1, 64, 1, None) == 0
+    assert L.bq_moe_route_topk(None, None, 0, 128, 8, None, None, None) == 0
+    assert L.bq_moe_router_logits(None, None, None, None, 0, 2816, 128, C.c_float(1),
+                                  C.c_float(1), None) == 0
     assert L.bq_moe_phase2_down(None, None, None, None, None, None, None, None, 128, 0, 8, 2816,
                                 704, 64, None, 0, None) == 0
 

@@ -92,3 +92,22 @@ def test_moe_tiled(gpu, O, monkeypatch, T, bm, bn):
     np.testing.assert_array_equal(host(accum), racc)
     np.testing.assert_array_equal(host(out), rout)
     tol_check(host(accum), racc)
+
+
+def test_moe_gate_up_hidden2816(gpu, O):
+    # model hidden size (K/64 = 44) with 128-165 routes per expert: 256-record
+    # tiles with partial m-tiles and a partial gate/up n-tile (inter 192)
+    T, E, k, H, I = 600, 8, 2, 2816, 192
+    logits = O.synth_normal_f32(21, 1.0, (T, E))
+    idx, w = O.route_topk_softmax(logits, k)
+    gu = O.bf16_to_f32(O.synth_normal_bf16(22, 0.02, (E * 2 * I, H)))
+    gq, gs = O.rotate_and_quant(gu, 128)
+    x = O.synth_normal_bf16(23, 1.0, (T, H))
+    xq, xsa = O.norm_quant(x, np.full(H, ONE, np.uint16), 128)
+    Wgu = gpu.ButterquantWeight(gpu.retile(dev(gq.reshape(-1)), E * 2 * I, H), dev(gs), E * 2 * I, H)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    bucket = gpu.moe_phase1(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    gp, gcs = O.pack_and_colsum(gq)
+    rb = O.moe_phase1(xq, xsa, reo, rroutes, gp, gs, gcs, I)
+    np.testing.assert_array_equal(host(bucket), rb)

@@ -265,6 +265,76 @@ def test_route_topk_softmax(O):
     assert idx[0, 0] == 5 and idx[0, 1] == 9
     np.testing.assert_allclose(w.sum(1), 1.0, rtol=2e-6)
     assert (np.diff(w, axis=1) <= 1e-7).all()
+    # the weights are a softmax over the k selected logits (not over all E):
+    # fast_exp_softmax_biased is within 1% of exp, so within ~2% normalized
+    top = np.take_along_axis(logits, idx, 1).astype(np.float64)
+    sm = np.exp(top - top[:, :1])
+    sm /= sm.sum(1, keepdims=True)
+    assert (np.abs(w / sm - 1) < 2.5e-2).all()
+
+
+def test_route_scale_and_sentinels(O):
+    lib = O.lib()
+    # out-of-range exponent inputs follow the x86 truncation (INT32_MIN -> -0.0)
+    for v in (-1e30, -1e20, float("nan"), float("-inf")):
+        r = lib.bqo_fast_exp_softmax_biased(v)
+        assert r == 0.0 and math.copysign(1.0, r) < 0
+    assert lib.bqo_fast_exp_softmax_biased(0.0) == pytest.approx(1.0, rel=1e-2)
+    # per-expert scale multiplies the normalized weight once, in f32
+    logits = O.synth_normal_f32(3, 1.0, (16, 32))
+    scale = O.f32_to_bf16(1.0 + 0.5 * O.synth_normal_f32(4, 1.0, (32,)))
+    idx, w = O.route_topk_softmax(logits, 4)
+    idx_s, w_s = O.route_topk_softmax(logits, 4, per_expert_scale=scale)
+    np.testing.assert_array_equal(idx_s, idx)
+    np.testing.assert_array_equal(w_s, (w * O.bf16_to_f32(scale)[idx]).astype(np.float32))
+    # fewer experts than k: the list is padded with {expert 0, -1e30}, whose
+    # weight is -0.0
+    idx3, w3 = O.route_topk_softmax(np.array([[0.5, 2.0, -1.0]], np.float32), 8)
+    np.testing.assert_array_equal(idx3[0], [1, 0, 2, 0, 0, 0, 0, 0])
+    assert (w3[0, 3:] == 0).all() and np.signbit(w3[0, 3:]).all()
+    np.testing.assert_allclose(w3[0, :3].sum(), 1.0, rtol=1e-6)
+    # logits at or below the sentinel, -inf and NaN never enter the list
+    row = np.array([[np.nan, -np.inf, -1e30, -2e30, 1.0, np.nan, 3.0, -1e29]], np.float32)
+    idx4, _ = O.route_topk_softmax(row, 4)
+    np.testing.assert_array_equal(idx4[0], [6, 4, 7, 0])
+    # no valid logit: k sentinels, each with fast_exp(0) / (k * fast_exp(0))
+    idx5, w5 = O.route_topk_softmax(np.full((1, 6), np.nan, np.float32), 4)
+    assert (idx5 == 0).all() and (w5 == w5[0, 0]).all()
+    assert w5[0, 0] == pytest.approx(0.25, rel=1e-6)
+    # -0.0 and +0.0 compare equal: the lower expert comes first
+    idx6, _ = O.route_topk_softmax(np.array([[0.0, -1.0, -0.0, 0.0]], np.float32), 3)
+    np.testing.assert_array_equal(idx6[0], [0, 2, 3])
+    idx7, _ = O.route_topk_softmax(np.array([[-0.0, -1.0, 0.0]], np.float32), 2)
+    np.testing.assert_array_equal(idx7[0], [0, 2])
+
+
+def test_router_logits(O):
+    rng = np.random.default_rng(6)
+    T, H, E = 5, 256, 12
+    x = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    proj = O.f32_to_bf16(0.05 * rng.standard_normal((E, H)).astype(np.float32))
+    rs = O.f32_to_bf16((1 + 0.2 * rng.standard_normal(H)).astype(np.float32))
+    lg = O.router_logits(x, proj, rs)
+    # float64 restatement of RMS-scale-and-project
+    xd, pd, sd = (O.bf16_to_f32(a).astype(np.float64) for a in (x, proj, rs))
+    sqrt_n, n_eps = O.norm_consts(H)
+    inv = sqrt_n / np.sqrt((xd ** 2).sum(1) + n_eps)
+    ref = (xd * sd * inv[:, None]) @ pd.T
+    assert np.abs(lg - ref).max() <= 1e-5 * np.abs(ref).max()
+    # one-hot projection rows pick single scaled elements exactly: pins the
+    # element order of the chains (a transposed or shifted index picks another
+    # element) and the scaling (x * scale) * inv_rms.  x in {+-1, +-2, +-0.5}
+    # makes the sum of squares exact in any order.
+    xs = O.f32_to_bf16(rng.choice([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], (T, H)).astype(np.float32))
+    cols = np.array([0, 1, 15, 16, 17, 127, 128, 200, 255, 31, 64, 100])
+    oh = np.zeros((E, H), np.float32)
+    oh[np.arange(E), cols] = 1.0
+    lg1 = O.router_logits(xs, O.f32_to_bf16(oh), rs)
+    xf = O.bf16_to_f32(xs)
+    ssq = (xf.astype(np.float64) ** 2).sum(1).astype(np.float32)
+    inv32 = (np.float32(sqrt_n) / np.sqrt(ssq + np.float32(n_eps))).astype(np.float32)
+    scaled = ((xf * O.bf16_to_f32(rs)[None, :]).astype(np.float32) * inv32[:, None]).astype(np.float32)
+    np.testing.assert_array_equal(lg1, scaled[:, cols])
 
 
 def test_build_schedule_vs_sort(O):
