@@ -182,6 +182,31 @@ __device__ inline uint64_t cand_key(float lg, int e) {
 
 __device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// One step of a wave max over 64-bit keys through DPP lane moves (a VALU
+// op, no LDS round trip).  Rows outside ROW_MASK keep their own value.
+template <int CTRL, int ROW_MASK>
+__device__ inline uint64_t dpp_max_step(uint64_t v) {
+  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
+  return umax64(v, ((uint64_t)ohi << 32) | olo);
+}
+
+// Wave-uniform maximum: quad swaps (xor 1, xor 2), half-row and row
+// mirrors leave every lane of a 16-lane row with the row maximum; the
+// row_bcast15 / row_bcast31 steps carry it up so lane 63 holds the wave's.
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+  v = dpp_max_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_max_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_max_step<0x141, 0xF>(v);  // row_half_mirror
+  v = dpp_max_step<0x140, 0xF>(v);  // row_mirror
+  v = dpp_max_step<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
+  v = dpp_max_step<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 template <int NE>
 __global__ __launch_bounds__(256) void k_route_topk(
     const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
@@ -204,13 +229,7 @@ __global__ __launch_bounds__(256) void k_route_topk(
   float mx = 0.0f, sum = 0.0f, my_ev = 0.0f;
   int my_e = 0;
   for (int k = 0; k < top_k; ++k) {
-    uint64_t best = local;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t lo = __shfl_xor((uint32_t)best, o, kWave);
-      const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), o, kWave);
-      best = umax64(best, ((uint64_t)hi << 32) | lo);
-    }
+    const uint64_t best = wave_max_u64(local);
     float lg = kRouterSentinel;
     int e = 0;
     if (best != 0ull) {
