@@ -197,6 +197,72 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                        int experts_per_rank, int seq_len, int top_k, int hidden, int inter,
                        int block, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- vocabulary head and embedding ----------------------------------------- */
+
+#define BQ_SAMPLE_NMAX 256 /* continuous_batching/schedule.mojo:9 MAXIMUM_SAMPLING_LOGITS */
+
+/* kernels/flash_sample.mojo:21-28 SamplingParams, in the Mojo struct's field
+ * order and sizes (Int = int64, Bool = one byte), 40 bytes. */
+typedef struct bq_sampling_params {
+  float temperature;
+  float min_p;
+  int64_t top_k;
+  uint64_t seed;
+  int64_t n_keep;
+  uint8_t greedy;
+  uint8_t pad_[7];
+} bq_sampling_params;
+
+/* kernels/flash_sample.mojo:120-134 SampleOutcome[256], 2064 bytes.
+ * Entries k >= n of topn_val / topn_idx hold -1e30 / -1. */
+typedef struct bq_sample_outcome {
+  int32_t token_id;
+  float logz;
+  int64_t n;
+  float topn_val[BQ_SAMPLE_NMAX];
+  int32_t topn_idx[BQ_SAMPLE_NMAX];
+} bq_sample_outcome;
+
+/* dispatch_bq_head_prep[hidden, block, sqrt_n, n_eps] (butterquant_kernels/
+ * head.mojo:57-78 -> runtime.mojo:40-47): bq_norm_quant with per-block
+ * activation scales, x_sa [num_rows, hidden/block] = block amax.
+ * block in {64, 128, 256, 512}; hidden % block == 0; src 4-byte aligned. */
+int bq_head_prep(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                 int num_rows, int hidden, int block, float sqrt_n, float n_eps, void* stream);
+
+/* Bytes of device workspace bq_flash_sample needs (bf16 logits [rows, vocab]
+ * plus per-workgroup partials). */
+size_t bq_flash_sample_workspace_size(int num_rows, int vocab);
+
+/* dispatch_bq_flash_sample[cols, cap, n_max = 256] (butterquant_kernels/
+ * head.mojo:127-167) + finalize_outcomes (kernels/flash_sample.mojo:221-265)
+ * over vocabulary rows [vocab_base, vocab_base + vocab): per (row, v)
+ * y = bf16(softcap(head_logit_row)), score = y/T + gumbel(seed, row, v)
+ * (0 when greedy); outcome = score argmax (or the min_p / top_k pick among
+ * the top 256), logz = log-sum-exp of y/T, the top n_keep (y, v) by y
+ * descending, lower v first.  weight: the per-block head in tile16x64
+ * [vocab, hidden], wscales [vocab, hidden/block]; x_i8 [num_rows, hidden]
+ * and x_sa [num_rows, hidden/block] from bq_head_prep.  params and outcome
+ * are device arrays of num_rows.  num_rows <= 32, vocab % 16 == 0,
+ * block in {64, 128, 256, 512}, hidden/block <= 64; x_i8 and weight 16-byte
+ * aligned; workspace >= bq_flash_sample_workspace_size(), 256-byte aligned. */
+int bq_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,
+                    const float* wscales, const bq_sampling_params* params,
+                    bq_sample_outcome* outcome, int num_rows, int vocab, int hidden, int block,
+                    float cap, int64_t vocab_base, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* dispatch_bq_embed_lookup[hidden, scale] (butterquant_kernels/embedding.mojo:
+ * 65-96; BqEmbedLookupKernel 21-62): per token id (device int32 [seq_len]),
+ * the row of this shard (rows [rank*shard_rows, (rank+1)*shard_rows)) is
+ * dequantized per block (q * wscales[row, b]), FWHT(block)-rotated and
+ * written as bf16(x * scale); a token of another shard gives a zero row.
+ * weight: the per-block table in tile16x64 [shard_rows, hidden] (the head's
+ * own buffer when the embedding is tied); block in {64, 128, 256, 512}. */
+int bq_embed_lookup(const int32_t* token_ids, const int8_t* weight, const float* wscales,
+                    uint16_t* dst, int seq_len, int hidden, int block, int shard_rows, int rank,
+                    float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

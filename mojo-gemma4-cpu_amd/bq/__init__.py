@@ -44,13 +44,19 @@ SIGNATURES = {
     "bq_moe_router_logits": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_moe_route_topk": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "bq_head_prep": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
+    "bq_flash_sample_workspace_size": [_i, _i],
+    "bq_flash_sample": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, C.c_int64, _vp, _sz,
+                        _vp],
+    "bq_embed_lookup": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp],
     "bq_moe_phase1_gate_up": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "bq_moe_phase2_workspace_size": [_i, _i, _i],
     "bq_moe_phase2_down": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                            _vp, _sz, _vp],
 }
 _RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
-             "bq_moe_phase2_workspace_size": C.c_size_t}
+             "bq_moe_phase2_workspace_size": C.c_size_t,
+             "bq_flash_sample_workspace_size": C.c_size_t}
 
 
 def _load():
@@ -329,3 +335,72 @@ def moe_phase2(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: int, seq
                                    hidden, inter, block, _p(workspace), workspace.numel(),
                                    _stream()))
     return accum, o
+
+
+# --------------------------------------------------------------------------
+# vocabulary head and embedding
+# --------------------------------------------------------------------------
+SAMPLE_NMAX = 256
+PARAMS_BYTES, OUTCOME_BYTES = 40, 2064
+
+
+def head_prep(x: torch.Tensor, gamma: torch.Tensor, block: int = 128, sqrt_n=None, n_eps=None,
+              out=None):
+    """dispatch_bq_head_prep: per-block norm-quant -> (int8 [R,H], sa [R, H/block])."""
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    r, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    if out is None:
+        xq = torch.empty((r, h), dtype=torch.int8, device=x.device)
+        sa = torch.empty((r, h // block), dtype=torch.float32, device=x.device)
+    else:
+        xq, sa = out
+    _check(_lib.bq_head_prep(_p(x), _p(gamma), _p(xq), _p(sa), r, h, block, sqrt_n, n_eps,
+                             _stream()))
+    return xq, sa
+
+
+def flash_sample_workspace_size(rows: int, vocab: int) -> int:
+    return int(_lib.bq_flash_sample_workspace_size(rows, vocab))
+
+
+def flash_sample(x_i8, x_sa, weight: ButterquantWeight, wscales, params: torch.Tensor,
+                 block: int = 128, cap: float = 30.0, vocab_base: int = 0, workspace=None,
+                 out=None):
+    """dispatch_bq_flash_sample.  params: uint8 device tensor [R, 40] holding
+    SamplingParams; returns uint8 [R, 2064] SampleOutcome records."""
+    r, h = x_i8.shape
+    vocab = weight.n_rows
+    if params.dtype != torch.uint8 or tuple(params.shape) != (r, PARAMS_BYTES):
+        raise ValueError("params: uint8 [rows, 40] SamplingParams records")
+    if workspace is None:
+        workspace = torch.empty(max(flash_sample_workspace_size(r, vocab), 256),
+                                dtype=torch.uint8, device=x_i8.device)
+    if out is None:
+        out = torch.empty((r, OUTCOME_BYTES), dtype=torch.uint8, device=x_i8.device)
+    _check(_lib.bq_flash_sample(_p(x_i8), _p(x_sa), _p(weight.data), _p(wscales), _p(params),
+                                _p(out), r, vocab, h, block, cap, vocab_base, _p(workspace),
+                                workspace.numel(), _stream()))
+    return out
+
+
+def embed_lookup(token_ids: torch.Tensor, weight: ButterquantWeight, wscales: torch.Tensor,
+                 block: int = 128, scale: float | None = None, shard_rows: int | None = None,
+                 rank: int = 0, out=None):
+    """dispatch_bq_embed_lookup -> bf16 [T, H]."""
+    _dev(token_ids, torch.int32)
+    t = token_ids.shape[0]
+    h = weight.k
+    if scale is None:
+        import numpy as np
+        s = np.sqrt(np.float32(h), dtype=np.float32)
+        scale = float(torch.tensor(float(s)).to(torch.bfloat16).float())
+    if shard_rows is None:
+        shard_rows = weight.n_rows
+    if out is None:
+        out = torch.empty((t, h), dtype=torch.bfloat16, device=token_ids.device)
+    _check(_lib.bq_embed_lookup(_p(token_ids), _p(weight.data), _p(wscales), _p(out), t, h, block,
+                                shard_rows, rank, scale, _stream()))
+    return out

@@ -279,3 +279,72 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
 }
 
 }  // extern "C"
+
+// ---- vocabulary head and embedding -----------------------------------------
+static_assert(sizeof(bq_sampling_params) == 40 && sizeof(bq::SamplingParams) == 40,
+              "SamplingParams layout");
+static_assert(sizeof(bq_sample_outcome) == 2064 && sizeof(bq::SampleOutcome) == 2064,
+              "SampleOutcome layout");
+static_assert(BQ_SAMPLE_NMAX == bq::kSampleNmax, "n_max");
+
+static bool head_block_ok(int block) {
+  return block == 64 || block == 128 || block == 256 || block == 512;
+}
+
+int bq_head_prep(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                 int num_rows, int hidden, int block, float sqrt_n, float n_eps, void* stream) {
+  if (num_rows <= 0) return BQ_OK;
+  if (!src || !gamma || !x_i8 || !x_sa) return fail(BQ_ERR_INVALID, "bq_head_prep: null pointer");
+  if (!head_block_ok(block) || hidden <= 0 || hidden % block)
+    return fail(BQ_ERR_SHAPE, "bq_head_prep: need block in {64,128,256,512} dividing hidden %d", hidden);
+  if (reinterpret_cast<uintptr_t>(src) & 3u)
+    return fail(BQ_ERR_INVALID, "bq_head_prep: src must be 4-byte aligned");
+  return check_hip(bq::launch_head_prep(src, gamma, x_i8, x_sa, num_rows, hidden, block, sqrt_n,
+                                        n_eps, S(stream)),
+                   "head_prep");
+}
+
+size_t bq_flash_sample_workspace_size(int num_rows, int vocab) {
+  if (num_rows <= 0 || vocab <= 0) return 0;
+  return bq::head_workspace_bytes(num_rows, vocab);
+}
+
+int bq_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,
+                    const float* wscales, const bq_sampling_params* params,
+                    bq_sample_outcome* outcome, int num_rows, int vocab, int hidden, int block,
+                    float cap, int64_t vocab_base, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (num_rows <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !weight || !wscales || !params || !outcome || !workspace)
+    return fail(BQ_ERR_INVALID, "bq_flash_sample: null pointer");
+  if (num_rows > 32) return fail(BQ_ERR_UNSUPPORTED, "bq_flash_sample: num_rows %d > 32", num_rows);
+  if (vocab <= 0 || vocab % 16 || !head_block_ok(block) || hidden <= 0 || hidden % block ||
+      hidden / block > 64)
+    return fail(BQ_ERR_SHAPE, "bq_flash_sample: need vocab %% 16 == 0, block in {64..512} "
+                              "dividing hidden, hidden/block <= 64");
+  if (!(cap > 0.0f)) return fail(BQ_ERR_SHAPE, "bq_flash_sample: cap must be positive");
+  if (!a16(x_i8) || !a16(weight) || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(BQ_ERR_INVALID, "bq_flash_sample: x_i8/weight 16-byte, workspace 256-byte aligned");
+  if (workspace_bytes < bq::head_workspace_bytes(num_rows, vocab))
+    return fail(BQ_ERR_SHAPE, "bq_flash_sample: workspace %zu < %zu bytes", workspace_bytes,
+                bq::head_workspace_bytes(num_rows, vocab));
+  return check_hip(bq::launch_flash_sample(x_i8, x_sa, weight, wscales,
+                                           reinterpret_cast<const bq::SamplingParams*>(params),
+                                           reinterpret_cast<bq::SampleOutcome*>(outcome),
+                                           num_rows, vocab, hidden, block, cap, vocab_base,
+                                           workspace, S(stream)),
+                   "flash_sample");
+}
+
+int bq_embed_lookup(const int32_t* token_ids, const int8_t* weight, const float* wscales,
+                    uint16_t* dst, int seq_len, int hidden, int block, int shard_rows, int rank,
+                    float scale, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!token_ids || !weight || !wscales || !dst) return fail(BQ_ERR_INVALID, "bq_embed_lookup: null pointer");
+  if (!head_block_ok(block) || hidden <= 0 || hidden % block || shard_rows <= 0 || rank < 0)
+    return fail(BQ_ERR_SHAPE, "bq_embed_lookup: need block in {64,128,256,512} dividing hidden, "
+                              "shard_rows > 0");
+  return check_hip(bq::launch_embed(token_ids, weight, wscales, dst, seq_len, hidden, block,
+                                    shard_rows, rank, scale, S(stream)),
+                   "embed_lookup");
+}

@@ -123,6 +123,65 @@ __device__ inline float fast_exp_softmax_biased(float x) {
   return k * (QC_A + f * (QC_B + f * QC_C));
 }
 
+// simd_math/ops.mojo:35-69 exp_f32: input clamped to [-87, 88] through
+// sign-bit masks, n = trunc(xn + 0.5 - sign(xn)), Cody-Waite reduction with
+// two ln2 constants, degree-6 polynomial, times 2^n.
+__device__ inline float exp_f32(float x) {
+  const float LN2_HI = 0.693145751953125f, LN2_LO = 1.4286068203094172e-06f;
+  const float INV_LN2 = 1.4426950408889634f, EXP_LO = -87.0f, EXP_HI = 88.0f;
+  const float lo = (float)((__float_as_uint(x - EXP_LO) >> 31) & 1u);
+  float xc = x * (1.0f - lo) + EXP_LO * lo;
+  const float hi = (float)((__float_as_uint(EXP_HI - xc) >> 31) & 1u);
+  xc = xc * (1.0f - hi) + EXP_HI * hi;
+  const float xn = xc * INV_LN2;
+  const float sign = (float)(__float_as_uint(xn) >> 31);
+  const int n = (int)(xn + 0.5f - sign);
+  const float nf = (float)n;
+  const float r = (xc - nf * LN2_HI) - nf * LN2_LO;
+  const float p = 1.0f + r * (0.9999999995f + r * (0.5000000004f + r * (0.1666666456f +
+                  r * (0.04166685110f + r * (0.008333621758f + r * 0.001389404636f)))));
+  return p * __uint_as_float(((uint32_t)(n + 127)) << 23);
+}
+
+// simd_math/ops.mojo:100-124 log_f32: exponent / mantissa split, mantissa
+// folded into [sqrt2/2, sqrt2), odd series in z = (m-1)/(m+1).
+__device__ inline float log_f32(float x) {
+  const float LN2 = 0.6931471805599453f, SQRT2 = 1.4142135623730951f;
+  const uint32_t bits = __float_as_uint(x);
+  int e = (int)(bits >> 23) - 127;
+  float m = __uint_as_float((bits & 0x007FFFFFu) | 0x3F800000u);
+  const uint32_t big = __float_as_uint(SQRT2 - m) >> 31;
+  m = m * (1.0f - 0.5f * (float)big);
+  e = e + (int)big;
+  const float z = (m - 1.0f) / (m + 1.0f);
+  const float z2 = z * z;
+  float t = (float)(1.0 / 11.0);
+  t = (float)(1.0 / 9.0) + z2 * t;
+  t = (float)(1.0 / 7.0) + z2 * t;
+  t = (float)(1.0 / 5.0) + z2 * t;
+  t = (float)(1.0 / 3.0) + z2 * t;
+  t = 1.0f + z2 * t;
+  return 2.0f * z * t + (float)e * LN2;
+}
+
+// simd_math/sampling_rng.mojo:10-43: SplitMix64 finalizer, counter
+// (row << 32) ^ idx, u = (f32(h >> 40) + 1) / f32(2^24 + 1), Gumbel draw
+// -log(-log(u)).
+__device__ inline uint64_t mix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__device__ inline float gumbel_noise(uint64_t seed, int64_t row, int64_t idx) {
+  const uint64_t counter = ((uint64_t)row << 32) ^ (uint64_t)idx;
+  const uint64_t h = mix64(seed ^ mix64(counter));
+  const float top24 = 16777216.0f;
+  const float u = ((float)(int64_t)(h >> 40) + 1.0f) / (top24 + 1.0f);
+  return -log_f32(-log_f32(u));
+}
+
 // ---------------------------------------------------------------------------
 // wave helpers
 // ---------------------------------------------------------------------------
@@ -195,6 +254,37 @@ __device__ inline void lds_barrier() {
 // 16-byte global loads/stores
 __device__ inline v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ inline void st16(int8_t* p, v4i v) { *reinterpret_cast<v4i*>(p) = v; }
+
+// Sum of squares of a bf16 row in the order of rms_reduce_row (rmsnorm.mojo:
+// 16-17 -> dot_products.mojo:144-191): chain c = p*16 + j (p < pu) takes the
+// bf16 pairs c + i*pu*16, odd element first; s_j = sum_p chain(p, j) in p
+// order; then a 16-lane halving tree.  Wave-uniform result.
+__device__ inline float wave_row_ssq(const uint32_t* __restrict__ pairs, int hidden, int pu) {
+  const int lane = lane_id();
+  const int chains = pu * 16;
+  const int iters = hidden / (pu * 32);
+  const int c0 = min(lane, chains - 1), c1 = min(lane + 64, chains - 1);
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+  for (int i = 0; i < iters; ++i) {
+    const uint32_t p0 = pairs[i * chains + c0], p1 = pairs[i * chains + c1];
+    a0 = fmaf(__uint_as_float(p0 & 0xFFFF0000u), __uint_as_float(p0 & 0xFFFF0000u), a0);
+    a0 = fmaf(__uint_as_float(p0 << 16), __uint_as_float(p0 << 16), a0);
+    a1 = fmaf(__uint_as_float(p1 & 0xFFFF0000u), __uint_as_float(p1 & 0xFFFF0000u), a1);
+    a1 = fmaf(__uint_as_float(p1 << 16), __uint_as_float(p1 << 16), a1);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int c = p * 16 + (lane & 15);
+    const float v0 = __shfl(a0, c & 63, kWave);
+    const float v1 = __shfl(a1, c & 63, kWave);
+    if (p < pu) sum = sum + (c < 64 ? v0 : v1);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sum = sum + __shfl_down(sum, 8 >> q, 16);
+  return __shfl(sum, 0, kWave);
+}
 
 __device__ inline v4i mfma16x16x64(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);

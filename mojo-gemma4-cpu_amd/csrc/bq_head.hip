@@ -1,0 +1,580 @@
+// bq_head.hip -- the butterquant vocabulary head and embedding
+// (butterquant_kernels/head.mojo, butterquant_kernels/embedding.mojo).
+//
+// Head prep (BqHeadPrepKernel, head.mojo:25-78 -> runtime.mojo:11-47): the
+//   norm-quant of the final hidden rows with per-block activation scales.
+// Flash sample (BqFlashSampleKernel, head.mojo:81-167, finalize_outcomes in
+//   kernels/flash_sample.mojo:221-265), in two kernels:
+//   1. k_head_logits streams the [V, H] int8 head once (tile16x64 strips of
+//      16 vocabulary rows, every strip a contiguous H KiB run) and computes,
+//      for every (row, vocabulary index), head_logit_row's per-block f32
+//      chain, the softcap, the bf16 rounding, the Gumbel score; it stores
+//      the bf16 logit and folds the score argmax and the log-sum-exp into
+//      per-workgroup partials.
+//   2. k_head_select, one workgroup per row, merges the partials and picks
+//      the top 256 logits (value descending, lower index first: the order
+//      SampleAccum.topn_insert keeps) by a two-level byte histogram of the
+//      bf16 keys, then applies the min_p / top_k rule and writes the
+//      SampleOutcome.
+//   The argmax and the top-256 list are independent of how the vocabulary
+//   is partitioned, so they match the reference exactly; the log-sum-exp is
+//   a sum whose f32 rounding follows the partition (the reference's too).
+// Embedding (BqEmbedLookupKernel, embedding.mojo:21-62): per token, the
+//   owning shard's int8 row is dequantized per block, FWHT-rotated and
+//   scaled to bf16.
+#include "bq_device.hpp"
+#include "bq_kernels.hpp"
+
+namespace bq {
+
+constexpr float kNegInf = -1.0e30f;  // kernels/flash_sample.mojo:17 NEG_INF
+
+// ---------------------------------------------------------------------------
+// head prep: per-block norm-quant, one workgroup (4 waves) per row; block =
+// R*64, wave w takes blocks w, w+4, ...
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(256) void k_head_prep(
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int hidden, int pu, float sqrt_n,
+    float n_eps, float fwht_scale) {
+  const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = lane_id();
+  const uint16_t* x = src + (size_t)t * hidden;
+  __shared__ float s_inv;
+  if (wave == 0) {
+    const float ssq = wave_row_ssq(reinterpret_cast<const uint32_t*>(x), hidden, pu);
+    if (lane == 0) s_inv = sqrt_n / __builtin_sqrtf(ssq + n_eps);
+  }
+  __syncthreads();
+  const float inv_rms = s_inv;
+  constexpr int B = R * kWave;
+  const int nb = hidden / B;
+  for (int b = wave; b < nb; b += 4) {
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int k = b * B + i * kWave + lane;
+      v[i] = bf16_to_f32(x[k]) * inv_rms * bf16_to_f32(gamma[k]);
+    }
+    fwht_wave<R>(v, B);
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      v[i] = v[i] * fwht_scale;
+      m = fmaxf(m, fabsf(v[i]));
+    }
+    const float amax = wave_max(m);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) xq[(size_t)t * hidden + b * B + i * kWave + lane] = quantize_i8(v[i], inv);
+    if (lane == 0) sa[(size_t)t * nb + b] = amax;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// embedding lookup: one workgroup (4 waves) per token; wave w rotates blocks
+// w, w+4, ... of the row read from the tile16x64 layout.
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(256) void k_embed(
+    const int32_t* __restrict__ tokens, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, uint16_t* __restrict__ dst, int hidden, int shard_rows,
+    int rank, float scale, float fwht_scale) {
+  const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = lane_id();
+  constexpr int B = R * kWave;
+  const int nb = hidden / B;
+  const int tid = tokens[t];
+  const int owner = tid / shard_rows;
+  uint16_t* d = dst + (size_t)t * hidden;
+  if (owner != rank) {  // embedding.mojo:53: zero_row for another shard's token
+    for (int k = threadIdx.x; k < hidden; k += blockDim.x) d[k] = 0;
+    return;
+  }
+  const int n = tid - owner * shard_rows;
+  for (int b = wave; b < nb; b += 4) {
+    const float s = ws[(size_t)n * nb + b];
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) v[i] = (float)w[tile_offset(n, b * B + i * kWave + lane, hidden)] * s;
+    fwht_wave<R>(v, B);
+#pragma unroll
+    for (int i = 0; i < R; ++i) d[b * B + i * kWave + lane] = f32_to_bf16(v[i] * fwht_scale * scale);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flash sample, pass 1
+// ---------------------------------------------------------------------------
+struct HeadArgs {
+  const int8_t* x;         // [R, H] int8 activation
+  const float* xsa;        // [R, H/block]
+  const int8_t* w;         // [V, H] tile16x64
+  const float* ws;         // [V, H/block]
+  const SamplingParams* params;
+  uint16_t* y;             // [R, V] bf16 logits (workspace)
+  float* part;             // [grid, 4, RP] partials (workspace)
+  int R, V, H, block, nstrips;
+  float cap;
+  int64_t vbase;
+};
+
+constexpr int kHeadWaves = 8;
+
+// LSE accumulator merge (SampleAccum.merge, flash_sample.mojo:92-104)
+__device__ inline void lse_merge(float& mx, float& sum, float omx, float osum) {
+  if (osum > 0.0f) {
+    if (sum <= 0.0f) {
+      mx = omx;
+      sum = osum;
+    } else if (omx > mx) {
+      sum = sum * exp_f32(mx - omx) + osum;
+      mx = omx;
+    } else {
+      sum = sum + osum * exp_f32(omx - mx);
+    }
+  }
+}
+
+// score argmax, ties to the lower vocabulary index
+__device__ inline void samp_merge(float& s, int& i, float os, int oi) {
+  if (os > s || (os == s && oi < i)) {
+    s = os;
+    i = oi;
+  }
+}
+
+template <int MI>
+__global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
+  constexpr int RP = 16 * MI;  // padded rows
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int H = a.H, K64 = H >> 6, nb = H / a.block, fpb = a.block >> 6;
+  const int xstride = H + 16;  // padded LDS row stride (bank spread)
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  int8_t* s_x = smem;                                                   // [RP][H+16]
+  float* s_sa = reinterpret_cast<float*>(smem + (size_t)RP * xstride);  // [nb][RP] sa/127
+  __shared__ float s_invt[RP];
+  __shared__ uint64_t s_seed[RP];
+  __shared__ int s_greedy[RP];
+  __shared__ float s_red[kHeadWaves][4][RP];
+
+  for (int i = threadIdx.x; i < RP * (H / 16); i += blockDim.x) {
+    const int r = i / (H / 16), c = i % (H / 16);
+    v4i v = {0, 0, 0, 0};
+    if (r < a.R) v = *reinterpret_cast<const v4i*>(a.x + (size_t)r * H + c * 16);
+    *reinterpret_cast<v4i*>(s_x + (size_t)r * xstride + c * 16) = v;
+  }
+  for (int i = threadIdx.x; i < RP * nb; i += blockDim.x) {
+    const int b = i / RP, r = i % RP;
+    // head_logit_row divides: sa[b] / 127 (dot_products.mojo:87)
+    s_sa[i] = r < a.R ? a.xsa[(size_t)r * nb + b] / 127.0f : 0.0f;
+  }
+  if (threadIdx.x < RP) {
+    const int r = threadIdx.x;
+    const SamplingParams p = a.params[r < a.R ? r : 0];
+    s_invt[r] = 1.0f / p.temperature;
+    s_seed[r] = p.seed;
+    s_greedy[r] = p.greedy != 0;
+  }
+  __syncthreads();
+
+  // running partials per (mi, v) row slot: rows 16*mi + 4*(lane>>4) + v
+  float best[MI][4], lmx[MI][4], lsum[MI][4];
+  int bidx[MI][4];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      best[mi][v] = kNegInf;
+      bidx[mi][v] = 0x7FFFFFFF;
+      lmx[mi][v] = kNegInf;
+      lsum[mi][v] = 0.0f;
+    }
+
+  const int stride = gridDim.x * kHeadWaves;
+  for (int s = blockIdx.x * kHeadWaves + wave; s < a.nstrips; s += stride) {
+    const int8_t* wstrip = a.w + (size_t)s * K64 * 1024 + lane * 16;
+    const int col = s * 16 + (lane & 15);  // this lane's vocabulary row
+    const float* wsr = a.ws + (size_t)col * nb;
+    float raw[MI][4];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) raw[mi][v] = 0.0f;
+    // blocks in chunks of up to 8 fragments whose loads go out together
+    for (int f0 = 0; f0 < K64; f0 += 8) {
+      v4i wf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wf[j] = *reinterpret_cast<const v4i*>(wstrip + (size_t)min(f0 + j, K64 - 1) * 1024);
+      // every block (fpb fragments; fpb divides 8 for block <= 512, and K64
+      // is a multiple of fpb) lies inside one chunk; its int32 MFMA chain
+      // starts from zero and is drained into the f32 sum once
+#pragma unroll
+      for (int j0 = 0; j0 < 8; j0 += 1) {
+        const int f = f0 + j0;
+        if (f >= K64 || (f % fpb) != 0) continue;
+        const int b = f / fpb;
+        const float wsb = wsr[b];
+        v4i acc[MI];
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) acc[mi] = {0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (q >= fpb) break;
+          const int ff = f + q;
+#pragma unroll
+          for (int mi = 0; mi < MI; ++mi) {
+            const v4i xa = *reinterpret_cast<const v4i*>(
+                s_x + (size_t)(16 * mi + (lane & 15)) * xstride + ff * 64 + (lane >> 4) * 16);
+            acc[mi] = mfma16x16x64(xa, wf[(j0 + q) & 7], acc[mi]);
+          }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+          const float4 sv = *reinterpret_cast<const float4*>(s_sa + b * RP + 16 * mi + 4 * (lane >> 4));
+          raw[mi][0] = raw[mi][0] + (float)acc[mi][0] * sv.x * wsb;
+          raw[mi][1] = raw[mi][1] + (float)acc[mi][1] * sv.y * wsb;
+          raw[mi][2] = raw[mi][2] + (float)acc[mi][2] * sv.z * wsb;
+          raw[mi][3] = raw[mi][3] + (float)acc[mi][3] * sv.w * wsb;
+        }
+      }
+    }
+    // epilogue: y = bf16(softcap(raw)), score = y/T + gumbel
+    const int64_t gidx = a.vbase + col;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * mi + 4 * (lane >> 4) + v;
+        if (r >= a.R) continue;
+        const uint16_t yb = f32_to_bf16(tanh_f32(raw[mi][v] / a.cap) * a.cap);
+        a.y[(size_t)r * a.V + col] = yb;
+        const float yt = bf16_to_f32(yb) * s_invt[r];
+        const float g = s_greedy[r] ? 0.0f : gumbel_noise(s_seed[r], r, gidx);
+        samp_merge(best[mi][v], bidx[mi][v], yt + g, (int)gidx);
+        // lse_push (flash_sample.mojo:77-85)
+        lse_merge(lmx[mi][v], lsum[mi][v], yt, 1.0f);
+      }
+  }
+
+  // fold the 16 lanes sharing each row (lane & 15 = vocabulary column) and
+  // then the waves, in a fixed order
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float os = __shfl_xor(best[mi][v], o, 16);
+        const int oi = __shfl_xor(bidx[mi][v], o, 16);
+        const float om = __shfl_xor(lmx[mi][v], o, 16);
+        const float ou = __shfl_xor(lsum[mi][v], o, 16);
+        // the lower lane keeps the merge order (lower lane first)
+        if (lane & o) {
+          float m2 = om, s2 = ou;
+          lse_merge(m2, s2, lmx[mi][v], lsum[mi][v]);
+          lmx[mi][v] = m2;
+          lsum[mi][v] = s2;
+        } else {
+          lse_merge(lmx[mi][v], lsum[mi][v], om, ou);
+        }
+        samp_merge(best[mi][v], bidx[mi][v], os, oi);
+      }
+      if ((lane & 15) == 0) {
+        const int r = 16 * mi + 4 * (lane >> 4) + v;
+        s_red[wave][0][r] = best[mi][v];
+        s_red[wave][1][r] = __int_as_float(bidx[mi][v]);
+        s_red[wave][2][r] = lmx[mi][v];
+        s_red[wave][3][r] = lsum[mi][v];
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x < RP) {
+    const int r = threadIdx.x;
+    float bs = kNegInf, mx = kNegInf, sm = 0.0f;
+    int bi = 0x7FFFFFFF;
+    for (int wv = 0; wv < kHeadWaves; ++wv) {
+      samp_merge(bs, bi, s_red[wv][0][r], __float_as_int(s_red[wv][1][r]));
+      lse_merge(mx, sm, s_red[wv][2][r], s_red[wv][3][r]);
+    }
+    float* part = a.part + (size_t)blockIdx.x * 4 * RP;
+    part[0 * RP + r] = bs;
+    part[1 * RP + r] = __int_as_float(bi);
+    part[2 * RP + r] = mx;
+    part[3 * RP + r] = sm;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flash sample, pass 2: one workgroup of 1024 threads per row
+// ---------------------------------------------------------------------------
+constexpr int kSelThreads = 1024, kSelWaves = kSelThreads / 64;
+
+// bf16 bits -> unsigned order (-0 taken as +0: the reference compares floats)
+__device__ inline uint32_t bf16_key(uint16_t b) {
+  if (b == 0x8000u) b = 0;
+  return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
+}
+__device__ inline uint16_t key_bf16(uint32_t k) {
+  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
+}
+
+__global__ __launch_bounds__(kSelThreads) void k_head_select(
+    const uint16_t* __restrict__ ybuf, const float* __restrict__ part, int nparts, int RP,
+    const SamplingParams* __restrict__ params, SampleOutcome* __restrict__ out, int V,
+    int64_t vbase) {
+  const int r = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const uint16_t* y = ybuf + (size_t)r * V;
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t cand[kSampleNmax];
+  __shared__ int cnt, s_hb, s_lb, s_gt_hb, s_gt_t;
+  __shared__ int wcnt[kSelWaves];
+  __shared__ float r_bs[kSelWaves], r_mx[kSelWaves], r_sm[kSelWaves];
+  __shared__ int r_bi[kSelWaves];
+  const SamplingParams p = params[r];
+
+  // 1. merge the per-workgroup partials in order
+  float bs = kNegInf, mx = kNegInf, sm = 0.0f;
+  int bi = 0x7FFFFFFF;
+  {
+    // thread i folds partials i, i + 1024, ... in order; then the threads
+    // fold in order through the waves
+    for (int i = tid; i < nparts; i += kSelThreads) {
+      const float* pp = part + (size_t)i * 4 * RP;
+      samp_merge(bs, bi, pp[r], __float_as_int(pp[RP + r]));
+      lse_merge(mx, sm, pp[2 * RP + r], pp[3 * RP + r]);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float os = __shfl_xor(bs, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      const float om = __shfl_xor(mx, o, 64);
+      const float ou = __shfl_xor(sm, o, 64);
+      if (lane & o) {
+        float m2 = om, s2 = ou;
+        lse_merge(m2, s2, mx, sm);
+        mx = m2;
+        sm = s2;
+      } else {
+        lse_merge(mx, sm, om, ou);
+      }
+      samp_merge(bs, bi, os, oi);
+    }
+    if (lane == 0) {
+      r_bs[wave] = bs;
+      r_bi[wave] = bi;
+      r_mx[wave] = mx;
+      r_sm[wave] = sm;
+    }
+  }
+
+  // 2. top-n threshold by byte histograms of the bf16 keys
+  const int need = V < kSampleNmax ? V : kSampleNmax;
+  if (tid < 256) hist[tid] = 0;
+  if (tid == 0) cnt = 0;
+  __syncthreads();
+  for (int i = tid; i < V; i += kSelThreads) atomicAdd(&hist[bf16_key(y[i]) >> 8], 1u);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, hb = 255;
+    for (; hb > 0; --hb) {
+      if (acc + (int)hist[hb] >= need) break;
+      acc += (int)hist[hb];
+    }
+    s_hb = hb;
+    s_gt_hb = acc;  // keys with a higher high byte
+  }
+  __syncthreads();
+  const uint32_t hb = (uint32_t)s_hb;
+  if (tid < 256) hist[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < V; i += kSelThreads) {
+    const uint32_t k = bf16_key(y[i]);
+    if ((k >> 8) == hb) atomicAdd(&hist[k & 255], 1u);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = s_gt_hb, lb = 255;
+    for (; lb > 0; --lb) {
+      if (acc + (int)hist[lb] >= need) break;
+      acc += (int)hist[lb];
+    }
+    s_lb = lb;
+    s_gt_t = acc;  // keys above the threshold key
+  }
+  __syncthreads();
+  const uint32_t thr_key = (hb << 8) | (uint32_t)s_lb;
+  const int ties_needed = need - s_gt_t;
+
+  // 3. collect: every key above the threshold, and the first ties_needed keys
+  // equal to it in vocabulary order
+  int eq_base = 0;
+  for (int c0 = 0; c0 < V; c0 += kSelThreads) {
+    const int i = c0 + tid;
+    const uint32_t k = i < V ? bf16_key(y[i]) : 0u;
+    const bool gt = i < V && k > thr_key;
+    const bool eq = i < V && k == thr_key;
+    const uint64_t m = __ballot(eq);
+    if (lane == 0) wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int wv = 0; wv < kSelWaves; ++wv) {
+      const int cw = wcnt[wv];
+      before += wv < wave ? cw : 0;
+      total += cw;
+    }
+    const int rank = eq_base + before + __popcll(m & ((1ull << lane) - 1ull));
+    if (gt || (eq && rank < ties_needed)) {
+      const int pos = atomicAdd(&cnt, 1);
+      cand[pos] = ((uint64_t)k << 32) | (uint32_t)(0x7FFFFFFF - i);
+    }
+    eq_base += total;
+    __syncthreads();
+  }
+  // pad and sort descending by (key, -index): bitonic over 256 entries
+  if (tid < kSampleNmax && tid >= need) cand[tid] = 0ull;
+  __syncthreads();
+  for (int size = 2; size <= kSampleNmax; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (tid < kSampleNmax) {
+        const int j = tid ^ stride;
+        if (j > tid) {
+          const bool desc = (tid & size) == 0;
+          const uint64_t a0 = cand[tid], a1 = cand[j];
+          if (desc ? (a0 < a1) : (a0 > a1)) {
+            cand[tid] = a1;
+            cand[j] = a0;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // 4. finalize (flash_sample.mojo:232-265)
+  if (tid == 0) {
+    float fbs = kNegInf, fmx = kNegInf, fsm = 0.0f;
+    int fbi = 0x7FFFFFFF;
+    for (int wv = 0; wv < kSelWaves; ++wv) {
+      samp_merge(fbs, fbi, r_bs[wv], r_bi[wv]);
+      lse_merge(fmx, fsm, r_mx[wv], r_sm[wv]);
+    }
+    const float inv_t = 1.0f / p.temperature;
+    const int n = need;
+    const int n_out = (int64_t)n < p.n_keep ? n : (int)p.n_keep;
+    int token = fbi == 0x7FFFFFFF ? -1 : fbi;
+    const bool use_min_p = p.min_p > 0.0f, use_top_k = p.top_k > 0;
+    if ((use_min_p || use_top_k) && n > 0) {
+      int limit = n;
+      if (use_top_k && p.top_k < limit) limit = (int)p.top_k;
+      const float v0 = bf16_to_f32(key_bf16((uint32_t)(cand[0] >> 32)));
+      const float thr = use_min_p ? v0 + p.temperature * log_f32(p.min_p) : kNegInf;
+      auto score_of = [&](int k) {
+        const float yv = bf16_to_f32(key_bf16((uint32_t)(cand[k] >> 32)));
+        const int64_t gi = vbase + (0x7FFFFFFF - (int)(uint32_t)cand[k]);
+        const float g = p.greedy ? 0.0f : gumbel_noise(p.seed, r, gi);
+        return yv * inv_t + g;
+      };
+      int best_k = 0;
+      float best_g = score_of(0);
+      for (int k = 1; k < limit; ++k) {
+        const float yv = bf16_to_f32(key_bf16((uint32_t)(cand[k] >> 32)));
+        const float gk = score_of(k);
+        if (yv >= thr && gk > best_g) {
+          best_g = gk;
+          best_k = k;
+        }
+      }
+      token = (int)(vbase + (0x7FFFFFFF - (int)(uint32_t)cand[best_k]));
+    }
+    out[r].token_id = token;
+    out[r].logz = fmx + log_f32(fsm);
+    out[r].n = n_out;
+    s_lb = n_out;
+  }
+  __syncthreads();
+  const int n_out = s_lb;
+  if (tid < kSampleNmax) {
+    const bool keep = tid < n_out;
+    out[r].topn_val[tid] = keep ? bf16_to_f32(key_bf16((uint32_t)(cand[tid] >> 32))) : kNegInf;
+    out[r].topn_idx[tid] = keep ? (int)(vbase + (0x7FFFFFFF - (int)(uint32_t)cand[tid])) : -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static int pick_pu_bf16(int cols) {
+  if (cols % 256 == 0) return 8;
+  if (cols % 128 == 0) return 4;
+  if (cols % 64 == 0) return 2;
+  return 1;
+}
+
+hipError_t launch_head_prep(const uint16_t* src, const uint16_t* gamma, int8_t* xq, float* sa,
+                            int rows, int hidden, int block, float sqrt_n, float n_eps,
+                            hipStream_t st) {
+  const float sc = fwht_scale_host(block);
+  const int pu = pick_pu_bf16(hidden);
+  const dim3 g(rows), b(256);
+  switch (block) {
+    case 64: hipLaunchKernelGGL(k_head_prep<1>, g, b, 0, st, src, gamma, xq, sa, hidden, pu, sqrt_n, n_eps, sc); break;
+    case 128: hipLaunchKernelGGL(k_head_prep<2>, g, b, 0, st, src, gamma, xq, sa, hidden, pu, sqrt_n, n_eps, sc); break;
+    case 256: hipLaunchKernelGGL(k_head_prep<4>, g, b, 0, st, src, gamma, xq, sa, hidden, pu, sqrt_n, n_eps, sc); break;
+    case 512: hipLaunchKernelGGL(k_head_prep<8>, g, b, 0, st, src, gamma, xq, sa, hidden, pu, sqrt_n, n_eps, sc); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const int32_t* tokens, const int8_t* w, const float* ws, uint16_t* dst,
+                        int T, int hidden, int block, int shard_rows, int rank, float scale,
+                        hipStream_t st) {
+  const float sc = fwht_scale_host(block);
+  const dim3 g(T), b(256);
+  switch (block) {
+    case 64: hipLaunchKernelGGL(k_embed<1>, g, b, 0, st, tokens, w, ws, dst, hidden, shard_rows, rank, scale, sc); break;
+    case 128: hipLaunchKernelGGL(k_embed<2>, g, b, 0, st, tokens, w, ws, dst, hidden, shard_rows, rank, scale, sc); break;
+    case 256: hipLaunchKernelGGL(k_embed<4>, g, b, 0, st, tokens, w, ws, dst, hidden, shard_rows, rank, scale, sc); break;
+    case 512: hipLaunchKernelGGL(k_embed<8>, g, b, 0, st, tokens, w, ws, dst, hidden, shard_rows, rank, scale, sc); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int head_grid(int vocab) {
+  const int strips = vocab / 16;
+  const int g = (strips + kHeadWaves - 1) / kHeadWaves;
+  return g < 1024 ? g : 1024;
+}
+
+size_t head_workspace_bytes(int rows, int vocab) {
+  const int RP = rows <= 16 ? 16 : 32;
+  const size_t y = ((size_t)rows * vocab * 2 + 255) & ~(size_t)255;
+  return y + (size_t)head_grid(vocab) * 4 * RP * sizeof(float);
+}
+
+hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* w, const float* ws,
+                               const SamplingParams* params, SampleOutcome* out, int R, int V,
+                               int H, int block, float cap, int64_t vbase, void* workspace,
+                               hipStream_t st) {
+  HeadArgs a{};
+  a.x = x; a.xsa = xsa; a.w = w; a.ws = ws; a.params = params;
+  a.y = reinterpret_cast<uint16_t*>(workspace);
+  a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                    (((size_t)R * V * 2 + 255) & ~(size_t)255));
+  a.R = R; a.V = V; a.H = H; a.block = block; a.nstrips = V / 16; a.cap = cap; a.vbase = vbase;
+  const int grid = head_grid(V);
+  const int RP = R <= 16 ? 16 : 32;
+  const size_t lds = (size_t)RP * (H + 16) + (size_t)(H / block) * RP * sizeof(float);
+  if (R <= 16)
+    hipLaunchKernelGGL(k_head_logits<1>, dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+  else
+    hipLaunchKernelGGL(k_head_logits<2>, dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_head_select, dim3(R), dim3(kSelThreads), 0, st, a.y, a.part, grid, RP,
+                     params, out, V, vbase);
+  return hipGetLastError();
+}
+
+}  // namespace bq

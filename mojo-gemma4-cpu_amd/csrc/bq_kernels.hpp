@@ -59,6 +59,36 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
                                  int block, int bm, hipStream_t st);
 int moe_tile_bm(int max_routes, int experts);
 
+// kernels/flash_sample.mojo:21-28 SamplingParams and :120-134
+// SampleOutcome[256], laid out as the Mojo structs are (bq_api.h mirrors them)
+constexpr int kSampleNmax = 256;
+struct SamplingParams {
+  float temperature;
+  float min_p;
+  int64_t top_k;
+  uint64_t seed;
+  int64_t n_keep;
+  uint8_t greedy;
+  uint8_t pad_[7];
+};
+struct SampleOutcome {
+  int32_t token_id;
+  float logz;
+  int64_t n;
+  float topn_val[kSampleNmax];
+  int32_t topn_idx[kSampleNmax];
+};
+hipError_t launch_head_prep(const uint16_t* src, const uint16_t* gamma, int8_t* xq, float* sa,
+                            int rows, int hidden, int block, float sqrt_n, float n_eps,
+                            hipStream_t st);
+hipError_t launch_embed(const int32_t* tokens, const int8_t* w, const float* ws, uint16_t* dst,
+                        int T, int hidden, int block, int shard_rows, int rank, float scale,
+                        hipStream_t st);
+size_t head_workspace_bytes(int rows, int vocab);
+hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* w, const float* ws,
+                               const SamplingParams* params, SampleOutcome* out, int R, int V,
+                               int H, int block, float cap, int64_t vbase, void* workspace,
+                               hipStream_t st);
 hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const uint16_t* rscale,
                                 float* logits, int T, int H, int E, float sqrt_n, float n_eps,
                                 hipStream_t st);

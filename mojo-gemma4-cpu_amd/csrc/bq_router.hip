@@ -22,37 +22,6 @@ namespace bq {
 
 constexpr float kRouterSentinel = -1.0e30f;
 
-// Sum of squares of a bf16 row in the order of rms_reduce_row (rmsnorm.mojo:
-// 16-17 -> dot_products.mojo:144-191): chain c = p*16 + j (p < pu) takes the
-// bf16 pairs c + i*pu*16, odd element first; s_j = sum_p chain(p, j) in p
-// order; then a 16-lane halving tree.  Wave-uniform result.
-__device__ inline float wave_row_ssq(const uint32_t* __restrict__ pairs, int hidden, int pu) {
-  const int lane = lane_id();
-  const int chains = pu * 16;
-  const int iters = hidden / (pu * 32);
-  const int c0 = min(lane, chains - 1), c1 = min(lane + 64, chains - 1);
-  float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < iters; ++i) {
-    const uint32_t p0 = pairs[i * chains + c0], p1 = pairs[i * chains + c1];
-    a0 = fmaf(__uint_as_float(p0 & 0xFFFF0000u), __uint_as_float(p0 & 0xFFFF0000u), a0);
-    a0 = fmaf(__uint_as_float(p0 << 16), __uint_as_float(p0 << 16), a0);
-    a1 = fmaf(__uint_as_float(p1 & 0xFFFF0000u), __uint_as_float(p1 & 0xFFFF0000u), a1);
-    a1 = fmaf(__uint_as_float(p1 << 16), __uint_as_float(p1 << 16), a1);
-  }
-  float sum = 0.0f;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int c = p * 16 + (lane & 15);
-    const float v0 = __shfl(a0, c & 63, kWave);
-    const float v1 = __shfl(a1, c & 63, kWave);
-    if (p < pu) sum = sum + (c < 64 ? v0 : v1);
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) sum = sum + __shfl_down(sum, 8 >> q, 16);
-  return __shfl(sum, 0, kWave);
-}
-
 // A workgroup computes TT tokens x (4 waves x EE experts).  Lane l owns the
 // CPL adjacent chains c = l*CPL + r of the PU = CPL*4 accumulator bank
 // (64*CPL chains); per step i it scales its TT x values on the fly

@@ -649,3 +649,204 @@ void bqo_synth_normal_bf16(uint64_t seed, double sigma, uint16_t* out, size_t n)
     }
     free(tmp);
 }
+
+/* ========================================================================
+ * bq head and embedding (butterquant_kernels/head.mojo, embedding.mojo)
+ * ======================================================================== */
+
+/* simd_math/ops.mojo:35-69 exp_f32: clamp to [-87, 88] through bit masks,
+ * n = trunc(xn + 0.5 - sign(xn)), two-constant Cody-Waite reduction, degree-6
+ * polynomial, times 2^n. */
+float bqo_exp_f32(float x) {
+    const float LN2_HI = 0.693145751953125f, LN2_LO = 1.4286068203094172e-06f;
+    const float INV_LN2 = 1.4426950408889634f, EXP_LO = -87.0f, EXP_HI = 88.0f;
+    float lo = (float)((f2u(x - EXP_LO) >> 31) & 1u);
+    float xc = x * (1.0f - lo) + EXP_LO * lo;
+    float hi = (float)((f2u(EXP_HI - xc) >> 31) & 1u);
+    xc = xc * (1.0f - hi) + EXP_HI * hi;
+    float xn = xc * INV_LN2;
+    float sign = (float)(f2u(xn) >> 31);
+    int32_t n = (int32_t)(xn + 0.5f - sign);
+    float nf = (float)n;
+    float r = (xc - nf * LN2_HI) - nf * LN2_LO;
+    float p = 1.0f + r * (0.9999999995f + r * (0.5000000004f + r * (0.1666666456f +
+              r * (0.04166685110f + r * (0.008333621758f + r * 0.001389404636f)))));
+    return p * u2f(((uint32_t)(n + 127)) << 23);
+}
+
+/* simd_math/ops.mojo:100-124 log_f32: exponent/mantissa split, mantissa
+ * folded into [sqrt2/2, sqrt2), atanh series in z = (m-1)/(m+1). */
+float bqo_log_f32(float x) {
+    const float LN2 = 0.6931471805599453f, SQRT2 = 1.4142135623730951f;
+    uint32_t bits = f2u(x);
+    int32_t e = (int32_t)(bits >> 23) - 127;
+    float m = u2f((bits & 0x007FFFFFu) | 0x3F800000u);
+    uint32_t big = f2u(SQRT2 - m) >> 31;
+    float big_f = (float)big;
+    m = m * (1.0f - 0.5f * big_f);
+    e = e + (int32_t)big;
+    float z = (m - 1.0f) / (m + 1.0f);
+    float z2 = z * z;
+    float t = (float)(1.0 / 11.0);
+    t = (float)(1.0 / 9.0) + z2 * t;
+    t = (float)(1.0 / 7.0) + z2 * t;
+    t = (float)(1.0 / 5.0) + z2 * t;
+    t = (float)(1.0 / 3.0) + z2 * t;
+    t = 1.0f + z2 * t;
+    return 2.0f * z * t + (float)e * LN2;
+}
+
+/* simd_math/sampling_rng.mojo:10-43: the SplitMix64 finalizer keyed on
+ * (row << 32) ^ idx; u = (f32(h >> 40) + 1) / (2^24 + 1 rounded to f32);
+ * gumbel = -log(-log(u)). */
+uint64_t bqo_mix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float bqo_gumbel_noise(uint64_t seed, int64_t row, int64_t idx) {
+    uint64_t counter = ((uint64_t)row << 32) ^ (uint64_t)idx;
+    uint64_t h = bqo_mix64(seed ^ bqo_mix64(counter));
+    const float top24 = 16777216.0f;
+    float u = ((float)(int64_t)(h >> 40) + 1.0f) / (top24 + 1.0f);
+    return -bqo_log_f32(-bqo_log_f32(u));
+}
+
+/* simd_math/ops.mojo:160-167 softcap_value[cap] = tanh_f32(x / cap) * cap */
+float bqo_softcap(float x, float cap) { return bqo_tanh_f32(x / cap) * cap; }
+
+/* butterquant/dot_products.mojo:76-88 head_logit_row: per block the exact
+ * int32 dot, then acc += f32(r) * (sa[b] / 127) * scales[b] in block order. */
+float bqo_head_logit_row(const int8_t* x_i8, const float* sa, const int8_t* w,
+                         const float* wscales, int cols, int block) {
+    float acc = 0.0f;
+    for (int b = 0; b < cols / block; ++b) {
+        int32_t r = 0;
+        for (int k = b * block; k < (b + 1) * block; ++k) r += (int32_t)x_i8[k] * (int32_t)w[k];
+        acc += (float)r * (sa[b] / 127.0f) * wscales[b];
+    }
+    return acc;
+}
+
+/* kernels/flash_sample.mojo:33-117 SampleAccum (one accumulator). */
+typedef struct {
+    int n;
+    float* val;
+    float* g;
+    int32_t* idx;
+    float lse_max, lse_sum, samp_score;
+    int32_t samp_idx;
+} accum_t;
+
+static void topn_insert(accum_t* a, float y, float g, int32_t idx, int cap) {
+    if (a->n == cap && y <= a->val[cap - 1]) return;
+    int p;
+    if (a->n < cap) { p = a->n; a->n += 1; } else { p = cap - 1; }
+    while (p > 0 && a->val[p - 1] < y) {
+        a->val[p] = a->val[p - 1]; a->g[p] = a->g[p - 1]; a->idx[p] = a->idx[p - 1];
+        p -= 1;
+    }
+    a->val[p] = y; a->g[p] = g; a->idx[p] = idx;
+}
+
+static void lse_push(accum_t* a, float yt) {
+    if (a->lse_sum <= 0.0f) {
+        a->lse_max = yt; a->lse_sum = 1.0f;
+    } else if (yt > a->lse_max) {
+        a->lse_sum = a->lse_sum * bqo_exp_f32(a->lse_max - yt) + 1.0f;
+        a->lse_max = yt;
+    } else {
+        a->lse_sum = a->lse_sum + bqo_exp_f32(yt - a->lse_max);
+    }
+}
+
+/* BqFlashSampleKernel.execute (butterquant_kernels/head.mojo:85-117) over the
+ * whole vocabulary as one worker, then finalize_outcomes
+ * (kernels/flash_sample.mojo:221-265).  weight int8 [V, cols] row-major,
+ * wscales [V, cols/block]; params / outcomes as bqo_sampling_params /
+ * bqo_sample_outcome. */
+void bqo_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,
+                      const float* wscales, int rows, int vocab, int cols, int block,
+                      float cap, int64_t vocab_base, const bqo_sampling_params* params,
+                      bqo_sample_outcome* out) {
+    const int nmax = BQO_SAMPLE_NMAX, nb = cols / block;
+    accum_t* acc = (accum_t*)calloc((size_t)rows, sizeof(accum_t));
+    for (int r = 0; r < rows; ++r) {
+        acc[r].val = (float*)malloc(sizeof(float) * nmax);
+        acc[r].g = (float*)malloc(sizeof(float) * nmax);
+        acc[r].idx = (int32_t*)malloc(sizeof(int32_t) * nmax);
+        for (int k = 0; k < nmax; ++k) { acc[r].val[k] = -1.0e30f; acc[r].g[k] = -1.0e30f; acc[r].idx[k] = -1; }
+        acc[r].n = 0; acc[r].lse_max = -1.0e30f; acc[r].lse_sum = 0.0f;
+        acc[r].samp_score = -1.0e30f; acc[r].samp_idx = -1;
+    }
+    for (int v = 0; v < vocab; ++v) {
+        const int64_t gidx = vocab_base + v;
+        for (int r = 0; r < rows; ++r) {
+            const bqo_sampling_params* p = &params[r];
+            float raw = bqo_head_logit_row(x_i8 + (size_t)r * cols, x_sa + (size_t)r * nb,
+                                           weight + (size_t)v * cols, wscales + (size_t)v * nb,
+                                           cols, block);
+            float inv_t = 1.0f / p->temperature;
+            float y = bqo_bf16_to_f32(bqo_f32_to_bf16(bqo_softcap(raw, cap)));
+            float g = p->greedy ? 0.0f : bqo_gumbel_noise(p->seed, r, gidx);
+            float yt = y * inv_t;
+            lse_push(&acc[r], yt);
+            float score = yt + g;
+            if (score > acc[r].samp_score) { acc[r].samp_score = score; acc[r].samp_idx = (int32_t)gidx; }
+            topn_insert(&acc[r], y, score, (int32_t)gidx, nmax);
+        }
+    }
+    for (int r = 0; r < rows; ++r) {
+        accum_t* f = &acc[r];
+        const bqo_sampling_params* p = &params[r];
+        int n_out = f->n < p->n_keep ? f->n : (int)p->n_keep;
+        int32_t token = f->samp_idx;
+        int use_min_p = p->min_p > 0.0f, use_top_k = p->top_k > 0;
+        if ((use_min_p || use_top_k) && f->n > 0) {
+            int limit = f->n;
+            if (use_top_k && p->top_k < limit) limit = (int)p->top_k;
+            float thr = -1.0e30f;
+            if (use_min_p) thr = f->val[0] + p->temperature * bqo_log_f32(p->min_p);
+            int32_t best_idx = f->idx[0];
+            float best_g = f->g[0];
+            for (int k = 1; k < limit; ++k)
+                if (f->val[k] >= thr && f->g[k] > best_g) { best_g = f->g[k]; best_idx = f->idx[k]; }
+            token = best_idx;
+        }
+        bqo_sample_outcome* o = &out[r];
+        o->token_id = token;
+        o->logz = f->lse_max + bqo_log_f32(f->lse_sum);
+        o->n = n_out;
+        for (int k = 0; k < nmax; ++k) { o->topn_val[k] = -1.0e30f; o->topn_idx[k] = -1; }
+        for (int k = 0; k < n_out; ++k) { o->topn_val[k] = f->val[k]; o->topn_idx[k] = f->idx[k]; }
+        free(f->val); free(f->g); free(f->idx);
+    }
+    free(acc);
+}
+
+/* BqEmbedLookupKernel.execute (butterquant_kernels/embedding.mojo:36-53):
+ * per token, the owning shard's row is dequantized per block (q * scale,
+ * butterquant/dequantize.mojo:6-21), FWHT(block)-rotated and written as
+ * bf16(x * scale) (dequantize.mojo:25-32); a token owned by another shard
+ * gives a zero row.  weight int8 [shard_rows, hidden] row-major. */
+void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
+                      const float* wscales, int hidden, int block, int shard_rows,
+                      int rank, float scale, uint16_t* dst) {
+    const int nb = hidden / block;
+    float* ws = (float*)malloc(sizeof(float) * hidden);
+    for (int t = 0; t < T; ++t) {
+        int tid = token_ids[t], owner = tid / shard_rows;
+        uint16_t* d = dst + (size_t)t * hidden;
+        if (owner != rank) { for (int k = 0; k < hidden; ++k) d[k] = 0; continue; }
+        int local = tid - owner * shard_rows;
+        const int8_t* q = weight + (size_t)local * hidden;
+        for (int b = 0; b < nb; ++b)
+            for (int k = b * block; k < (b + 1) * block; ++k)
+                ws[k] = (float)q[k] * wscales[(size_t)local * nb + b];
+        bqo_fwht_row(ws, hidden, block);
+        for (int k = 0; k < hidden; ++k) d[k] = bqo_f32_to_bf16(ws[k] * scale);
+    }
+    free(ws);
+}

@@ -118,6 +118,41 @@ void bqo_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, int inter,
                     const float* d_colsum, int hidden, float* accum,
                     uint16_t* out);
 
+/* ---- bq head and embedding --------------------------------------------------- */
+#define BQO_SAMPLE_NMAX 256  /* continuous_batching/schedule.mojo:9 MAXIMUM_SAMPLING_LOGITS */
+/* kernels/flash_sample.mojo:21-28 SamplingParams (Mojo field order and sizes) */
+typedef struct {
+    float temperature;
+    float min_p;
+    int64_t top_k;
+    uint64_t seed;
+    int64_t n_keep;
+    uint8_t greedy;
+    uint8_t pad_[7];
+} bqo_sampling_params;
+/* kernels/flash_sample.mojo:120-134 SampleOutcome[256] */
+typedef struct {
+    int32_t token_id;
+    float logz;
+    int64_t n;
+    float topn_val[BQO_SAMPLE_NMAX];
+    int32_t topn_idx[BQO_SAMPLE_NMAX];
+} bqo_sample_outcome;
+float bqo_exp_f32(float x);                       /* simd_math/ops.mojo:35-69 */
+float bqo_log_f32(float x);                       /* simd_math/ops.mojo:100-124 */
+uint64_t bqo_mix64(uint64_t x);                   /* simd_math/sampling_rng.mojo:10-21 */
+float bqo_gumbel_noise(uint64_t seed, int64_t row, int64_t idx); /* sampling_rng.mojo:24-43 */
+float bqo_softcap(float x, float cap);            /* simd_math/ops.mojo:160-167 */
+float bqo_head_logit_row(const int8_t* x_i8, const float* sa, const int8_t* w,
+                         const float* wscales, int cols, int block); /* dot_products.mojo:76-88 */
+void bqo_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,
+                      const float* wscales, int rows, int vocab, int cols, int block,
+                      float cap, int64_t vocab_base, const bqo_sampling_params* params,
+                      bqo_sample_outcome* out);   /* head.mojo:85-167 */
+void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
+                      const float* wscales, int hidden, int block, int shard_rows,
+                      int rank, float scale, uint16_t* dst); /* embedding.mojo:21-96 */
+
 /* ---- synthetic inputs ---------------------------------------------------- */
 uint64_t bqo_splitmix64(uint64_t* state);
 /* splitmix64 -> Box-Muller (f64) -> *sigma -> f32 -> bf16 RNE */

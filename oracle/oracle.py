@@ -61,6 +61,15 @@ def _declare(L):
                  "bqo_fast_exp_softmax_biased"):
         getattr(L, name).restype = C.c_float
         getattr(L, name).argtypes = [C.c_float]
+    for name in ("bqo_exp_f32", "bqo_log_f32"):
+        getattr(L, name).restype = C.c_float
+        getattr(L, name).argtypes = [C.c_float]
+    L.bqo_mix64.restype = C.c_uint64
+    L.bqo_mix64.argtypes = [C.c_uint64]
+    L.bqo_gumbel_noise.restype = C.c_float
+    L.bqo_gumbel_noise.argtypes = [C.c_uint64, C.c_int64, C.c_int64]
+    L.bqo_softcap.restype = C.c_float
+    L.bqo_softcap.argtypes = [C.c_float, C.c_float]
     L.bqo_vnni_offset.restype = C.c_size_t
     L.bqo_vnni_offset.argtypes = [C.c_int, C.c_int, C.c_int]
 
@@ -156,23 +165,25 @@ def norm_consts(hidden: int):
 
 
 def norm_quant(x_bf16: np.ndarray, gamma_bf16: np.ndarray, block: int = 128,
-               sqrt_n=None, n_eps=None):
+               sqrt_n=None, n_eps=None, per_block: bool = False):
     """dispatch_bq_norm_quant (butterquant_kernels/linear.mojo:58-82 ->
-    runtime.mojo:11-37): bf16 [M,H] -> (int8 [M,H], sa [M])."""
+    runtime.mojo:11-37): bf16 [M,H] -> (int8 [M,H], sa [M]); with per_block
+    the head prep (runtime.mojo:40-47): sa [M, H/block]."""
     x = _c(x_bf16, np.uint16)
     g = _c(gamma_bf16, np.uint16)
     m, h = x.shape
     if sqrt_n is None:
         sqrt_n, n_eps = norm_consts(h)
     q = np.empty((m, h), np.int8)
-    sa = np.empty(m, np.float32)
+    nsa = h // block if per_block else 1
+    sa = np.empty((m, nsa) if per_block else m, np.float32)
     f = lib().bqo_prepare_norm_activation
     f.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                   C.c_float, C.c_float, C.c_int]
     for r in range(m):
         rc = f(C.c_void_p(x.ctypes.data + r * h * 2), _p(g),
-               C.c_void_p(q.ctypes.data + r * h), C.c_void_p(sa.ctypes.data + r * 4),
-               h, block, sqrt_n, n_eps, 0)
+               C.c_void_p(q.ctypes.data + r * h), C.c_void_p(sa.ctypes.data + r * nsa * 4),
+               h, block, sqrt_n, n_eps, int(per_block))
         if rc != 0:
             raise ValueError("norm_quant: bad block/hidden")
     return q, sa
@@ -390,3 +401,66 @@ def synth_normal_f32(seed: int, sigma: float, shape) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().bqo_synth_normal_f32(C.c_uint64(seed), C.c_double(sigma), _p(out), C.c_size_t(n))
     return out.reshape(shape)
+
+
+# ---------------------------------------------------------------- bq head / embedding
+SAMPLE_NMAX = 256  # continuous_batching/schedule.mojo:9
+# kernels/flash_sample.mojo:21-28 SamplingParams, kernels/flash_sample.mojo:120-134 SampleOutcome
+PARAMS_DT = np.dtype([("temperature", "<f4"), ("min_p", "<f4"), ("top_k", "<i8"), ("seed", "<u8"),
+                      ("n_keep", "<i8"), ("greedy", "u1"), ("pad", "u1", 7)])
+OUTCOME_DT = np.dtype([("token_id", "<i4"), ("logz", "<f4"), ("n", "<i8"),
+                       ("topn_val", "<f4", SAMPLE_NMAX), ("topn_idx", "<i4", SAMPLE_NMAX)])
+
+
+def sampling_params(rows, temperature=1.0, min_p=0.0, top_k=0, seed=0, n_keep=SAMPLE_NMAX,
+                    greedy=False):
+    """One SamplingParams per row; scalars broadcast, sequences per row."""
+    p = np.zeros(rows, PARAMS_DT)
+    for name, v in (("temperature", temperature), ("min_p", min_p), ("top_k", top_k),
+                    ("seed", seed), ("n_keep", n_keep), ("greedy", greedy)):
+        p[name] = v
+    return p
+
+
+def flash_sample(x_i8, x_sa, weight, wscales, params, block=128, cap=30.0, vocab_base=0):
+    """BqFlashSampleKernel over the whole vocabulary as one worker +
+    finalize_outcomes (butterquant_kernels/head.mojo:85-167,
+    kernels/flash_sample.mojo:221-265).  weight int8 [V, H] row-major."""
+    x = _c(x_i8, np.int8)
+    sa = _c(x_sa, np.float32)
+    w = _c(weight, np.int8)
+    ws = _c(wscales, np.float32)
+    pr = np.ascontiguousarray(params, PARAMS_DT)
+    R, H = x.shape
+    V = w.shape[0]
+    assert sa.shape == (R, H // block) and ws.shape == (V, H // block) and pr.shape == (R,)
+    out = np.zeros(R, OUTCOME_DT)
+    f = lib().bqo_flash_sample
+    f.argtypes = [C.c_void_p] * 4 + [C.c_int] * 4 + [C.c_float, C.c_int64, C.c_void_p, C.c_void_p]
+    f(_p(x), _p(sa), _p(w), _p(ws), R, V, H, block, cap, vocab_base, _p(pr), _p(out))
+    return out
+
+
+def embed_lookup(token_ids, weight, wscales, block=128, scale=None, shard_rows=None, rank=0):
+    """BqEmbedLookupKernel (butterquant_kernels/embedding.mojo:21-96):
+    int8 [rows, H] per-block scales -> bf16 [T, H]."""
+    tok = _c(token_ids, np.int32)
+    w = _c(weight, np.int8)
+    ws = _c(wscales, np.float32)
+    rows, H = w.shape
+    if scale is None:
+        scale = embed_scale(H)
+    if shard_rows is None:
+        shard_rows = rows
+    out = np.empty((tok.shape[0], H), np.uint16)
+    f = lib().bqo_embed_lookup
+    f.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                  C.c_int, C.c_float, C.c_void_p]
+    f(_p(tok), tok.shape[0], _p(w), _p(ws), H, block, shard_rows, rank, scale, _p(out))
+    return out
+
+
+def embed_scale(hidden: int) -> float:
+    """f32(bf16(sqrtf(hidden))) (gemma_4_moe_bq.mojo:965-966)."""
+    s = np.sqrt(np.float32(hidden), dtype=np.float32)
+    return float(bf16_to_f32(f32_to_bf16(np.array([s], np.float32)))[0])

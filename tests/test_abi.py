@@ -64,6 +64,19 @@ def test_validation_errors(L):
     assert L.bq_block_quant(P, P, P, 704, 1, 256, 0, None) == 2
     assert L.bq_moe_build_schedule(P, P, 4, 8, 0, 512, P, P, None) == 4
     assert L.bq_moe_route_topk(P, None, 4, 128, 17, P, P, None) == 4
+    assert L.bq_head_prep(P, P, P, P, 2, 2816, 96, C.c_float(1), C.c_float(1), None) == 2
+    assert L.bq_head_prep(C.c_void_p(18), P, P, P, 2, 2816, 128, C.c_float(1), C.c_float(1),
+                          None) == 1
+    ws = C.c_void_p(256)
+    assert L.bq_flash_sample(P, P, P, P, P, P, 33, 4096, 2816, 128, C.c_float(30), 0, ws,
+                             1 << 30, None) == 4
+    assert L.bq_flash_sample(P, P, P, P, P, P, 2, 4100, 2816, 128, C.c_float(30), 0, ws,
+                             1 << 30, None) == 2
+    assert L.bq_flash_sample(P, P, P, P, P, P, 2, 4096, 2816, 128, C.c_float(30), 0, ws,
+                             16, None) == 2
+    assert L.bq_flash_sample(P, P, P, P, P, P, 2, 4096, 2816, 128, C.c_float(30), 0,
+                             C.c_void_p(272), 1 << 30, None) == 1
+    assert L.bq_embed_lookup(P, P, P, P, 3, 2816, 100, 64, 0, C.c_float(1), None) == 2
     assert L.bq_moe_route_topk(P, None, 4, 2048, 8, P, P, None) == 4
     assert L.bq_moe_route_topk(P, None, 4, 128, 0, P, P, None) == 2
     assert L.bq_moe_route_topk(None, None, 4, 128, 8, P, P, None) == 1

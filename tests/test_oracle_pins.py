@@ -19,7 +19,13 @@ Pin map (oracle function -> pins):
   route top-k/softmax numpy stable argsort; weights sum to 1
   build_schedule      python stable sort of (expert, token, k)
   moe phase1/phase2   f64 closed forms over the unpacked weights
+  router logits       f64 projection; one-hot rows (element order, scaling)
+  exp_f32/log_f32     libm; SplitMix64 published outputs; Gumbel moments/CDF
+  head_logit_row      exact integers at unit scales; f64 per-block chain
+  flash_sample        numpy lexsort top-n, argmax, f64 logsumexp; filters
+  embed_lookup        one-hot FWHT closed form, f64 rotation, shard zeros
 """
+import ctypes as C
 import math
 
 import numpy as np
@@ -403,3 +409,154 @@ def test_synth_normal(O):
     assert abs(x.mean()) < 2e-4 and abs(x.std() - 0.02) < 2e-4
     b = O.synth_normal_bf16(0, 0.02, (1001,))
     np.testing.assert_array_equal(b, O.f32_to_bf16(O.synth_normal_f32(0, 0.02, (1001,))))
+
+
+# ---------------------------------------------------------------- head / embedding
+def test_sampling_rng_and_math(O):
+    L = O.lib()
+    # SplitMix64 from state 0 publishes 0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+    # 0x06C45D188009454F: the finalizer of gamma, 2*gamma, 3*gamma
+    gamma = 0x9E3779B97F4A7C15
+    assert L.bqo_mix64(0) == 0xE220A8397B1DCDAF
+    assert L.bqo_mix64(gamma) == 0x6E789E6AA1B965F4
+    assert L.bqo_mix64((2 * gamma) % (1 << 64)) == 0x06C45D188009454F
+    # exp_f32 / log_f32 against libm; the exp clamp at -87 / 88
+    xs = np.linspace(-87, 88, 2001).astype(np.float32)
+    e = np.array([L.bqo_exp_f32(float(v)) for v in xs])
+    assert (np.abs(e / np.exp(xs.astype(np.float64)) - 1) < 2e-6).all()
+    assert L.bqo_exp_f32(-100.0) == L.bqo_exp_f32(-87.0)
+    ls = np.exp(np.linspace(-60, 60, 2001)).astype(np.float32)
+    lg = np.array([L.bqo_log_f32(float(v)) for v in ls])
+    assert (np.abs(lg - np.log(ls.astype(np.float64))) < 2e-6 * np.maximum(1, np.abs(lg))).all()
+    # Gumbel(0, 1): mean = Euler-Mascheroni, variance = pi^2/6, CDF exp(-exp(-x))
+    g = np.array([L.bqo_gumbel_noise(11, 3, i) for i in range(200000)])
+    assert abs(g.mean() - 0.5772156649) < 0.01 and abs(g.var() - math.pi ** 2 / 6) < 0.03
+    for q in (-1.0, 0.0, 1.0, 3.0):
+        assert abs((g <= q).mean() - math.exp(-math.exp(-q))) < 0.005
+    # different rows / seeds give different streams
+    assert L.bqo_gumbel_noise(11, 4, 5) != L.bqo_gumbel_noise(11, 3, 5)
+    assert L.bqo_gumbel_noise(12, 3, 5) != L.bqo_gumbel_noise(11, 3, 5)
+    # softcap: tanh(x/c)*c with the fast tanh
+    for v in (-100.0, -3.0, 0.5, 29.0, 1000.0):
+        assert abs(L.bqo_softcap(v, 30.0) - 30 * math.tanh(v / 30)) < 3e-3 * 30
+
+
+def _head_case(O, R, V, H, seed, block=128, spread=1.0):
+    rng = np.random.default_rng(seed)
+    x = O.f32_to_bf16(rng.standard_normal((R, H)).astype(np.float32))
+    xq, xsa = O.norm_quant(x, np.full(H, 0x3F80, np.uint16), block, per_block=True)
+    w = rng.integers(-127, 128, (V, H), dtype=np.int8)
+    ws = (spread * rng.random((V, H // block)) / 127 / 40).astype(np.float32)
+    return xq, xsa, w, ws
+
+
+def test_head_logit_row(O):
+    rng = np.random.default_rng(3)
+    H, B = 512, 128
+    x = rng.integers(-127, 128, H, dtype=np.int8)
+    w = rng.integers(-127, 128, H, dtype=np.int8)
+    # sa = 127, scale = 1: the f32 chain sums exact integers (< 2^24)
+    f = O.lib().bqo_head_logit_row
+    f.restype = C.c_float
+    f.argtypes = [C.c_void_p] * 4 + [C.c_int, C.c_int]
+    ones = np.ones(H // B, np.float32)
+    got = f(x.ctypes.data, (127 * ones).ctypes.data, w.ctypes.data, ones.ctypes.data, H, B)
+    assert got == float(np.dot(x.astype(np.int64), w.astype(np.int64)))
+    sa = rng.random(H // B).astype(np.float32) * 4
+    ws = rng.random(H // B).astype(np.float32) * 0.01
+    got = f(x.ctypes.data, sa.ctypes.data, w.ctypes.data, ws.ctypes.data, H, B)
+    blocks = (x.astype(np.int64) * w).reshape(-1, B).sum(1)
+    ref = float((blocks * (sa.astype(np.float64) / 127) * ws).sum())
+    assert abs(got - ref) <= 1e-5 * abs(ref)
+
+
+def test_flash_sample_greedy_and_filters(O):
+    R, V, H = 3, 2048, 256
+    xq, xsa, w, ws = _head_case(O, R, V, H, 5)
+    p = O.sampling_params(R, temperature=[1.0, 0.5, 2.0], greedy=True)
+    out = O.flash_sample(xq, xsa, w, ws, p)
+    # y for every (row, v) from the per-row function + softcap + bf16
+    L = O.lib()
+    f = L.bqo_head_logit_row
+    f.restype = C.c_float
+    f.argtypes = [C.c_void_p] * 4 + [C.c_int, C.c_int]
+    y = np.zeros((R, V), np.float32)
+    for r in range(R):
+        for v in range(V):
+            raw = f(xq[r].ctypes.data, xsa[r].ctypes.data, w[v].ctypes.data, ws[v].ctypes.data, H, 128)
+            y[r, v] = O.bf16_to_f32(O.f32_to_bf16(np.array([L.bqo_softcap(raw, 30.0)], np.float32)))[0]
+    for r in range(R):
+        order = np.lexsort((np.arange(V), -y[r]))   # y descending, lower index first
+        assert out["n"][r] == 256
+        np.testing.assert_array_equal(out["topn_idx"][r], order[:256])
+        np.testing.assert_array_equal(out["topn_val"][r], y[r, order[:256]])
+        assert out["token_id"][r] == order[0]       # greedy: the first maximum
+        T = p["temperature"][r]
+        yt = y[r].astype(np.float64) * np.float64(np.float32(1) / np.float32(T))
+        lse = yt.max() + np.log(np.exp(yt - yt.max()).sum())
+        assert abs(out["logz"][r] - lse) < 1e-5 * abs(lse) + 1e-5
+    # top_k = 1 picks the top logit; n_keep truncates; min_p = 1 keeps only
+    # the maximal value
+    p2 = O.sampling_params(R, seed=[7, 8, 9], top_k=[1, 0, 0], n_keep=[256, 10, 256],
+                           min_p=[0.0, 0.0, 1.0])
+    out2 = O.flash_sample(xq, xsa, w, ws, p2)
+    assert out2["token_id"][0] == out["topn_idx"][0][0]
+    assert out2["n"][1] == 10 and (out2["topn_idx"][1][10:] == -1).all()
+    assert (out2["topn_val"][1][10:] == np.float32(-1e30)).all()
+    top2 = out2["topn_idx"][2]
+    assert y[2, out2["token_id"][2]] == y[2, top2[0]]
+    # without filters the token is the argmax of y/T + gumbel (first on ties)
+    for r in (1,):
+        g = np.array([L.bqo_gumbel_noise(int(p2["seed"][r]), r, v) for v in range(V)], np.float32)
+        score = (y[r] * (np.float32(1) / np.float32(p2["temperature"][r]))).astype(np.float32) + g
+        assert out2["token_id"][r] == int(np.argmax(score))
+
+
+def test_embed_lookup(O):
+    rng = np.random.default_rng(8)
+    rows, H, B = 64, 512, 128
+    w = np.zeros((rows, H), np.int8)
+    ws = (rng.random((rows, H // B)) + 0.5).astype(np.float32)
+    w[3, 130] = 5            # a single code in block 1 of row 3
+    w[7] = rng.integers(-127, 128, H, dtype=np.int8)
+    tok = np.array([3, 7, 70, 3], np.int32)  # 70 belongs to shard 1
+    scale = O.embed_scale(2816)
+    assert scale == 53.0
+    out = O.bf16_to_f32(O.embed_lookup(tok, w, ws, B, scale=scale))
+    # FWHT of a one-hot: +-c_B everywhere in that block, zero elsewhere
+    c = O.fwht_scale(B)
+    k = np.arange(B)
+    sign = np.where([bin(v & (130 - B)).count("1") % 2 for v in k], -1.0, 1.0)
+    ref = np.float32(5 * ws[3, 1]) * np.float32(c) * sign
+    ref = O.bf16_to_f32(O.f32_to_bf16((ref.astype(np.float32) * np.float32(scale)).astype(np.float32)))
+    np.testing.assert_array_equal(out[0, B:2 * B], ref)
+    assert (out[0, :B] == 0).all() and (out[0, 2 * B:] == 0).all()
+    assert (out[2] == 0).all()                 # foreign shard: zero row
+    np.testing.assert_array_equal(out[3], out[0])
+    # a generic row against the float64 rotation
+    deq = w[7].astype(np.float64).reshape(-1, B) * ws[7][:, None]
+    hd = np.array([[(-1) ** bin(i & j).count("1") for j in range(B)] for i in range(B)], np.float64)
+    rot = (deq @ hd.T / math.sqrt(B)).reshape(-1) * scale
+    assert np.abs(out[1] - rot).max() <= 2 ** -7 * np.abs(rot).max()
+    # sharded: rank 1 of two owns rows [32, 64)
+    out_r1 = O.embed_lookup(np.array([40, 3], np.int32), w[32:], ws[32:], B, scale=scale,
+                            shard_rows=32, rank=1)
+    assert (out_r1[1] == 0).all()
+    np.testing.assert_array_equal(out_r1[0], O.embed_lookup(np.array([40], np.int32), w, ws, B,
+                                                            scale=scale)[0])
+
+
+def test_head_prep_per_block(O):
+    # per-block head prep: block == hidden reproduces the per-row norm-quant;
+    # every block's amax maps to +-127
+    rng = np.random.default_rng(9)
+    H = 512
+    x = O.f32_to_bf16(rng.standard_normal((4, H)).astype(np.float32))
+    g = np.full(H, 0x3F80, np.uint16)
+    q1, s1 = O.norm_quant(x, g, 512)
+    q2, s2 = O.norm_quant(x, g, 512, per_block=True)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2[:, 0])
+    q3, s3 = O.norm_quant(x, g, 128, per_block=True)
+    assert s3.shape == (4, 4)
+    assert (np.abs(q3.reshape(4, 4, 128)).max(2) == 127).all()
