@@ -15,7 +15,8 @@ replayed, so host launch overhead does not stretch the timed region.
 Timing uses HIP events on the stream the kernels run on, bracketed by
 device synchronizations.  Data: synthetic, bf16 N(0, 0.02) weights (seed 0)
 quantized by libbq's own encoder, bf16 N(0,1) activations (seed 1),
-N(0,1) router logits (seed 2).
+N(0,1) router logits (seed 2); the vocabulary head uses uniform random int8
+codes with per-block scales (seed 0).
 """
 from __future__ import annotations
 
@@ -40,7 +41,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16"])
+                    choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16", "head"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
@@ -175,6 +176,44 @@ class MoeLayer:
         bq.block_quant(self.bucket, 64, True, out=(self.bi8, self.bsa))
         bq.moe_phase2(self.bi8, self.bsa, self.eo, self.routes, self.Wd, E, T, TOPK, H,
                       workspace=self.ws, out=(self.accum, self.out))
+
+
+def bench_head(bq, torch, steps, rows_list=(1, 16)):
+    """The tied vocabulary head at decode: head prep (per-block norm-quant of
+    the final hidden rows) + flash sample over all 262144 vocabulary rows
+    (per-block B = 128 int8 head, softcap 30, Gumbel sampling, top-256),
+    graph-replayed.  The 761 MB head is larger than the Infinity Cache, so
+    every replay streams it from HBM."""
+    import numpy as np
+    V, HH, B = 262144, H, 128
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    codes = torch.randint(-127, 128, (V * HH,), generator=gen, dtype=torch.int8, device="cuda")
+    W = bq.ButterquantWeight(bq.retile(codes, V, HH),
+                             torch.rand(V, HH // B, generator=gen, device="cuda") / 127 / 30, V, HH)
+    del codes
+    gamma = torch.ones(HH, dtype=torch.bfloat16, device="cuda")
+    alg = V * HH + V * (HH // B) * 4
+    out = {}
+    for R in rows_list:
+        xg = torch.Generator(device="cuda").manual_seed(1)
+        x = torch.randn(R, HH, generator=xg, device="cuda").to(torch.bfloat16)
+        xq = torch.empty(R, HH, dtype=torch.int8, device="cuda")
+        xsa = torch.empty(R, HH // B, dtype=torch.float32, device="cuda")
+        p = np.zeros((R, 40), np.uint8)
+        pv = p.view(np.dtype([("t", "<f4"), ("m", "<f4"), ("k", "<i8"), ("s", "<u8"),
+                              ("n", "<i8"), ("g", "u1"), ("pad", "u1", 7)])).reshape(R)
+        pv["t"], pv["n"], pv["s"], pv["k"], pv["m"] = 1.0, 256, np.arange(R) + 1, 64, 0.05
+        pr = torch.from_numpy(p).cuda()
+        ws = torch.empty(bq.flash_sample_workspace_size(R, V), dtype=torch.uint8, device="cuda")
+        res = torch.empty(R, 2064, dtype=torch.uint8, device="cuda")
+
+        def step(_i=0):
+            bq.head_prep(x, gamma, B, out=(xq, xsa))
+            bq.flash_sample(xq, xsa, W, W.scale, pr, block=B, workspace=ws, out=res)
+        g = graph_of(step, 4)
+        ms, wall, n = time_graph(g, 4, max(8, steps // 64), 4)
+        out[R] = dict(ms=ms, gbs=alg / (ms * 1e-3) / 1e9)
+    return dict(alg_bytes=alg, rows=out)
 
 
 def moe_weights(bq, torch):
@@ -339,6 +378,8 @@ def main():
             res["moe2048"] = bench_moe(bq, torch, 2048, reps, max(10, args.steps // 32))
         if wl in ("all", "layer16"):
             res["layer16"] = bench_layer16(bq, torch, Wgu, Wd, max(10, args.steps // 32))
+    if wl in ("all", "head"):
+        res["head"] = bench_head(bq, torch, args.steps)
     if args.calib_copy:
         calib_copy(torch)
 
@@ -384,6 +425,13 @@ def main():
                 "int8_tops": round(m["ops"] / (m["ms"] * 1e-3) / 1e12, 1)}
     if "layer16" in res:
         line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()}
+    if "head" in res:
+        hd = res["head"]
+        line["head_flash_sample_v262144"] = {
+            f"rows{R}": {"us": round(v["ms"] * 1e3, 1), "weight_GBs": round(v["gbs"], 1),
+                         "hbm_frac": round(v["gbs"] / HBM_PEAK_GBS, 4)}
+            for R, v in hd["rows"].items()}
+        line["head_flash_sample_v262144"]["alg_bytes"] = hd["alg_bytes"]
     if "gemv" in res and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_gemv(res["gemv"]["codes"], res["gemv"]["scales"],
                                                  args.cpu_seconds)

@@ -243,7 +243,7 @@ size_t bq_flash_sample_workspace_size(int num_rows, int vocab);
  * descending, lower v first.  weight: the per-block head in tile16x64
  * [vocab, hidden], wscales [vocab, hidden/block]; x_i8 [num_rows, hidden]
  * and x_sa [num_rows, hidden/block] from bq_head_prep.  params and outcome
- * are device arrays of num_rows.  num_rows <= 32, vocab % 16 == 0,
+ * are device arrays of num_rows.  num_rows <= 32, vocab % 16 == 0, vocab <= 2^20,
  * block in {64, 128, 256, 512}, hidden/block <= 64; x_i8 and weight 16-byte
  * aligned; workspace >= bq_flash_sample_workspace_size(), 256-byte aligned. */
 int bq_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,

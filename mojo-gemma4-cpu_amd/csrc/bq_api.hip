@@ -317,7 +317,9 @@ int bq_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weight,
   if (num_rows <= 0) return BQ_OK;
   if (!x_i8 || !x_sa || !weight || !wscales || !params || !outcome || !workspace)
     return fail(BQ_ERR_INVALID, "bq_flash_sample: null pointer");
-  if (num_rows > 32) return fail(BQ_ERR_UNSUPPORTED, "bq_flash_sample: num_rows %d > 32", num_rows);
+  if (num_rows > 32 || vocab > (1 << 20))
+    return fail(BQ_ERR_UNSUPPORTED, "bq_flash_sample: num_rows %d > 32 or vocab %d > 2^20", num_rows,
+                vocab);
   if (vocab <= 0 || vocab % 16 || !head_block_ok(block) || hidden <= 0 || hidden % block ||
       hidden / block > 64)
     return fail(BQ_ERR_SHAPE, "bq_flash_sample: need vocab %% 16 == 0, block in {64..512} "

@@ -305,9 +305,22 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// flash sample, pass 2: one workgroup of 1024 threads per row
+// flash sample, pass 2: exact top-256 selection over the bf16 logits of each
+// row, spread over chunks of 4096 logits (one workgroup each), then one
+// workgroup per row to sort and finalize.
+//   hist_hi   : per chunk, a histogram of the keys' high byte
+//   thr_hi    : per row, the high byte hb of the 256th largest key
+//   hist_lo   : per chunk, a histogram of the low byte among keys in hb
+//   thr_lo    : per row, the threshold key t, the count of keys above it,
+//               how many ties (keys equal to t) are needed, and each chunk's
+//               count of earlier ties
+//   collect   : per chunk, appends the keys above t and the needed ties
+//               (lowest indices first) to the row's candidate list
+//   finalize  : per row, sorts the 256 candidates, applies min_p / top_k,
+//               writes the SampleOutcome
 // ---------------------------------------------------------------------------
-constexpr int kSelThreads = 1024, kSelWaves = kSelThreads / 64;
+constexpr int kChunk = 4096, kChunkThreads = 256;  // 16 logits per thread
+constexpr int kSelThreads = 256, kSelWaves = kSelThreads / 64;
 
 // bf16 bits -> unsigned order (-0 taken as +0: the reference compares floats)
 __device__ inline uint32_t bf16_key(uint16_t b) {
@@ -318,25 +331,222 @@ __device__ inline uint16_t key_bf16(uint32_t k) {
   return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
 }
 
+struct SelArgs {
+  const uint16_t* y;   // [R, V]
+  uint32_t* hist1;     // [R, nc, 256]
+  uint32_t* hist2;     // [R, nc, 256]
+  int* thr;            // [R, 4]: hb, keys above hb, threshold key, ties needed
+  int* eqpre;          // [R, nc] ties in earlier chunks
+  int* cnt;            // [R] candidates appended
+  uint64_t* cand;      // [R, 256] (key << 32) | (0x7FFFFFFF - index)
+  int V, nc;
+};
+
+// this thread's 16 keys of chunk c (V % 16 == 0: all valid or none)
+__device__ inline bool chunk_keys(const SelArgs& a, int r, int c, uint32_t (&k)[16]) {
+  const int i0 = c * kChunk + threadIdx.x * 16;
+  if (i0 >= a.V) return false;
+  const v4i* src = reinterpret_cast<const v4i*>(a.y + (size_t)r * a.V + i0);
+  const v4i u0 = src[0], u1 = src[1];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    k[2 * q] = bf16_key((uint16_t)((uint32_t)u0[q] & 0xFFFFu));
+    k[2 * q + 1] = bf16_key((uint16_t)((uint32_t)u0[q] >> 16));
+    k[8 + 2 * q] = bf16_key((uint16_t)((uint32_t)u1[q] & 0xFFFFu));
+    k[8 + 2 * q + 1] = bf16_key((uint16_t)((uint32_t)u1[q] >> 16));
+  }
+  return true;
+}
+
+// LDS histogram increment (no return value: the hardware serializes only
+// the lanes of one instruction that hit the same bin)
+__device__ inline void hist_add(uint32_t* hist, uint32_t bin, bool active) {
+  if (active) atomicAdd(&hist[bin], 1u);
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_hist_hi(SelArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  __shared__ uint32_t hist[256];
+  hist[tid] = 0;
+  if (c == 0 && tid == 0) a.cnt[r] = 0;
+  __syncthreads();
+  uint32_t k[16];
+  const bool ok = chunk_keys(a, r, c, k);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) hist_add(hist, ok ? k[q] >> 8 : 0u, ok);
+  __syncthreads();
+  a.hist1[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];
+}
+
+// Block-wide inclusive suffix sum over 256 bins (bin 255 first), 256 threads.
+__device__ inline int suffix_sum256(int v, int* tmp) {
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  // scan in descending bin order: reversed position j = 255 - tid
+  int s = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_down(s, o, 64);  // lanes above hold higher bins
+    if (lane + o < 64) s += u;
+  }
+  if (lane == 0) tmp[wave] = s;
+  __syncthreads();
+  int above = 0;
+  for (int w = wave + 1; w < 4; ++w) above += tmp[w];
+  __syncthreads();
+  return s + above;
+}
+
+// Find bin b with suffix(b) >= need > suffix(b + 1); writes (b, suffix(b+1)).
+__device__ inline void pick_bin(int suffix, int total, int need, int base, int* out_bin,
+                                int* out_above) {
+  const int tid = threadIdx.x;
+  const int s_incl = base + suffix, s_excl = base + suffix - total;
+  if (s_incl >= need && s_excl < need) {
+    *out_bin = tid;
+    *out_above = s_excl;
+  }
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_hi(SelArgs a) {
+  const int r = blockIdx.x, tid = threadIdx.x;
+  __shared__ int tmp[4];
+  __shared__ int s_bin, s_above;
+  int total = 0;
+#pragma unroll 8
+  for (int c = 0; c < a.nc; ++c) total += (int)a.hist1[((size_t)r * a.nc + c) * 256 + tid];
+  const int need = a.V < kSampleNmax ? a.V : kSampleNmax;
+  if (tid == 0) { s_bin = 0; s_above = 0; }
+  __syncthreads();
+  const int suf = suffix_sum256(total, tmp);
+  pick_bin(suf, total, need, 0, &s_bin, &s_above);
+  __syncthreads();
+  if (tid == 0) {
+    a.thr[r * 4 + 0] = s_bin;
+    a.thr[r * 4 + 1] = s_above;
+  }
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_hist_lo(SelArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  __shared__ uint32_t hist[256];
+  hist[tid] = 0;
+  __syncthreads();
+  const uint32_t hb = (uint32_t)a.thr[r * 4 + 0];
+  uint32_t k[16];
+  const bool ok = chunk_keys(a, r, c, k);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) hist_add(hist, ok ? k[q] & 255u : 0u, ok && (k[q] >> 8) == hb);
+  __syncthreads();
+  a.hist2[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_lo(SelArgs a) {
+  const int r = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  __shared__ int tmp[4];
+  __shared__ int s_bin, s_above;
+  int total = 0;
+#pragma unroll 8
+  for (int c = 0; c < a.nc; ++c) total += (int)a.hist2[((size_t)r * a.nc + c) * 256 + tid];
+  const int need = a.V < kSampleNmax ? a.V : kSampleNmax;
+  const int hb = a.thr[r * 4 + 0], above_hb = a.thr[r * 4 + 1];
+  if (tid == 0) { s_bin = 0; s_above = above_hb; }
+  __syncthreads();
+  const int suf = suffix_sum256(total, tmp);
+  pick_bin(suf, total, need, above_hb, &s_bin, &s_above);
+  __syncthreads();
+  const int lb = s_bin;
+  // ties (key == threshold) in the chunks before each chunk: exclusive scan
+  // over chunks (nc <= 256: thread c holds chunk c)
+  const int e = tid < a.nc ? (int)a.hist2[((size_t)r * a.nc + tid) * 256 + lb] : 0;
+  int incl = e;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += tmp[w];
+  if (tid < a.nc) a.eqpre[(size_t)r * a.nc + tid] = before + incl - e;
+  if (tid == 0) {
+    a.thr[r * 4 + 2] = (hb << 8) | lb;
+    a.thr[r * 4 + 3] = need - s_above;  // ties needed
+  }
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_collect(SelArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  __shared__ int tmp_e[4], tmp_s[4];
+  __shared__ int s_base;
+  const uint32_t t = (uint32_t)a.thr[r * 4 + 2];
+  const int ties_needed = a.thr[r * 4 + 3];
+  const int eq_before = a.eqpre[(size_t)r * a.nc + c];
+  uint32_t k[16];
+  const bool ok = chunk_keys(a, r, c, k);
+  // ties before this thread's keys, in index order
+  int n_eq = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) n_eq += (ok && k[q] == t) ? 1 : 0;
+  int inc_e = n_eq;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc_e, o, 64);
+    if (lane >= o) inc_e += u;
+  }
+  if (lane == 63) tmp_e[wave] = inc_e;
+  __syncthreads();
+  int be = 0;
+  for (int w = 0; w < wave; ++w) be += tmp_e[w];
+  int rank = eq_before + be + inc_e - n_eq;
+  // which of this thread's keys are selected
+  uint32_t sel = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const bool eq = ok && k[q] == t;
+    if ((ok && k[q] > t) || (eq && rank < ties_needed)) sel |= 1u << q;
+    rank += eq ? 1 : 0;
+  }
+  // one global atomic per workgroup reserves the chunk's slots
+  const int n_sel = __popc(sel);
+  int inc_s = n_sel;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc_s, o, 64);
+    if (lane >= o) inc_s += u;
+  }
+  if (lane == 63) tmp_s[wave] = inc_s;
+  __syncthreads();
+  if (tid == 0) {
+    const int total = tmp_s[0] + tmp_s[1] + tmp_s[2] + tmp_s[3];
+    s_base = total ? atomicAdd(&a.cnt[r], total) : 0;
+  }
+  __syncthreads();
+  int pos = s_base + inc_s - n_sel;
+  for (int w = 0; w < wave; ++w) pos += tmp_s[w];
+  const int i0 = c * kChunk + tid * 16;
+#pragma unroll
+  for (int q = 0; q < 16; ++q)
+    if (sel & (1u << q)) a.cand[(size_t)r * kSampleNmax + pos++] = ((uint64_t)k[q] << 32) | (uint32_t)(0x7FFFFFFF - (i0 + q));
+}
+
 __global__ __launch_bounds__(kSelThreads) void k_head_select(
-    const uint16_t* __restrict__ ybuf, const float* __restrict__ part, int nparts, int RP,
+    const uint64_t* __restrict__ cand_g, const float* __restrict__ part, int nparts, int RP,
     const SamplingParams* __restrict__ params, SampleOutcome* __restrict__ out, int V,
     int64_t vbase) {
   const int r = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  const uint16_t* y = ybuf + (size_t)r * V;
-  __shared__ uint32_t hist[256];
   __shared__ uint64_t cand[kSampleNmax];
-  __shared__ int cnt, s_hb, s_lb, s_gt_hb, s_gt_t;
-  __shared__ int wcnt[kSelWaves];
-  __shared__ float r_bs[kSelWaves], r_mx[kSelWaves], r_sm[kSelWaves];
-  __shared__ int r_bi[kSelWaves];
+  __shared__ int s_nout;
+  __shared__ float s_score0;
+  __shared__ float r_bs[kSelWaves], r_mx[kSelWaves], r_sm[kSelWaves], r_ps[kSelWaves];
+  __shared__ int r_bi[kSelWaves], r_pk[kSelWaves];
   const SamplingParams p = params[r];
 
   // 1. merge the per-workgroup partials in order
   float bs = kNegInf, mx = kNegInf, sm = 0.0f;
   int bi = 0x7FFFFFFF;
   {
-    // thread i folds partials i, i + 1024, ... in order; then the threads
+    // thread i folds partials i, i + 256, ... in order; then the threads
     // fold in order through the waves
     for (int i = tid; i < nparts; i += kSelThreads) {
       const float* pp = part + (size_t)i * 4 * RP;
@@ -367,71 +577,10 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
     }
   }
 
-  // 2. top-n threshold by byte histograms of the bf16 keys
+  // 2. the selected candidates, padded and sorted descending by
+  // (key, -index): bitonic over 256 entries
   const int need = V < kSampleNmax ? V : kSampleNmax;
-  if (tid < 256) hist[tid] = 0;
-  if (tid == 0) cnt = 0;
-  __syncthreads();
-  for (int i = tid; i < V; i += kSelThreads) atomicAdd(&hist[bf16_key(y[i]) >> 8], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0, hb = 255;
-    for (; hb > 0; --hb) {
-      if (acc + (int)hist[hb] >= need) break;
-      acc += (int)hist[hb];
-    }
-    s_hb = hb;
-    s_gt_hb = acc;  // keys with a higher high byte
-  }
-  __syncthreads();
-  const uint32_t hb = (uint32_t)s_hb;
-  if (tid < 256) hist[tid] = 0;
-  __syncthreads();
-  for (int i = tid; i < V; i += kSelThreads) {
-    const uint32_t k = bf16_key(y[i]);
-    if ((k >> 8) == hb) atomicAdd(&hist[k & 255], 1u);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = s_gt_hb, lb = 255;
-    for (; lb > 0; --lb) {
-      if (acc + (int)hist[lb] >= need) break;
-      acc += (int)hist[lb];
-    }
-    s_lb = lb;
-    s_gt_t = acc;  // keys above the threshold key
-  }
-  __syncthreads();
-  const uint32_t thr_key = (hb << 8) | (uint32_t)s_lb;
-  const int ties_needed = need - s_gt_t;
-
-  // 3. collect: every key above the threshold, and the first ties_needed keys
-  // equal to it in vocabulary order
-  int eq_base = 0;
-  for (int c0 = 0; c0 < V; c0 += kSelThreads) {
-    const int i = c0 + tid;
-    const uint32_t k = i < V ? bf16_key(y[i]) : 0u;
-    const bool gt = i < V && k > thr_key;
-    const bool eq = i < V && k == thr_key;
-    const uint64_t m = __ballot(eq);
-    if (lane == 0) wcnt[wave] = __popcll(m);
-    __syncthreads();
-    int before = 0, total = 0;
-    for (int wv = 0; wv < kSelWaves; ++wv) {
-      const int cw = wcnt[wv];
-      before += wv < wave ? cw : 0;
-      total += cw;
-    }
-    const int rank = eq_base + before + __popcll(m & ((1ull << lane) - 1ull));
-    if (gt || (eq && rank < ties_needed)) {
-      const int pos = atomicAdd(&cnt, 1);
-      cand[pos] = ((uint64_t)k << 32) | (uint32_t)(0x7FFFFFFF - i);
-    }
-    eq_base += total;
-    __syncthreads();
-  }
-  // pad and sort descending by (key, -index): bitonic over 256 entries
-  if (tid < kSampleNmax && tid >= need) cand[tid] = 0ull;
+  if (tid < kSampleNmax) cand[tid] = tid < need ? cand_g[(size_t)r * kSampleNmax + tid] : 0ull;
   __syncthreads();
   for (int size = 2; size <= kSampleNmax; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -450,7 +599,44 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
     }
   }
 
-  // 4. finalize (flash_sample.mojo:232-265)
+  // 3. finalize (flash_sample.mojo:232-265).  The min_p / top_k pick scans
+  // the top list keeping the first strictly larger score among entries
+  // 1..limit-1 that pass the min_p threshold, starting from entry 0: that is
+  // entry 0 unless the best passing score M beats it, else the first entry
+  // scoring M -- a max / min-index reduction over the 256 entries.
+  const float inv_t = 1.0f / p.temperature;
+  const bool use_min_p = p.min_p > 0.0f, use_top_k = p.top_k > 0;
+  int limit = need;
+  if (use_top_k && p.top_k < limit) limit = (int)p.top_k;
+  const float v0 = bf16_to_f32(key_bf16((uint32_t)(cand[0] >> 32)));
+  const float thr = use_min_p ? v0 + p.temperature * log_f32(p.min_p) : kNegInf;
+  float sc = kNegInf;
+  int kk = 0x7FFFFFFF;
+  if (tid < need) {
+    const float yv = bf16_to_f32(key_bf16((uint32_t)(cand[tid] >> 32)));
+    const int64_t gi = vbase + (0x7FFFFFFF - (int)(uint32_t)cand[tid]);
+    const float g = p.greedy ? 0.0f : gumbel_noise(p.seed, r, gi);
+    const float score = yv * inv_t + g;
+    if (tid == 0) s_score0 = score;
+    if (tid >= 1 && tid < limit && yv >= thr) {
+      sc = score;
+      kk = tid;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float os = __shfl_xor(sc, o, 64);
+    const int ok = __shfl_xor(kk, o, 64);
+    if (os > sc || (os == sc && ok < kk)) {
+      sc = os;
+      kk = ok;
+    }
+  }
+  if (lane == 0) {
+    r_ps[wave] = sc;
+    r_pk[wave] = kk;
+  }
+  __syncthreads();
   if (tid == 0) {
     float fbs = kNegInf, fmx = kNegInf, fsm = 0.0f;
     int fbi = 0x7FFFFFFF;
@@ -458,41 +644,27 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
       samp_merge(fbs, fbi, r_bs[wv], r_bi[wv]);
       lse_merge(fmx, fsm, r_mx[wv], r_sm[wv]);
     }
-    const float inv_t = 1.0f / p.temperature;
     const int n = need;
     const int n_out = (int64_t)n < p.n_keep ? n : (int)p.n_keep;
     int token = fbi == 0x7FFFFFFF ? -1 : fbi;
-    const bool use_min_p = p.min_p > 0.0f, use_top_k = p.top_k > 0;
     if ((use_min_p || use_top_k) && n > 0) {
-      int limit = n;
-      if (use_top_k && p.top_k < limit) limit = (int)p.top_k;
-      const float v0 = bf16_to_f32(key_bf16((uint32_t)(cand[0] >> 32)));
-      const float thr = use_min_p ? v0 + p.temperature * log_f32(p.min_p) : kNegInf;
-      auto score_of = [&](int k) {
-        const float yv = bf16_to_f32(key_bf16((uint32_t)(cand[k] >> 32)));
-        const int64_t gi = vbase + (0x7FFFFFFF - (int)(uint32_t)cand[k]);
-        const float g = p.greedy ? 0.0f : gumbel_noise(p.seed, r, gi);
-        return yv * inv_t + g;
-      };
-      int best_k = 0;
-      float best_g = score_of(0);
-      for (int k = 1; k < limit; ++k) {
-        const float yv = bf16_to_f32(key_bf16((uint32_t)(cand[k] >> 32)));
-        const float gk = score_of(k);
-        if (yv >= thr && gk > best_g) {
-          best_g = gk;
-          best_k = k;
+      float best = kNegInf;
+      int bk = 0x7FFFFFFF;
+      for (int wv = 0; wv < kSelWaves; ++wv)
+        if (r_ps[wv] > best || (r_ps[wv] == best && r_pk[wv] < bk)) {
+          best = r_ps[wv];
+          bk = r_pk[wv];
         }
-      }
-      token = (int)(vbase + (0x7FFFFFFF - (int)(uint32_t)cand[best_k]));
+      const int pick = (bk != 0x7FFFFFFF && best > s_score0) ? bk : 0;
+      token = (int)(vbase + (0x7FFFFFFF - (int)(uint32_t)cand[pick]));
     }
     out[r].token_id = token;
     out[r].logz = fmx + log_f32(fsm);
     out[r].n = n_out;
-    s_lb = n_out;
+    s_nout = n_out;
   }
   __syncthreads();
-  const int n_out = s_lb;
+  const int n_out = s_nout;
   if (tid < kSampleNmax) {
     const bool keep = tid < n_out;
     out[r].topn_val[tid] = keep ? bf16_to_f32(key_bf16((uint32_t)(cand[tid] >> 32))) : kNegInf;
@@ -547,21 +719,41 @@ int head_grid(int vocab) {
   return g < 1024 ? g : 1024;
 }
 
-size_t head_workspace_bytes(int rows, int vocab) {
+struct HeadWs {
+  size_t y, part, hist1, hist2, thr, eqpre, cnt, cand, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static HeadWs head_ws_layout(int rows, int vocab) {
   const int RP = rows <= 16 ? 16 : 32;
-  const size_t y = ((size_t)rows * vocab * 2 + 255) & ~(size_t)255;
-  return y + (size_t)head_grid(vocab) * 4 * RP * sizeof(float);
+  const int nc = (vocab + kChunk - 1) / kChunk;
+  HeadWs w{};
+  size_t o = 0;
+  w.y = o; o = align256(o + (size_t)rows * vocab * 2);
+  w.part = o; o = align256(o + (size_t)head_grid(vocab) * 4 * RP * sizeof(float));
+  w.hist1 = o; o = align256(o + (size_t)rows * nc * 256 * 4);
+  w.hist2 = o; o = align256(o + (size_t)rows * nc * 256 * 4);
+  w.thr = o; o = align256(o + (size_t)rows * 4 * 4);
+  w.eqpre = o; o = align256(o + (size_t)rows * nc * 4);
+  w.cnt = o; o = align256(o + (size_t)rows * 4);
+  w.cand = o; o = align256(o + (size_t)rows * kSampleNmax * 8);
+  w.total = o;
+  return w;
 }
+
+size_t head_workspace_bytes(int rows, int vocab) { return head_ws_layout(rows, vocab).total; }
 
 hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* w, const float* ws,
                                const SamplingParams* params, SampleOutcome* out, int R, int V,
                                int H, int block, float cap, int64_t vbase, void* workspace,
                                hipStream_t st) {
+  const HeadWs L = head_ws_layout(R, V);
+  char* base = reinterpret_cast<char*>(workspace);
   HeadArgs a{};
   a.x = x; a.xsa = xsa; a.w = w; a.ws = ws; a.params = params;
-  a.y = reinterpret_cast<uint16_t*>(workspace);
-  a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
-                                    (((size_t)R * V * 2 + 255) & ~(size_t)255));
+  a.y = reinterpret_cast<uint16_t*>(base + L.y);
+  a.part = reinterpret_cast<float*>(base + L.part);
   a.R = R; a.V = V; a.H = H; a.block = block; a.nstrips = V / 16; a.cap = cap; a.vbase = vbase;
   const int grid = head_grid(V);
   const int RP = R <= 16 ? 16 : 32;
@@ -572,7 +764,24 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
     hipLaunchKernelGGL(k_head_logits<2>, dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_head_select, dim3(R), dim3(kSelThreads), 0, st, a.y, a.part, grid, RP,
+
+  SelArgs s{};
+  s.y = a.y;
+  s.hist1 = reinterpret_cast<uint32_t*>(base + L.hist1);
+  s.hist2 = reinterpret_cast<uint32_t*>(base + L.hist2);
+  s.thr = reinterpret_cast<int*>(base + L.thr);
+  s.eqpre = reinterpret_cast<int*>(base + L.eqpre);
+  s.cnt = reinterpret_cast<int*>(base + L.cnt);
+  s.cand = reinterpret_cast<uint64_t*>(base + L.cand);
+  s.V = V;
+  s.nc = (V + kChunk - 1) / kChunk;
+  const dim3 cg(s.nc, R), cb(kChunkThreads);
+  hipLaunchKernelGGL(k_sel_hist_hi, cg, cb, 0, st, s);
+  hipLaunchKernelGGL(k_sel_thr_hi, dim3(R), cb, 0, st, s);
+  hipLaunchKernelGGL(k_sel_hist_lo, cg, cb, 0, st, s);
+  hipLaunchKernelGGL(k_sel_thr_lo, dim3(R), cb, 0, st, s);
+  hipLaunchKernelGGL(k_sel_collect, cg, cb, 0, st, s);
+  hipLaunchKernelGGL(k_head_select, dim3(R), dim3(kSelThreads), 0, st, s.cand, a.part, grid, RP,
                      params, out, V, vbase);
   return hipGetLastError();
 }
