@@ -41,17 +41,18 @@ struct TiledArgs {
   int order;                // MoE work order (0: n-tile fastest, 1: XCD ranges, 2: m-tile per XCD)
 };
 
-// Wait until at most n (< 64) of this wave's vector memory loads are
-// outstanding; n is wave-uniform, s_waitcnt takes an immediate.
-__device__ inline void wait_vm(int n) {
-  switch (n) {
-#define BQ_VM1(k) case k: asm volatile("s_waitcnt vmcnt(%0)" :: "n"(k) : "memory"); break;
-#define BQ_VM8(k) BQ_VM1(k) BQ_VM1(k + 1) BQ_VM1(k + 2) BQ_VM1(k + 3) BQ_VM1(k + 4) \
-                  BQ_VM1(k + 5) BQ_VM1(k + 6) BQ_VM1(k + 7)
-    BQ_VM8(1) BQ_VM8(9) BQ_VM8(17) BQ_VM8(25) BQ_VM8(33) BQ_VM8(41) BQ_VM8(49)
-    BQ_VM1(57) BQ_VM1(58) BQ_VM1(59) BQ_VM1(60) BQ_VM1(61) BQ_VM1(62) BQ_VM1(63)
-#undef BQ_VM8
-#undef BQ_VM1
+// Wait until at most `later` stages of this wave's fragment DMAs (D each)
+// are outstanding: s_waitcnt takes an immediate, so dispatch on the count.
+template <int D, int NBUF>
+__device__ inline void wait_dma(int later) {
+  static_assert((NBUF - 2) * D <= 63, "vmcnt field holds 6 bits");
+  switch (later) {
+#define BQ_WAIT_CASE(n) \
+    case n: if constexpr (n <= NBUF - 2) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(n * D) : "memory"); break; }
+    BQ_WAIT_CASE(12) BQ_WAIT_CASE(11) BQ_WAIT_CASE(10) BQ_WAIT_CASE(9) BQ_WAIT_CASE(8)
+    BQ_WAIT_CASE(7) BQ_WAIT_CASE(6) BQ_WAIT_CASE(5) BQ_WAIT_CASE(4)
+    BQ_WAIT_CASE(3) BQ_WAIT_CASE(2) BQ_WAIT_CASE(1)
+#undef BQ_WAIT_CASE
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 }
@@ -150,13 +151,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
   const bool odd = K64 & 1;
 
   // ---- this wave's DMAs: DMA wave + NW*d, d < D (or D - 1) ---------------
-  // A slot is live unless all its rows lie past the tile's last record (A)
-  // or its 16 weight rows lie past N (B): a dead slot's LDS bytes feed only
-  // outputs that are never stored, so its DMA is not issued.  Liveness does
-  // not depend on the stage, so every stage issues the same nd DMAs.
   const int8_t* src[D];
   int dst_off[D];
-  bool is_a[D], hi[D], live[D];  // hi: reads the second k-step of the stage
+  bool is_a[D], hi[D];  // hi: reads the second k-step of the stage
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int f = min(wave + NW * d, FA + FB - 1);  // the clamped slot is never issued
@@ -172,7 +169,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
       dst_off[d] = f * 1024;
       is_a[d] = true;
       hi[d] = c >= 4;
-      live[d] = f * 8 < r1 - r0;
     } else {
       const int g = f - FA;
       const int ks = g & 1, nsub = g >> 1;
@@ -194,14 +190,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
       dst_off[d] = g * 1024;
       is_a[d] = false;
       hi[d] = ks == 1;
-      live[d] = ok;
     }
   }
-  int nd_ = 0;
-#pragma unroll
-  for (int d = 0; d < D; ++d) nd_ += (live[d] && (d < D - 1 || full_d)) ? 1 : 0;
-  const int nd = __builtin_amdgcn_readfirstlane(nd_);
-  static_assert((NBUF - 2) * D <= 63, "vmcnt field holds 6 bits");
 
   if constexpr (PER_BLOCK) {
     const float* sc = MODE == MODE_DENSE ? args.lin.sa : args.a_scale;
@@ -219,7 +209,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       if (d == D - 1 && !full_d) break;
-      if (!live[d]) continue;
       // stage st starts at K byte 128*st (A) / fragment 2*st (B); in a
       // one-step tail stage the second-half reads fall back to the first half
       const int back = (odd && st == tail && hi[d]) ? (is_a[d] ? 64 : 1024) : 0;
@@ -305,7 +294,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
   const bool busy = wm * MI * 16 < r1 - r0;
 
   auto compute = [&](const int8_t* abuf, const int8_t* bbuf, int st) {
-    if (!busy) return;
+    if constexpr (MODE != MODE_DENSE) {
+      if (!busy) return;
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == 1 && odd && st == tail) break;
@@ -355,7 +346,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tiled(TiledArgs args) {
       const int s = s0 + i;
       if (s >= nstages) break;
       const int later = min(NBUF - 2, nstages - 1 - s);
-      wait_vm(later * nd);
+      if (full_d) wait_dma<D, NBUF>(later);
+      else wait_dma<D - 1, NBUF>(later);
       lds_barrier();
       if (s + NBUF - 1 < nstages) issue(abuf_[(i + NBUF - 1) % NBUF], bbuf_[(i + NBUF - 1) % NBUF], s + NBUF - 1);
       compute(abuf_[i], bbuf_[i], s);
