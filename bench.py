@@ -33,6 +33,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, published (no sparsity)
 BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, published
 H, I, E, TOPK = 2816, 704, 128, 8   # Gemma-4-26B-A4B (modeling/gemma4_common.mojo)
+MOE_LAYERS = []  # the timed MoE layers (inputs reused by the CPU baseline leg)
 
 
 def parse():
@@ -228,6 +229,7 @@ def bench_moe(bq, torch, T, weights, steps):
     between them so each step's ~0.7 GB of experts is not resident in the
     256 MB Infinity Cache from the previous step."""
     layers = [MoeLayer(bq, torch, T, Wgu, Wd) for Wgu, Wd in weights]
+    MOE_LAYERS.append(layers[0])
     g = graph_of(lambda i: layers[i](), len(layers))
     ms, wall, n = time_graph(g, len(layers), steps, max(3, steps // 8))
     layer = layers[0]
@@ -344,6 +346,72 @@ def cpu_baseline_gemv(codes, scales, seconds):
                        f"{med * 1e6:.1f} us; ISA {lib.bqcpu_isa().decode()}")
 
 
+def cpu_baseline_moe(bq, torch, Wgu, Wd, layers, seconds):
+    """The reference CPU path of the MoE layer (router top-k + softmax merge,
+    CSR schedule, norm-quant, phase 1 over intermediate tiles, FWHT64
+    block-quant, phase 2 over hidden tiles; VNNI u8 x i8 with colsums) from
+    oracle/cpu_baseline.c and the oracle's router / schedule, on the host
+    cores, for each MoeLayer's inputs; bounded to about `seconds` per T."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    lib = O.cpu()
+    nthreads = max(1, min(16, os.cpu_count() or 1))
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+    gu = bq.unpack(Wgu.data, Wgu.n_rows, Wgu.k).cpu().numpy().reshape(Wgu.n_rows, Wgu.k)
+    dn = bq.unpack(Wd.data, Wd.n_rows, Wd.k).cpu().numpy().reshape(Wd.n_rows, Wd.k)
+    gp, gcs = O.pack_and_colsum(gu)
+    dp, dcs = O.pack_and_colsum(dn, 64, False)
+    del gu, dn
+    gsc = Wgu.scale.cpu().numpy()
+    dsc = Wd.scale.cpu().numpy()
+    sqrt_n, n_eps = O.norm_consts(H)
+    res = {}
+    for layer in layers:
+        T = layer.T
+        x = layer.x.view(torch.int16).cpu().numpy().view(np.uint16)
+        logits = layer.logits.cpu().numpy()
+        gamma = np.full(H, 0x3F80, np.uint16)
+        pes = np.full(E, 0x3F80, np.uint16)
+        xq = np.empty((T, H), np.int8)
+        xsa = np.empty(T, np.float32)
+        bucket = np.empty((T * TOPK, I), np.uint16)
+        bi8 = np.empty((T * TOPK, I), np.int8)
+        bsa = np.empty((T * TOPK, I // 64), np.float32)
+        accum = np.empty((T, H), np.float32)
+        out = np.empty((T, H), np.uint16)
+
+        def call():
+            idx, w = O.route_topk_softmax(logits, TOPK, pes)
+            eo, routes = O.build_schedule(idx, w, E)
+            lib.bqcpu_norm_quant(ptr(x), ptr(gamma), ptr(xq), ptr(xsa), T, H, 128,
+                                 C.c_float(sqrt_n), C.c_float(n_eps), nthreads)
+            lib.bqcpu_moe_phase1(ptr(xq), ptr(xsa), H, ptr(eo), ptr(routes), E, ptr(gp), ptr(gsc),
+                                 ptr(gcs), I, ptr(bucket), nthreads)
+            lib.bqcpu_block_quant(ptr(bucket), ptr(bi8), ptr(bsa), T * TOPK, I, 64, 1, nthreads)
+            lib.bqcpu_moe_phase2(ptr(bi8), ptr(bsa), I, 64, ptr(eo), ptr(routes), E, T, ptr(dp),
+                                 ptr(dsc), ptr(dcs), H, ptr(accum), ptr(out), nthreads)
+
+        call()
+        ts = []
+        t_end = time.perf_counter() + seconds
+        while (time.perf_counter() < t_end and len(ts) < 600) or len(ts) < 2:
+            t0 = time.perf_counter()
+            call()
+            ts.append(time.perf_counter() - t0)
+        med = float(np.median(ts))
+        res[f"T{T}"] = {"tokens_per_s": round(T / med, 1), "ms": round(med * 1e3, 3),
+                        "samples": len(ts)}
+    res.update(unit="tokens/s", cores=nthreads, kind="port",
+               sample=f"MoE layer from router logits, 128 experts, top-8, H={H}, I={I}; "
+                      f"median of the calls in ~{seconds:.0f} s per T after one warm call; "
+                      f"ISA {lib.bqcpu_isa().decode()}")
+    return res
+
+
 def calib_copy(torch):
     """A plain device copy of 256 MiB (the PMC calibration kernel)."""
     a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -370,6 +438,7 @@ def main():
         res["prefill"] = bench_prefill(bq, torch, args.steps, args.warmup)
     if wl in ("all", "moe32", "moe2048", "layer16"):
         Wgu, Wd = moe_weights(bq, torch)
+        moe_w = (Wgu, Wd)
         reps = [(Wgu, Wd), tuple(bq.ButterquantWeight(w.data.clone(), w.scale, w.n_rows, w.k)
                                  for w in (Wgu, Wd))]
         if wl in ("all", "moe32"):
@@ -435,6 +504,9 @@ def main():
     if "gemv" in res and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_gemv(res["gemv"]["codes"], res["gemv"]["scales"],
                                                  args.cpu_seconds)
+    if MOE_LAYERS and not args.no_cpu:
+        line["cpu_baseline_moe"] = cpu_baseline_moe(bq, torch, *moe_w, MOE_LAYERS,
+                                                    args.cpu_seconds / 2)
     print(json.dumps(line))
 
 
