@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16", "head"])
+                    choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16", "head",
+                             "load"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
@@ -215,6 +216,43 @@ def bench_head(bq, torch, steps, rows_list=(1, 16)):
         ms, wall, n = time_graph(g, 4, max(8, steps // 64), 4)
         out[R] = dict(ms=ms, gbs=alg / (ms * 1e-3) / 1e9)
     return dict(alg_bytes=alg, rows=out)
+
+
+def bench_load(bq, torch):
+    """The on-disk -> device path on the MoE gate/up tensor (128 experts x
+    1408 x 2816 int8 + per-row scales, 507 MB) written as a safetensors file
+    under $TMPDIR: bq_load_quantized (mmap, validate, host -> device copy
+    through a 64 MiB staging buffer, re-tile), file in the page cache.
+    Opt-in (--workload load): it writes a 0.5 GB file."""
+    import tempfile
+
+    import numpy as np
+    from safetensors.numpy import save_file
+    n, k = E * 2 * I, H
+    rng = np.random.default_rng(0)
+    codes = rng.integers(-127, 128, (E, 2 * I, k), dtype=np.int8)
+    scales = rng.random((E, 2 * I)).astype(np.float32)
+    d = tempfile.mkdtemp()
+    path = os.path.join(d, "experts.safetensors")
+    save_file({"experts.gate_up": codes, "experts.gate_up.scale": scales.reshape(-1)}, path)
+    f = bq.SafetensorsFile(path)
+    staging = torch.empty(64 << 20, dtype=torch.int8, device="cuda")
+    w = torch.empty(n * k, dtype=torch.int8, device="cuda")
+    s = torch.empty(n, dtype=torch.float32, device="cuda")
+    ts = []
+    for _ in range(6):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        bq.load_quantized([f], "experts.gate_up", n, k, staging=staging, out=(w, s))
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    ok = bool((bq.unpack(w[: 16 * k], 16, k).cpu().numpy().reshape(16, k) ==
+               codes.reshape(n, k)[:16]).all())
+    f.close()
+    os.remove(path)
+    os.rmdir(d)
+    med = float(np.median(ts[1:]))
+    return dict(ms=med * 1e3, gbs=(n * k + n * 4) / med / 1e9, checked=ok)
 
 
 def moe_weights(bq, torch):
@@ -449,6 +487,8 @@ def main():
             res["layer16"] = bench_layer16(bq, torch, Wgu, Wd, max(10, args.steps // 32))
     if wl in ("all", "head"):
         res["head"] = bench_head(bq, torch, args.steps)
+    if wl == "load":
+        res["load"] = bench_load(bq, torch)
     if args.calib_copy:
         calib_copy(torch)
 
@@ -494,6 +534,11 @@ def main():
                 "int8_tops": round(m["ops"] / (m["ms"] * 1e-3) / 1e12, 1)}
     if "layer16" in res:
         line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()}
+    if "load" in res:
+        ld = res["load"]
+        line["load_safetensors_gate_up_507MB"] = {"ms": round(ld["ms"], 2),
+                                                  "GBs": round(ld["gbs"], 2),
+                                                  "checked": ld["checked"]}
     if "head" in res:
         hd = res["head"]
         line["head_flash_sample_v262144"] = {

@@ -263,6 +263,54 @@ int bq_embed_lookup(const int32_t* token_ids, const int8_t* weight, const float*
                     uint16_t* dst, int seq_len, int hidden, int block, int shard_rows, int rank,
                     float scale, void* stream);
 
+/* ---- on-disk weights (safetensors) -------------------------------------------- */
+
+/* safetensors dtype tags (safetensors/parser.mojo:19-54) */
+#define BQ_DT_BOOL 0
+#define BQ_DT_U8 1
+#define BQ_DT_I8 2
+#define BQ_DT_I16 3
+#define BQ_DT_U16 4
+#define BQ_DT_F16 5
+#define BQ_DT_BF16 6
+#define BQ_DT_I32 7
+#define BQ_DT_U32 8
+#define BQ_DT_F32 9
+#define BQ_DT_F64 10
+#define BQ_DT_F8_E4M3 11
+#define BQ_DT_F8_E5M2 12
+#define BQ_DT_I64 13
+#define BQ_DT_U64 14
+
+/* A memory-mapped safetensors shard (host). */
+typedef struct bq_st_file bq_st_file;
+
+/* parse_safetensors_header (safetensors/parser.mojo:270-320) on a mapped
+ * file: the same validation (header <= 100 MiB, required fields, supported
+ * dtypes, byte size = dtype size x numel, offsets inside the payload, no
+ * overlapping ranges or duplicate names, payload fully indexed, no trailing
+ * content); BQ_ERR_INVALID with the reason otherwise.  Host only. */
+int bq_st_open(const char* path, bq_st_file** out);
+void bq_st_close(bq_st_file* f);
+int bq_st_num_tensors(const bq_st_file* f);
+/* Metadata of one tensor (shape: up to 8 dims) and a host pointer to its
+ * bytes inside the mapping; BQ_ERR_INVALID "missing tensor" if absent. */
+int bq_st_tensor_info(const bq_st_file* f, const char* name, int* dtype, int* ndim,
+                      int64_t* shape, size_t* nbytes, const void** host_data);
+
+/* Load one quantized weight straight from its on-disk members
+ * (quant/manifest.mojo:69-199: int8 codes "<name>" row-major [n_rows, k],
+ * f32 scales "<name>.scale" [n_rows] (scale_cols = 1) or [n_rows,
+ * scale_cols]) located across shards (modeling/loader.mojo:151-186) and
+ * validated like validate_weight (loader.mojo:52-96: dtype, 1-D / 2-D / 3-D
+ * folded shapes), into device buffers: codes re-tiled to tile16x64 through a
+ * device staging buffer of at least 16*k bytes (whole 16-row strips per
+ * chunk), scales copied as they are.  Replaces the loader's host reads plus
+ * the VNNI pack at init.  n_rows % 16 == 0, k % 64 == 0. */
+int bq_load_quantized(const bq_st_file* const* files, int n_files, const char* name, int n_rows,
+                      int k, int scale_cols, int8_t* w_tiled, float* scales, int8_t* staging,
+                      size_t staging_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,13 @@ SIGNATURES = {
     "bq_flash_sample": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, C.c_int64, _vp, _sz,
                         _vp],
     "bq_embed_lookup": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp],
+    "bq_st_open": [C.c_char_p, C.POINTER(C.c_void_p)],
+    "bq_st_close": [_vp],
+    "bq_st_num_tensors": [_vp],
+    "bq_st_tensor_info": [_vp, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                          C.POINTER(C.c_int64), C.POINTER(C.c_size_t), C.POINTER(C.c_void_p)],
+    "bq_load_quantized": [C.POINTER(C.c_void_p), _i, C.c_char_p, _i, _i, _i, _vp, _vp, _vp, _sz,
+                          _vp],
     "bq_moe_phase1_gate_up": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "bq_moe_phase2_workspace_size": [_i, _i, _i],
     "bq_moe_phase2_down": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
@@ -56,7 +63,7 @@ SIGNATURES = {
 }
 _RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
              "bq_moe_phase2_workspace_size": C.c_size_t,
-             "bq_flash_sample_workspace_size": C.c_size_t}
+             "bq_flash_sample_workspace_size": C.c_size_t, "bq_st_close": None}
 
 
 def _load():
@@ -404,3 +411,60 @@ def embed_lookup(token_ids: torch.Tensor, weight: ButterquantWeight, wscales: to
     _check(_lib.bq_embed_lookup(_p(token_ids), _p(weight.data), _p(wscales), _p(out), t, h, block,
                                 shard_rows, rank, scale, _stream()))
     return out
+
+
+# --------------------------------------------------------------------------
+# on-disk weights (safetensors)
+# --------------------------------------------------------------------------
+DT_NAMES = ["BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "F64",
+            "F8_E4M3", "F8_E5M2", "I64", "U64"]
+
+
+class SafetensorsFile:
+    """A memory-mapped safetensors shard parsed by libbq (host only)."""
+
+    handle = None
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        _check(_lib.bq_st_open(os.fsencode(path), C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            _lib.bq_st_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def __len__(self):
+        return _lib.bq_st_num_tensors(self.handle)
+
+    def info(self, name: str):
+        """-> (dtype tag, shape, nbytes, host address)."""
+        dt, nd = C.c_int(), C.c_int()
+        shape = (C.c_int64 * 8)()
+        nbytes, data = C.c_size_t(), C.c_void_p()
+        _check(_lib.bq_st_tensor_info(self.handle, name.encode(), C.byref(dt), C.byref(nd), shape,
+                                      C.byref(nbytes), C.byref(data)))
+        return DT_NAMES[dt.value], tuple(shape[i] for i in range(nd.value)), nbytes.value, data.value
+
+
+def load_quantized(files, name: str, n_rows: int, k: int, scale_cols: int = 1,
+                   staging: torch.Tensor | None = None, out=None) -> ButterquantWeight:
+    """bq_load_quantized: codes "<name>" + scales "<name>.scale" from the
+    shards -> ButterquantWeight (tile16x64 codes, f32 scales) on the device."""
+    arr = (C.c_void_p * len(files))(*[f.handle for f in files])
+    if staging is None:
+        staging = torch.empty(min(n_rows * k, 64 << 20) // (16 * k) * 16 * k or 16 * k,
+                              dtype=torch.int8, device="cuda")
+    if out is None:
+        w = torch.empty(n_rows * k, dtype=torch.int8, device="cuda")
+        s = torch.empty((n_rows,) if scale_cols == 1 else (n_rows, scale_cols), dtype=torch.float32,
+                        device="cuda")
+    else:
+        w, s = out
+    _check(_lib.bq_load_quantized(arr, len(files), name.encode(), n_rows, k, scale_cols, _p(w),
+                                  _p(s), _p(staging), staging.numel(), _stream()))
+    return ButterquantWeight(w, s, n_rows, k)

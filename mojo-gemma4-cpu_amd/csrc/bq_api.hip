@@ -36,6 +36,14 @@ inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) =
 
 }  // namespace
 
+namespace bq {
+// the shared last-error slot, for entry points defined in other files
+int api_failv(int code, const char* fmt, va_list ap) {
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  return code;
+}
+}  // namespace bq
+
 extern "C" {
 
 const char* bq_version(void) { return "bq-mi355x 0.1 (gfx950)"; }

@@ -2,6 +2,8 @@
 // (internal to the library; the public C ABI is include/bq_api.h).
 #pragma once
 
+#include <stdarg.h>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -89,6 +91,7 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
                                const SamplingParams* params, SampleOutcome* out, int R, int V,
                                int H, int block, float cap, int64_t vbase, void* workspace,
                                hipStream_t st);
+int api_failv(int code, const char* fmt, va_list ap);  // sets bq_last_error()
 hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const uint16_t* rscale,
                                 float* logits, int T, int H, int E, float sqrt_n, float n_eps,
                                 hipStream_t st);
