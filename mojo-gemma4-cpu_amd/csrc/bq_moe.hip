@@ -192,8 +192,11 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 
 // Phase 2 GEMM: y[rec, n] = (facc * ws[n]) * route_w[rec] with facc the fma
 // chain over K blocks (moe.mojo:198-223).  The m-tile's per-block activation
-// scales (16 records x K/block <= 64) are staged in LDS up front.
-template <int U>
+// scales (16 records x K/block <= 64) are staged in LDS up front.  A wave
+// owns NS 16-row strips of the output: the records' activation fragments
+// are loaded once per k-step for all of them, and NS weight fragments per
+// k-step are in flight.
+template <int U, int NS>
 __global__ __launch_bounds__(256) void k_moe_down_skinny(
     const int8_t* __restrict__ b_i8, const float* __restrict__ b_sa,
     const int32_t* __restrict__ eo, const Route* __restrict__ routes,
@@ -209,14 +212,19 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
   }
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
-  const int nsub = blockIdx.x * 4 + wave;
-  if (nsub * 16 >= hidden) return;
-  const int8_t* wb = w_d + (size_t)e * hidden * K + (size_t)nsub * K64 * 1024 + lane * 16;
+  const int nsub0 = (blockIdx.x * 4 + wave) * NS;
+  const int nstrips = hidden / 16;
+  if (nsub0 >= nstrips) return;
+  const int8_t* wb[NS];
+  float wsc[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int ns = min(nsub0 + j, nstrips - 1);  // a strip past the end is never stored
+    wb[j] = w_d + (size_t)e * hidden * K + (size_t)ns * K64 * 1024 + lane * 16;
+    wsc[j] = d_scale[(size_t)e * hidden + ns * 16 + (lane & 15)];
+  }
   const int arow = r0 + (lane & 15);
   const int8_t* ab = b_i8 + (size_t)(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
-  // epilogue operands and per-block scales
-  const int col = nsub * 16 + (lane & 15);
-  const float wsc = d_scale[(size_t)e * hidden + col];
   float rw[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -224,14 +232,22 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
     rw[v] = routes[rec < r1 ? rec : r0].weight;
   }
   const v4i zero = {0, 0, 0, 0};
-  float facc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  v4i c = zero;
-  v4i bf[2][U], af[2][U];
+  float facc[NS][4];
+  v4i c[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    c[j] = zero;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) facc[j][v] = 0.0f;
+  }
+  v4i bf[2][NS][U], af[2][U];
   auto load = [&](int s, int ch) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kt = min(ch * U + u, K64 - 1);
-      bf[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)kt * 1024));
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        bf[s][j][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb[j] + (size_t)kt * 1024));
       af[s][u] = ld16(ab + kt * 64);
     }
   };
@@ -240,14 +256,18 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
     for (int u = 0; u < U; ++u) {
       const int kt = ch * U + u;
       if (kt < K64) {
-        c = mfma16x16x64(af[s][u], bf[s][u], c);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) c[j] = mfma16x16x64(af[s][u], bf[s][j][u], c[j]);
         if (((kt + 1) & (fpb - 1)) == 0) {
           const int b = kt / fpb;
-          const int cc[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            facc[v] = fmaf((float)cc[v], s_sa[(4 * (lane >> 4) + v) * nb + b], facc[v]);
-          c = zero;
+          for (int j = 0; j < NS; ++j) {
+            const int cc[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              facc[j][v] = fmaf((float)cc[v], s_sa[(4 * (lane >> 4) + v) * nb + b], facc[j][v]);
+            c[j] = zero;
+          }
         }
       }
     }
@@ -262,10 +282,15 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
     mul(1, ch + 1);
   }
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int rec = r0 + 4 * (lane >> 4) + v;
-    if (rec >= r1) continue;
-    y[(size_t)rec * hidden + col] = facc[v] * wsc * rw[v];
+  for (int j = 0; j < NS; ++j) {
+    if (nsub0 + j >= nstrips) continue;
+    const int col = (nsub0 + j) * 16 + (lane & 15);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rec = r0 + 4 * (lane >> 4) + v;
+      if (rec >= r1) continue;
+      y[(size_t)rec * hidden + col] = facc[j][v] * wsc[j] * rw[v];
+    }
   }
 }
 
@@ -405,8 +430,8 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
-      dim3 g((hidden / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
-      hipLaunchKernelGGL(k_moe_down_skinny<4>, g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
+      dim3 g((hidden / 16 + 7) / 8, mtile_bound(max_routes, experts, 16)), b(256);
+      hipLaunchKernelGGL((k_moe_down_skinny<4, 2>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
                          w_down, down_scale, y, experts, hidden, inter, block, max_routes);
     }
   }
