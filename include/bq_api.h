@@ -263,6 +263,90 @@ int bq_embed_lookup(const int32_t* token_ids, const int8_t* weight, const float*
                     uint16_t* dst, int seq_len, int hidden, int block, int shard_rows, int rank,
                     float scale, void* stream);
 
+/* ---- int8-KV attention -------------------------------------------------------- */
+
+/* One run of buffer rows that share a page table (kernels/attention_ops.mojo:
+ * 54-58 KVRun): rows [buf_start, next run's buf_start) hold positions
+ * base_pos, base_pos + 1, ...; page j of the run is physical row base
+ * base_rows[rows_off + j].  Device arrays: the KVRunTable's runs and
+ * base_rows lists (attention_ops.mojo:61-91) copied as they are. */
+typedef struct {
+    int32_t buf_start, base_pos, rows_off, page_count;
+} bq_kv_run;
+
+/* dispatch_bq_attn_prep[head_dim, rope_half, pair_stride, sqrt_n, n_eps]
+ * (butterquant_kernels/attention.mojo:537-583; BqAttnPrepKernel 474-534,
+ * prep_head_qk_i8 / prep_head_v_i8 butterquant/head_prep.mojo:39-92): per
+ * token (position = run.base_pos + row - run.buf_start) and q head: per-head
+ * RMS (sqrt_n / sqrt(ssq + n_eps)) x q_norm, RoPE (cos/sin_table
+ * [position, rope_half] on pairs (i, pair_stride + i), i < rope_half), FWHT
+ * (head_dim), absmax int8 -> q_i8 [seq_len, num_q*head_dim], qi_bias =
+ * 128 * sum(codes), f_q = amax [seq_len, num_q].  K heads (k_norm, RoPE) and V
+ * heads (no gain, no RoPE) the same way into the paged caches
+ * (k_cache/v_cache [slots, num_kv*head_dim] int8, k_scale/v_scale
+ * [slots, num_kv]) at slot base_rows[rows_off + ((p >> page_shift) &
+ * page_mask)] + (p & row_mask), p = position / cache_degree, for positions
+ * with position % cache_degree == rank.  v_src may equal k_src (K = V
+ * layers).  cos/sin_table may be NULL when rope_half is 0.  head_dim in
+ * {64, 128, 256, 512}; rope_half and pair_stride
+ * multiples of 64 with rope_half <= pair_stride, pair_stride + rope_half <=
+ * head_dim. */
+int bq_attn_prep(const uint16_t* q_src, const uint16_t* k_src, const uint16_t* v_src,
+                 const uint16_t* q_norm, const uint16_t* k_norm, int8_t* q_i8, float* qi_bias,
+                 float* f_q, int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                 const float* cos_table, const float* sin_table, const bq_kv_run* runs,
+                 int num_runs, const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                 int rope_half, int pair_stride, float sqrt_n, float n_eps, int cache_degree,
+                 int rank, int page_shift, int row_mask, int page_mask, int seq_len,
+                 void* stream);
+
+/* The split count s_max the attention entry points are sized for: each
+ * token's KV range of L positions is cut into min(s_max, ceil(L / 32))
+ * contiguous parts (worker_range, kernels/helpers.mojo:182-190) processed in
+ * parallel and merged in order.  max_kv_len: the longest range any token
+ * has (the window for sliding layers). */
+int bq_attention_splits(int seq_len, int num_kv, int max_kv_len);
+
+/* Bytes of device workspace the attention entry points need for s_max
+ * splits (f32 partials [seq_len, num_q, s_max] x (head_dim + 2)). */
+size_t bq_attention_workspace_size(int seq_len, int num_q, int head_dim, int s_max);
+
+/* dispatch_bq_sliding_attention[head_dim, max_q, gqa_ratio, window,
+ * cache_size, page_len] (butterquant_kernels/attention.mojo:330-403; decode
+ * kernel 83-146, sliding prefill 149-247, bq_process_kv_tile 32-80): per
+ * token and q head h (kv head h / (num_q/num_kv)), softmax attention over the
+ * cached positions [max(0, pos - window + 1), pos]: score =
+ * (f32(sum (k ^ 0x80) * q) - qi_bias) * f_q * ks / 127^2, tiles of 16
+ * positions with online_softmax_tile (kernels/attention_ops.mojo:166-182),
+ * acc += (w * vs / 127) * v; output bf16 [seq_len, num_q*head_dim] =
+ * acc / l (zeros if l = 0), or the logsum merge of the splits
+ * (kernels/logsum_merge.mojo:29-122).  Page addressing as bq_attn_prep with
+ * p = position.  num_q % num_kv == 0 with num_q/num_kv in {1, 2, 4, 8, 16};
+ * head_dim in {64, 128, 256, 512}; q_i8, k_cache, v_cache 16-byte aligned;
+ * workspace >= bq_attention_workspace_size(seq_len, num_q, head_dim, s_max),
+ * 16-byte aligned. */
+int bq_sliding_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                         const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                         const float* v_scale, uint16_t* output, void* workspace,
+                         size_t workspace_bytes, const bq_kv_run* runs, int num_runs,
+                         const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                         int window, int page_shift, int row_mask, int page_mask, int s_max,
+                         int seq_len, void* stream);
+
+/* dispatch_bq_full_attention[head_dim, num_q, num_kv, gqa_ratio, kv_stride,
+ * partial_stride, page_len] (butterquant_kernels/attention.mojo:406-471; full
+ * prefill 250-327) at one cache rank: every token attends to positions
+ * [0, pos]; the per-token result goes through the logsum merge as the
+ * reference's does.  Same layout and limits as bq_sliding_attention
+ * (page_mask -1 for an unbounded page table). */
+int bq_full_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                      const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                      const float* v_scale, uint16_t* output, void* workspace,
+                      size_t workspace_bytes, const bq_kv_run* runs, int num_runs,
+                      const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                      int page_shift, int row_mask, int page_mask, int s_max, int seq_len,
+                      void* stream);
+
 /* ---- on-disk weights (safetensors) -------------------------------------------- */
 
 /* safetensors dtype tags (safetensors/parser.mojo:19-54) */

@@ -49,6 +49,11 @@ SIGNATURES = {
     "bq_flash_sample": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, C.c_int64, _vp, _sz,
                         _vp],
     "bq_embed_lookup": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp],
+    "bq_attn_prep": [_vp] * 15 + [_i, _vp] + [_i] * 5 + [_f, _f] + [_i] * 6 + [_vp],
+    "bq_attention_splits": [_i, _i, _i],
+    "bq_attention_workspace_size": [_i, _i, _i, _i],
+    "bq_sliding_attention": [_vp] * 9 + [_sz, _vp, _i, _vp] + [_i] * 9 + [_vp],
+    "bq_full_attention": [_vp] * 9 + [_sz, _vp, _i, _vp] + [_i] * 8 + [_vp],
     "bq_st_open": [C.c_char_p, C.POINTER(C.c_void_p)],
     "bq_st_close": [_vp],
     "bq_st_num_tensors": [_vp],
@@ -63,7 +68,8 @@ SIGNATURES = {
 }
 _RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
              "bq_moe_phase2_workspace_size": C.c_size_t,
-             "bq_flash_sample_workspace_size": C.c_size_t, "bq_st_close": None}
+             "bq_flash_sample_workspace_size": C.c_size_t, "bq_st_close": None,
+             "bq_attention_workspace_size": C.c_size_t}
 
 
 def _load():
@@ -411,6 +417,81 @@ def embed_lookup(token_ids: torch.Tensor, weight: ButterquantWeight, wscales: to
     _check(_lib.bq_embed_lookup(_p(token_ids), _p(weight.data), _p(wscales), _p(out), t, h, block,
                                 shard_rows, rank, scale, _stream()))
     return out
+
+
+# --------------------------------------------------------------------------
+# int8-KV attention
+# --------------------------------------------------------------------------
+def attn_prep(q_src, k_src, v_src, q_norm, k_norm, k_cache, k_scale, v_cache, v_scale,
+              cos_table, sin_table, runs, base_rows, num_q: int, num_kv: int, head_dim: int,
+              rope_half: int, pair_stride: int, page_shift: int, row_mask: int,
+              page_mask: int, sqrt_n: float | None = None, n_eps: float | None = None,
+              cache_degree: int = 1, rank: int = 0, out=None):
+    """dispatch_bq_attn_prep -> (q_i8 [T, num_q*hd], qi_bias [T, num_q],
+    f_q [T, num_q]); K/V rows and scales are written into the caches.
+    runs: int32 [num_runs, 4] (buf_start, base_pos, rows_off, page_count)."""
+    for t in (q_src, k_src, v_src, q_norm, k_norm):
+        _dev(t, torch.bfloat16)
+    for t in (k_cache, v_cache):
+        _dev(t, torch.int8)
+    for t in (k_scale, v_scale, cos_table, sin_table):
+        _dev(t, torch.float32)
+    _dev(runs, torch.int32)
+    _dev(base_rows, torch.int32)
+    T = q_src.shape[0]
+    if sqrt_n is None:
+        import numpy as np
+        sqrt_n = float(np.sqrt(np.float32(head_dim), dtype=np.float32))
+        n_eps = float(np.float32(head_dim) * np.float32(1e-6))
+    if out is None:
+        d = q_src.device
+        out = (torch.empty((T, num_q * head_dim), dtype=torch.int8, device=d),
+               torch.empty((T, num_q), dtype=torch.float32, device=d),
+               torch.empty((T, num_q), dtype=torch.float32, device=d))
+    q_i8, qi_bias, f_q = out
+    _check(_lib.bq_attn_prep(_p(q_src), _p(k_src), _p(v_src), _p(q_norm), _p(k_norm), _p(q_i8),
+                             _p(qi_bias), _p(f_q), _p(k_cache), _p(k_scale), _p(v_cache),
+                             _p(v_scale), _p(cos_table), _p(sin_table), _p(runs), runs.shape[0],
+                             _p(base_rows), num_q, num_kv, head_dim, rope_half, pair_stride,
+                             sqrt_n, n_eps, cache_degree, rank, page_shift, row_mask, page_mask,
+                             T, _stream()))
+    return q_i8, qi_bias, f_q
+
+
+def attention_splits(seq_len: int, num_kv: int, max_kv_len: int) -> int:
+    return int(_lib.bq_attention_splits(seq_len, num_kv, max_kv_len))
+
+
+def attention_workspace(seq_len: int, num_q: int, head_dim: int, s_max: int, device="cuda"):
+    n = int(_lib.bq_attention_workspace_size(seq_len, num_q, head_dim, s_max))
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
+def attention(q_i8, qi_bias, f_q, k_cache, k_scale, v_cache, v_scale, runs, base_rows,
+              num_q: int, num_kv: int, head_dim: int, window: int, page_shift: int,
+              row_mask: int, page_mask: int, s_max: int | None = None,
+              max_kv_len: int | None = None, workspace=None, out=None):
+    """dispatch_bq_sliding_attention (window > 0) or dispatch_bq_full_attention
+    (window == 0) -> bf16 [T, num_q*hd].  Returns (out, s_max)."""
+    _dev(q_i8, torch.int8)
+    T = q_i8.shape[0]
+    if s_max is None:
+        s_max = attention_splits(T, num_kv, max_kv_len if max_kv_len else max(window, 1))
+    if workspace is None:
+        workspace = attention_workspace(T, num_q, head_dim, s_max, q_i8.device)
+    if out is None:
+        out = torch.empty((T, num_q * head_dim), dtype=torch.bfloat16, device=q_i8.device)
+    common = (_p(q_i8), _p(qi_bias), _p(f_q), _p(k_cache), _p(k_scale), _p(v_cache),
+              _p(v_scale), _p(out), _p(workspace), workspace.numel(), _p(runs), runs.shape[0],
+              _p(base_rows), num_q, num_kv, head_dim)
+    if window > 0:
+        rc = _lib.bq_sliding_attention(*common, window, page_shift, row_mask, page_mask, s_max,
+                                       T, _stream())
+    else:
+        rc = _lib.bq_full_attention(*common, page_shift, row_mask, page_mask, s_max, T,
+                                    _stream())
+    _check(rc)
+    return out, s_max
 
 
 # --------------------------------------------------------------------------

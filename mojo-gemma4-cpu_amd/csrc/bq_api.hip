@@ -358,3 +358,119 @@ int bq_embed_lookup(const int32_t* token_ids, const int8_t* weight, const float*
                                     shard_rows, rank, scale, S(stream)),
                    "embed_lookup");
 }
+
+static_assert(sizeof(bq_kv_run) == sizeof(bq::KvRun), "bq_kv_run layout");
+
+namespace {
+inline bool attn_hd_ok(int hd) { return hd == 64 || hd == 128 || hd == 256 || hd == 512; }
+
+int attn_common(const char* who, const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                const float* v_scale, uint16_t* output, void* workspace,
+                size_t workspace_bytes, const bq_kv_run* runs, int num_runs,
+                const int32_t* base_rows, int num_q, int num_kv, int head_dim, int window,
+                int page_shift, int row_mask, int page_mask, int s_max, int seq_len,
+                void* stream) {
+  if (!q_i8 || !qi_bias || !f_q || !k_cache || !k_scale || !v_cache || !v_scale || !output ||
+      !runs || !base_rows || !workspace)
+    return fail(BQ_ERR_INVALID, "%s: null pointer", who);
+  if (num_runs <= 0 || num_q <= 0 || num_kv <= 0 || num_q % num_kv || s_max <= 0 ||
+      page_shift < 0 || page_shift > 30)
+    return fail(BQ_ERR_SHAPE, "%s: need num_runs > 0, num_q %% num_kv == 0, s_max > 0", who);
+  const int gqa = num_q / num_kv;
+  if (!attn_hd_ok(head_dim) || !(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8 || gqa == 16))
+    return fail(BQ_ERR_SHAPE, "%s: need head_dim in {64,128,256,512} and num_q/num_kv in "
+                              "{1,2,4,8,16}", who);
+  if (!a16(q_i8) || !a16(k_cache) || !a16(v_cache) || !a16(workspace) || !a16(output))
+    return fail(BQ_ERR_INVALID, "%s: q_i8, caches, output and workspace must be 16-byte aligned",
+                who);
+  const size_t need = bq_attention_workspace_size(seq_len, num_q, head_dim, s_max);
+  if (workspace_bytes < need)
+    return fail(BQ_ERR_SHAPE, "%s: workspace of %zu bytes, need %zu", who, workspace_bytes, need);
+  bq::AttnArgs a{};
+  a.q_i8 = q_i8; a.qi_bias = qi_bias; a.f_q = f_q; a.k_cache = k_cache; a.k_scale = k_scale;
+  a.v_cache = v_cache; a.v_scale = v_scale;
+  a.runs = reinterpret_cast<const bq::KvRun*>(runs); a.base_rows = base_rows; a.out = output;
+  a.ws_acc = static_cast<float*>(workspace);
+  a.ws_ml = a.ws_acc + (size_t)seq_len * num_q * s_max * head_dim;
+  a.num_runs = num_runs; a.T = seq_len; a.num_q = num_q; a.num_kv = num_kv; a.window = window;
+  a.page_shift = page_shift; a.row_mask = row_mask; a.page_mask = page_mask; a.s_max = s_max;
+  return check_hip(bq::launch_flash_attn(a, head_dim, S(stream)), who);
+}
+}  // namespace
+
+extern "C" {
+
+int bq_attn_prep(const uint16_t* q_src, const uint16_t* k_src, const uint16_t* v_src,
+                 const uint16_t* q_norm, const uint16_t* k_norm, int8_t* q_i8, float* qi_bias,
+                 float* f_q, int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                 const float* cos_table, const float* sin_table, const bq_kv_run* runs,
+                 int num_runs, const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                 int rope_half, int pair_stride, float sqrt_n, float n_eps, int cache_degree,
+                 int rank, int page_shift, int row_mask, int page_mask, int seq_len,
+                 void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !q_i8 || !qi_bias || !f_q ||
+      !k_cache || !k_scale || !v_cache || !v_scale || !runs || !base_rows ||
+      (rope_half > 0 && (!cos_table || !sin_table)))
+    return fail(BQ_ERR_INVALID, "bq_attn_prep: null pointer");
+  if (!attn_hd_ok(head_dim) || num_runs <= 0 || num_q <= 0 || num_kv <= 0 ||
+      cache_degree <= 0 || rank < 0 || rank >= cache_degree || page_shift < 0 || page_shift > 30)
+    return fail(BQ_ERR_SHAPE, "bq_attn_prep: need head_dim in {64,128,256,512}, num_runs, "
+                              "num_q, num_kv > 0, 0 <= rank < cache_degree");
+  if (rope_half < 0 || rope_half % 64 || pair_stride % 64 || rope_half > pair_stride ||
+      pair_stride + rope_half > head_dim || (rope_half > 0 && pair_stride <= 0))
+    return fail(BQ_ERR_SHAPE, "bq_attn_prep: rope_half and pair_stride must be multiples of 64 "
+                              "with rope_half <= pair_stride and pair_stride + rope_half <= "
+                              "head_dim");
+  bq::PrepArgs a{};
+  a.q_src = q_src; a.k_src = k_src; a.v_src = v_src; a.q_norm = q_norm; a.k_norm = k_norm;
+  a.q_i8 = q_i8; a.qi_bias = qi_bias; a.f_q = f_q; a.k_cache = k_cache; a.k_scale = k_scale;
+  a.v_cache = v_cache; a.v_scale = v_scale; a.cos_table = cos_table; a.sin_table = sin_table;
+  a.runs = reinterpret_cast<const bq::KvRun*>(runs); a.base_rows = base_rows;
+  a.num_runs = num_runs; a.T = seq_len; a.num_q = num_q; a.num_kv = num_kv;
+  a.rope_half = rope_half; a.pair_stride = pair_stride; a.sqrt_n = sqrt_n; a.n_eps = n_eps;
+  a.cache_degree = cache_degree; a.rank = rank;
+  a.page_shift = page_shift; a.row_mask = row_mask; a.page_mask = page_mask;
+  return check_hip(bq::launch_attn_prep(a, head_dim, S(stream)), "attn_prep");
+}
+
+int bq_attention_splits(int seq_len, int num_kv, int max_kv_len) {
+  return bq::attn_splits(seq_len, num_kv, max_kv_len);
+}
+
+size_t bq_attention_workspace_size(int seq_len, int num_q, int head_dim, int s_max) {
+  if (seq_len <= 0 || num_q <= 0 || head_dim <= 0 || s_max <= 0) return 0;
+  return (size_t)seq_len * num_q * s_max * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+int bq_sliding_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                         const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                         const float* v_scale, uint16_t* output, void* workspace,
+                         size_t workspace_bytes, const bq_kv_run* runs, int num_runs,
+                         const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                         int window, int page_shift, int row_mask, int page_mask, int s_max,
+                         int seq_len, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (window <= 0) return fail(BQ_ERR_SHAPE, "bq_sliding_attention: window must be > 0");
+  return attn_common("bq_sliding_attention", q_i8, qi_bias, f_q, k_cache, k_scale, v_cache,
+                     v_scale, output, workspace, workspace_bytes, runs, num_runs, base_rows,
+                     num_q, num_kv, head_dim, window, page_shift, row_mask, page_mask, s_max,
+                     seq_len, stream);
+}
+
+int bq_full_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                      const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                      const float* v_scale, uint16_t* output, void* workspace,
+                      size_t workspace_bytes, const bq_kv_run* runs, int num_runs,
+                      const int32_t* base_rows, int num_q, int num_kv, int head_dim,
+                      int page_shift, int row_mask, int page_mask, int s_max, int seq_len,
+                      void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  return attn_common("bq_full_attention", q_i8, qi_bias, f_q, k_cache, k_scale, v_cache,
+                     v_scale, output, workspace, workspace_bytes, runs, num_runs, base_rows,
+                     num_q, num_kv, head_dim, 0, page_shift, row_mask, page_mask, s_max,
+                     seq_len, stream);
+}
+
+}  // extern "C"

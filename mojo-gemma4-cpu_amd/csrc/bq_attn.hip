@@ -1,0 +1,503 @@
+// int8-KV attention on gfx950: the attention prep (per-head RMS norm, RoPE,
+// FWHT, absmax int8 with the code sum) that fills the paged int8 KV cache,
+// and flash attention over that cache.
+//
+// Reference: butterquant/head_prep.mojo:9-92 (per-head prep),
+// butterquant_kernels/attention.mojo:32-80 (bq_process_kv_tile), :83-146
+// (decode kernel), :149-247 (sliding prefill), :250-327 (full prefill),
+// :474-534 (BqAttnPrepKernel), kernels/attention_ops.mojo:45-51 (PagedKV),
+// :166-182 (online_softmax_tile), kernels/logsum_merge.mojo:29-122 (merge).
+//
+// Layout.  KV cache rows are slots: k_cache[slot][kv_head][head_dim] int8 with
+// k_scale[slot][kv_head] f32 (amax), the same for V.  A token's position p
+// maps to slot base_rows[run.rows_off + ((p >> shift) & page_mask)] +
+// (p & row_mask).  Q codes are [token][q_head][head_dim] int8 with
+// qi_bias = 128 * sum(codes) and f_q = amax per (token, q_head).
+//
+// Flash attention: one wave per (token, kv head, split).  The split is a
+// contiguous range of the token's KV positions (worker_range of the range
+// into S = min(s_max, ceil(L / kAttnMinSplit)) parts).  A wave walks its
+// range in tiles of 16 positions exactly as the reference does: the 16 x G
+// scores of a tile come from head_dim/64 int8 MFMAs (A = the G query heads
+// of this kv head, B = 16 K rows); per head the tile max, corr and weights
+// use the reference's fast exp and its 16-lane tree sum; then acc *= corr and
+// acc += (w * vs / 127) * v position by position, each lane owning head_dim/64
+// consecutive output columns of every head.  A token whose range is one split
+// of a sliding layer is finalized in the wave (acc * (1/l), the sliding
+// prefill kernel); every other token's splits are written as (m, l, acc)
+// partials and merged by k_attn_merge in split order with the reference's
+// merge (corrections masked by l > 0, a 16-lane tree per batch of 16 splits,
+// the first contributing split multiplied, the rest fma-accumulated).
+#include "bq_kernels.hpp"
+#include "bq_device.hpp"
+
+namespace bq {
+
+namespace {
+
+// The run holding buffer row tok: the reference advances r while
+// tok >= runs[r + 1].buf_start (attention.mojo:489-492), i.e. r + 1 is the
+// first j >= 1 with tok < runs[j].buf_start, else num_runs - 1.
+__device__ inline int run_of(const KvRun* __restrict__ runs, int n, int tok) {
+  const int lane = lane_id();
+  for (int base = 1; base < n; base += kWave) {
+    const int j = base + lane;
+    const bool stop = j < n && tok < runs[j].buf_start;
+    const unsigned long long m = __ballot(stop);
+    if (m) return base + (__ffsll((long long)m) - 1) - 1;
+  }
+  return n - 1;
+}
+
+__device__ inline int64_t paged_slot(const int32_t* __restrict__ rows, int shift, int row_mask,
+                                     int page_mask, int64_t p) {
+  return (int64_t)rows[(p >> shift) & page_mask] + (p & row_mask);
+}
+
+// sum over the 16 lanes of each aligned 16-lane group in the order of a
+// SIMD[f32, 16].reduce_add (halving tree: j + 8, j + 4, j + 2, j + 1); the
+// result is broadcast to the group
+__device__ inline float tree16(float v) {
+  v = v + __shfl_down(v, 8, 16);
+  v = v + __shfl_down(v, 4, 16);
+  v = v + __shfl_down(v, 2, 16);
+  v = v + __shfl_down(v, 1, 16);
+  return __shfl(v, lane_id() & ~15, kWave);
+}
+
+__device__ inline float max87(float x) { return x > -87.0f ? x : -87.0f; }
+
+__device__ inline float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// token metadata shared by the attention and merge kernels
+struct TokRange {
+  const int32_t* rows;
+  int64_t lo;
+  int L;
+};
+
+__device__ inline TokRange token_range(const AttnArgs& a, int tok) {
+  const int r = run_of(a.runs, a.num_runs, tok);
+  const KvRun run = a.runs[r];
+  const int64_t pos = (int64_t)run.base_pos + (tok - run.buf_start);
+  TokRange t;
+  t.rows = a.base_rows + run.rows_off;
+  if (a.window > 0) {  // attention.mojo:196-199: [max(0, pos - window + 1), pos]
+    t.lo = pos - a.window + 1 > 0 ? pos - a.window + 1 : 0;
+    t.L = (int)(pos + 1 - t.lo);
+  } else {             // attention_ops.mojo:146-152 at one rank: rows [0, pos]
+    t.lo = 0;
+    t.L = pos < 0 ? 0 : (int)(pos + 1);
+  }
+  return t;
+}
+
+__device__ inline int num_splits(int L, int s_max) {
+  if (L <= 0) return 1;
+  const int s = (L + kAttnMinSplit - 1) / kAttnMinSplit;
+  return s < s_max ? s : s_max;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// attention prep: one wave per (token, head) over q heads, then k heads, then
+// v heads.  Element e of the head is value r = e / 64 of lane e % 64.
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(256) void k_attn_prep(PrepArgs a) {
+  constexpr int HD = R * kWave;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int nh = a.num_q + 2 * a.num_kv;
+  const int item = blockIdx.x * 4 + wave;
+  if (item >= a.T * nh) return;
+  const int tok = item / nh, j = item % nh;
+  const int r = run_of(a.runs, a.num_runs, tok);
+  const KvRun run = a.runs[r];
+  const int64_t pos = (int64_t)run.base_pos + (tok - run.buf_start);
+  const bool is_q = j < a.num_q, is_v = j >= a.num_q + a.num_kv;
+  const int h = is_q ? j : is_v ? j - a.num_q - a.num_kv : j - a.num_q;
+  // attention.mojo:515: K/V rows only for positions this cache rank owns
+  if (!is_q && pos % a.cache_degree != a.rank) return;
+  const int64_t kvs = (int64_t)a.num_kv * HD;
+  const uint16_t* src = is_q ? a.q_src + (int64_t)tok * a.num_q * HD + (int64_t)h * HD
+                      : (is_v ? a.v_src : a.k_src) + (int64_t)tok * kvs + (int64_t)h * HD;
+  float v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) v[i] = bf16_to_f32(src[i * kWave + lane]);
+
+  // head_inv_rms (head_prep.mojo:9-16): chain k of 16 takes x[16i + k] in i
+  // order (product first, then fma), then the 16-lane tree.  x[16i + k] is
+  // value i / 4 of lane 16 * (i % 4) + k.
+  const int k = lane & 15;
+  float ssq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < HD / 16; ++i) {
+    const float x = __shfl(v[i / 4], 16 * (i % 4) + k, kWave);
+    ssq = i == 0 ? x * x : fmaf(x, x, ssq);
+  }
+  ssq = tree16(ssq);
+  const float inv = a.sqrt_n / __builtin_sqrtf(__shfl(ssq, 0, kWave) + a.n_eps);
+
+  const uint16_t* gamma = is_q ? a.q_norm : a.k_norm;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    v[i] = v[i] * inv;
+    if (!is_v) v[i] = v[i] * bf16_to_f32(gamma[i * kWave + lane]);
+  }
+  if (!is_v) {
+    // RoPE on (e, pair_stride + e) for e < rope_half (head_prep.mojo:58-65);
+    // rope_half and pair_stride are multiples of 64, so both elements of a
+    // pair are values of the same lane
+    const int ps = a.pair_stride / kWave, rh = a.rope_half / kWave;
+    const float* cs = a.cos_table + pos * a.rope_half;
+    const float* sn = a.sin_table + pos * a.rope_half;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (i >= rh) continue;
+      const float c = cs[i * kWave + lane], s = sn[i * kWave + lane];
+#pragma unroll
+      for (int i2 = 0; i2 < R; ++i2) {
+        if (i2 != i + ps) continue;
+        const float lo = v[i], hi = v[i2];
+        v[i] = lo * c - hi * s;
+        v[i2] = hi * c + lo * s;
+      }
+    }
+  }
+  fwht_wave<R>(v, HD);
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    v[i] = v[i] * a.fwht_scale;
+    m = fmaxf(m, fabsf(v[i]));
+  }
+  float amax = wave_max(m);
+  if (amax < 1e-10f) amax = 1e-10f;
+  const float qinv = 127.0f / amax;
+  int8_t* dst;
+  if (is_q) {
+    dst = a.q_i8 + (int64_t)tok * a.num_q * HD + (int64_t)h * HD;
+  } else {
+    const int64_t slot = paged_slot(a.base_rows + run.rows_off, a.page_shift, a.row_mask,
+                                    a.page_mask, pos / a.cache_degree);
+    dst = (is_v ? a.v_cache : a.k_cache) + slot * kvs + (int64_t)h * HD;
+    if (lane == 0) (is_v ? a.v_scale : a.k_scale)[slot * a.num_kv + h] = amax;
+  }
+  int qs = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int8_t c = quantize_i8(v[i], qinv);
+    dst[i * kWave + lane] = c;
+    qs += c;
+  }
+  if (is_q) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) qs += __shfl_xor(qs, o, kWave);
+    if (lane == 0) {
+      a.qi_bias[(int64_t)tok * a.num_q + h] = (float)qs * 128.0f;
+      a.f_q[(int64_t)tok * a.num_q + h] = amax;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flash attention: one wave per (token, kv head, split); G query heads share
+// the kv head (G <= 16).
+// ---------------------------------------------------------------------------
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
+  constexpr int C = HD / 64;  // 64-byte K chunks per row = V bytes per lane
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int per_tok = a.num_kv * a.s_max;
+  const int item = blockIdx.x * 4 + wave;
+  if (item >= a.T * per_tok) return;
+  const int tok = item / per_tok, rem = item % per_tok;
+  const int kvh = rem / a.s_max, s = rem % a.s_max;
+  const TokRange tr = token_range(a, tok);
+  const int S = num_splits(tr.L, a.s_max);
+  if (s >= S) return;
+  int start, end;
+  {
+    const int per = (tr.L + S - 1) / S;
+    start = s * per;
+    end = start + per < tr.L ? start + per : tr.L;
+    if (start >= tr.L) start = end = tr.L;
+  }
+  const int64_t kvs = (int64_t)a.num_kv * HD;
+  const int p16 = lane & 15, grp = lane >> 4;
+  const int qh0 = kvh * G;  // first query head of this kv head
+
+  // A operand: lane (h + 16 g) holds head h's bytes [c*64 + g*16, +16)
+  v4i qa[C];
+  const v4i zero4 = {0, 0, 0, 0};
+  {
+    const int hq = lane & 15;
+    const int8_t* qrow = a.q_i8 + ((int64_t)tok * a.num_q + qh0 + hq) * HD + grp * 16;
+#pragma unroll
+    for (int c = 0; c < C; ++c) qa[c] = hq < G ? ld16(qrow + c * 64) : zero4;
+  }
+  // score layout: lane (p + 16 g), value i <-> head 4 g + i, position p.
+  // The u8-shifted dot of the reference is dot + 128 * sum(q).
+  float qb[4], fq[4];
+  int qsum128[4];
+  {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * grp + i;
+      qb[i] = 0.0f; fq[i] = 0.0f; qsum128[i] = 0;
+      if (h < G) {
+        qb[i] = a.qi_bias[(int64_t)tok * a.num_q + qh0 + h];
+        fq[i] = a.f_q[(int64_t)tok * a.num_q + qh0 + h];
+      }
+    }
+    // sum of the query codes of head hq, lane-parallel over the 16-byte pieces
+    int part = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int w4[4] = {qa[c].x, qa[c].y, qa[c].z, qa[c].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        part += (int)(int8_t)w4[q] + (int)(int8_t)(w4[q] >> 8) + (int)(int8_t)(w4[q] >> 16) +
+                (w4[q] >> 24);
+    }
+    part += __shfl_xor(part, 16, kWave);
+    part += __shfl_xor(part, 32, kWave);  // lane hq (and hq + 16 g): sum of head hq
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qsum128[i] = 128 * __shfl(part, 4 * grp + i, kWave);
+  }
+
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { m[i] = -1e30f; l[i] = 0.0f; }
+  float acc[G][C];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[h][c] = 0.0f;
+
+  const int8_t* kbase = a.k_cache + (int64_t)kvh * HD;
+  const int8_t* vbase = a.v_cache + (int64_t)kvh * HD + lane * C;
+  for (int p0 = start; p0 < end; p0 += 16) {
+    const int tl = end - p0 < 16 ? end - p0 : 16;
+    // slots of the tile (lane p16); idle lanes repeat the first position
+    const int pp = p16 < tl ? p16 : 0;
+    const int64_t slot = paged_slot(tr.rows, a.page_shift, a.row_mask, a.page_mask,
+                                    tr.lo + p0 + pp);
+    v4i kb[C];
+    const int8_t* krow = kbase + slot * kvs + grp * 16;
+#pragma unroll
+    for (int c = 0; c < C; ++c) kb[c] = ld16(krow + c * 64);
+    const float ks = a.k_scale[slot * a.num_kv + kvh];
+    const float vs = a.v_scale[slot * a.num_kv + kvh];
+    // V rows of the tile, this lane's C bytes of each
+    uint32_t vraw[16][(C + 3) / 4];
+    const int slot_lo = (int)slot;  // slots fit in 32 bits (checked by the host)
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      if (p < tl) {
+        const int sp = __builtin_amdgcn_readlane(slot_lo, p);
+        const int8_t* vr = vbase + (int64_t)sp * kvs;
+        if constexpr (C >= 8) {
+          const uint2 w = *reinterpret_cast<const uint2*>(vr);
+          vraw[p][0] = w.x; vraw[p][1] = w.y;
+        } else if constexpr (C == 4) {
+          vraw[p][0] = *reinterpret_cast<const uint32_t*>(vr);
+        } else if constexpr (C == 2) {
+          vraw[p][0] = *reinterpret_cast<const uint16_t*>(vr);
+        } else {
+          vraw[p][0] = (uint8_t)*vr;
+        }
+      }
+    }
+    v4i d = zero4;
+#pragma unroll
+    for (int c = 0; c < C; ++c) d = mfma16x16x64(qa[c], kb[c], d);
+    const int dv[4] = {d.x, d.y, d.z, d.w};
+    float sc[4], corr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sco = -1e30f;
+      if (4 * grp + i < G && p16 < tl)
+        sco = (((float)(dv[i] + qsum128[i]) - qb[i]) * fq[i]) * ks * inv127sq;
+      const float tmax = group_max(sco, 16);
+      const float m_new = tmax > m[i] ? tmax : m[i];
+      corr[i] = fast_exp_softmax_biased(max87(m[i] - m_new));
+      const float w = fast_exp_softmax_biased(max87(sco - m_new));
+      l[i] = l[i] * corr[i] + tree16(w);
+      m[i] = m_new;
+      sc[i] = p16 < tl ? w * vs * inv127 : 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float ch = readlane_f(corr[h % 4], 16 * (h / 4));
+#pragma unroll
+      for (int c = 0; c < C; ++c) acc[h][c] = acc[h][c] * ch;
+    }
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      if (p < tl) {
+        float vf[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          vf[c] = (float)(int8_t)(vraw[p][c / 4] >> (8 * (c % 4)));
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float w = readlane_f(sc[h % 4], p + 16 * (h / 4));
+#pragma unroll
+          for (int c = 0; c < C; ++c) acc[h][c] = fmaf(vf[c], w, acc[h][c]);
+        }
+      }
+    }
+  }
+
+  const bool direct = a.window > 0 && S == 1;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float mh = readlane_f(m[h % 4], 16 * (h / 4));
+    const float lh = readlane_f(l[h % 4], 16 * (h / 4));
+    const int64_t qrow = (int64_t)tok * a.num_q + qh0 + h;
+    if (direct) {
+      uint16_t o[C];
+      if (lh > 0.0f) {
+        const float inv_l = 1.0f / lh;
+#pragma unroll
+        for (int c = 0; c < C; ++c) o[c] = f32_to_bf16(acc[h][c] * inv_l);
+      } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) o[c] = 0;
+      }
+      uint16_t* dst = a.out + qrow * HD + lane * C;
+#pragma unroll
+      for (int c = 0; c < C; ++c) dst[c] = o[c];
+    } else {
+      float* pa = a.ws_acc + (qrow * a.s_max + s) * HD + lane * C;
+#pragma unroll
+      for (int c = 0; c < C; ++c) pa[c] = acc[h][c];
+      if (lane == 0) {
+        a.ws_ml[(qrow * a.s_max + s) * 2 + 0] = mh;
+        a.ws_ml[(qrow * a.s_max + s) * 2 + 1] = lh;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// merge of the split partials: one wave per (token, query head)
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+  constexpr int C = HD / 64;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int item = blockIdx.x * 4 + wave;
+  if (item >= a.T * a.num_q) return;
+  const int tok = item / a.num_q;
+  const TokRange tr = token_range(a, tok);
+  const int S = num_splits(tr.L, a.s_max);
+  if (a.window > 0 && S == 1) return;  // finalized by the attention wave
+  const int64_t base = (int64_t)item * a.s_max;
+  const float* ml = a.ws_ml + base * 2;
+  float gm = -1e30f;
+  for (int s0 = 0; s0 < S; s0 += kWave) {
+    const float v = s0 + lane < S ? ml[(s0 + lane) * 2] : -1e30f;
+    gm = fmaxf(gm, wave_max(v));
+  }
+  // global l: batches of 16 splits, each a 16-lane tree of l * c
+  float gl = 0.0f;
+  for (int s0 = 0; s0 < S; s0 += kWave) {
+    const int sidx = s0 + lane;
+    float d = -1e30f, ls = 0.0f;
+    if (sidx < S) { d = ml[sidx * 2] - gm; ls = ml[sidx * 2 + 1]; }
+    float c = fast_exp_softmax_biased(max87(d));
+    if (!(ls > 0.0f)) c = 0.0f;
+    const float bsum = tree16(ls * c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (s0 + 16 * q < S) gl = gl + readlane_f(bsum, 16 * q);
+  }
+  float out[C];
+  bool first = true;
+  for (int s = 0; s < S; ++s) {
+    const float ls = ml[s * 2 + 1];
+    float c = fast_exp_softmax_biased(max87(ml[s * 2] - gm));
+    if (!(ls > 0.0f)) c = 0.0f;
+    if (c <= 0.0f) continue;
+    const float* src = a.ws_acc + (base + s) * HD + lane * C;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) out[cc] = first ? src[cc] * c : fmaf(src[cc], c, out[cc]);
+    first = false;
+  }
+  uint16_t* dst = a.out + (int64_t)item * HD + lane * C;
+  if (!(gl > 0.0f)) {
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) dst[cc] = 0;
+    return;
+  }
+  const float inv_l = 1.0f / gl;
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) dst[cc] = f32_to_bf16(out[cc] * inv_l);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_attn_prep(const PrepArgs& args, int head_dim, hipStream_t st) {
+  PrepArgs a = args;
+  a.fwht_scale = fwht_scale_host(head_dim);
+  const int items = a.T * (a.num_q + 2 * a.num_kv);
+  if (items <= 0) return hipSuccess;
+  const dim3 g((items + 3) / 4), b(256);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL(k_attn_prep<1>, g, b, 0, st, a); break;
+    case 128: hipLaunchKernelGGL(k_attn_prep<2>, g, b, 0, st, a); break;
+    case 256: hipLaunchKernelGGL(k_attn_prep<4>, g, b, 0, st, a); break;
+    case 512: hipLaunchKernelGGL(k_attn_prep<8>, g, b, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t launch_attn_hd(const AttnArgs& a, int gqa, hipStream_t st) {
+  const int items = a.T * a.num_kv * a.s_max;
+  const dim3 g((items + 3) / 4), b(256);
+  switch (gqa) {
+    case 1: hipLaunchKernelGGL((k_flash_attn<HD, 1>), g, b, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_flash_attn<HD, 2>), g, b, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_flash_attn<HD, 4>), g, b, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_flash_attn<HD, 8>), g, b, 0, st, a); break;
+    case 16: hipLaunchKernelGGL((k_flash_attn<HD, 16>), g, b, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  const dim3 gm((a.T * a.num_q + 3) / 4);
+  hipLaunchKernelGGL(k_attn_merge<HD>, gm, b, 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_flash_attn(const AttnArgs& a, int head_dim, hipStream_t st) {
+  if (a.T <= 0) return hipSuccess;
+  const int gqa = a.num_q / a.num_kv;
+  switch (head_dim) {
+    case 64: return launch_attn_hd<64>(a, gqa, st);
+    case 128: return launch_attn_hd<128>(a, gqa, st);
+    case 256: return launch_attn_hd<256>(a, gqa, st);
+    case 512: return launch_attn_hd<512>(a, gqa, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int attn_splits(int seq_len, int num_kv, int max_kv_len) {
+  // enough splits for ~2048 waves, each at least kAttnMinSplit positions
+  if (seq_len <= 0 || num_kv <= 0) return 1;
+  const int64_t items = (int64_t)seq_len * num_kv;
+  int s = (int)((2048 + items - 1) / items);
+  const int cap = max_kv_len > 0 ? (max_kv_len + kAttnMinSplit - 1) / kAttnMinSplit : 1;
+  if (s > cap) s = cap;
+  return s < 1 ? 1 : s;
+}
+
+}  // namespace bq

@@ -111,4 +111,41 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa,
                              uint16_t* out, int experts, int seq_len, int max_routes, int hidden,
                              int inter, int block, void* workspace, hipStream_t st);
 
+// int8-KV attention (bq_attn.hip)
+struct KvRun {  // kernels/attention_ops.mojo:54-58 KVRun
+  int32_t buf_start, base_pos, rows_off, page_count;
+};
+constexpr int kAttnMinSplit = 32;  // fewest KV positions per split
+struct PrepArgs {
+  const uint16_t *q_src, *k_src, *v_src, *q_norm, *k_norm;
+  int8_t* q_i8;
+  float *qi_bias, *f_q;
+  int8_t* k_cache;
+  float* k_scale;
+  int8_t* v_cache;
+  float* v_scale;
+  const float *cos_table, *sin_table;
+  const KvRun* runs;
+  const int32_t* base_rows;
+  int num_runs, T, num_q, num_kv, rope_half, pair_stride;
+  float sqrt_n, n_eps, fwht_scale;  // fwht_scale: set by launch_attn_prep
+  int cache_degree, rank, page_shift, row_mask, page_mask;
+};
+struct AttnArgs {
+  const int8_t* q_i8;
+  const float *qi_bias, *f_q;
+  const int8_t* k_cache;
+  const float* k_scale;
+  const int8_t* v_cache;
+  const float* v_scale;
+  const KvRun* runs;
+  const int32_t* base_rows;
+  uint16_t* out;
+  float *ws_acc, *ws_ml;
+  int num_runs, T, num_q, num_kv, window, page_shift, row_mask, page_mask, s_max;
+};
+hipError_t launch_attn_prep(const PrepArgs& a, int head_dim, hipStream_t st);
+hipError_t launch_flash_attn(const AttnArgs& a, int head_dim, hipStream_t st);
+int attn_splits(int seq_len, int num_kv, int max_kv_len);
+
 }  // namespace bq

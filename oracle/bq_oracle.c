@@ -850,3 +850,275 @@ void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
     }
     free(ws);
 }
+
+/* ------------------------------------------------------------------------ */
+/* int8-KV attention: prep and flash attention                               */
+/* ------------------------------------------------------------------------ */
+
+/* 16-lane halving-tree reduce_add of one SIMD[f32, 16] */
+static float tree16(float* s) {
+    for (int half = 8; half >= 1; half /= 2)
+        for (int j = 0; j < half; ++j) s[j] = s[j] + s[j + half];
+    return s[0];
+}
+
+/* attention_ops.mojo:45-51 PagedKV.slot(0, p) */
+static int64_t paged_slot(const int32_t* rows, int shift, int row_mask, int page_mask, int64_t p) {
+    return (int64_t)rows[(p >> shift) & page_mask] + (p & row_mask);
+}
+
+/* attention.mojo:489-492: the run holding buffer row tok (runs advance while
+ * tok >= runs[r+1].buf_start) */
+static int run_of(const bqo_kv_run* runs, int num_runs, int tok) {
+    int r = 0;
+    while (r + 1 < num_runs && tok >= runs[r + 1].buf_start) ++r;
+    return r;
+}
+
+/* head_prep.mojo:9-92.  head_inv_rms (:9-16): 16 f32 lanes, lane k is
+ * x[k]*x[k] then an fma chain over x[16i + k], then a 16-lane tree;
+ * inv = sqrt_n / sqrt(ssq + n_eps).  q/k (prep_head_qk_i8 :39-71): x*inv*g,
+ * RoPE on pairs (i, pair_stride + i) for i < rope_half, FWHT(head_dim),
+ * absmax quantize (:19-36: amax floored at 1e-10, codes, their i32 sum).
+ * v (prep_head_v_i8 :74-92): x*inv, FWHT, quantize.  gamma == NULL selects
+ * the v form. */
+static void prep_head(const uint16_t* src, const uint16_t* gamma, const float* cs,
+                      const float* sn, int hd, int rope_half, int pair_stride, float sqrt_n,
+                      float n_eps, int8_t* out, float* amax_out, int32_t* qsum_out) {
+    float r[1024];
+    for (int i = 0; i < hd; ++i) r[i] = bqo_bf16_to_f32(src[i]);
+    float ssq[16];
+    for (int k = 0; k < 16; ++k) {
+        ssq[k] = r[k] * r[k];
+        for (int i = 1; i < hd / 16; ++i) ssq[k] = fmaf(r[16 * i + k], r[16 * i + k], ssq[k]);
+    }
+    float inv = sqrt_n / sqrtf(tree16(ssq) + n_eps);
+    for (int i = 0; i < hd; ++i) {
+        r[i] = r[i] * inv;
+        if (gamma) r[i] = r[i] * bqo_bf16_to_f32(gamma[i]);
+    }
+    if (gamma) {
+        for (int i = 0; i < rope_half; ++i) {
+            float lo = r[i], hi = r[pair_stride + i];
+            r[i] = lo * cs[i] - hi * sn[i];
+            r[pair_stride + i] = hi * cs[i] + lo * sn[i];
+        }
+    }
+    bqo_fwht_block(r, hd);
+    float amax = 0.0f;
+    for (int i = 0; i < hd; ++i) amax = fmaxf(amax, fabsf(r[i]));
+    if (amax < 1e-10f) amax = 1e-10f;
+    float qinv = 127.0f / amax;
+    int32_t qsum = 0;
+    for (int i = 0; i < hd; ++i) {
+        out[i] = quantize_i8(r[i], qinv);
+        qsum += out[i];
+    }
+    *amax_out = amax;
+    if (qsum_out) *qsum_out = qsum;
+}
+
+/* attention.mojo:474-534 BqAttnPrepKernel.execute */
+void bqo_attn_prep(const uint16_t* q_src, const uint16_t* k_src, const uint16_t* v_src,
+                   const uint16_t* q_norm, const uint16_t* k_norm, int8_t* q_i8,
+                   float* qi_bias, float* f_q, int8_t* k_cache, float* k_scale,
+                   int8_t* v_cache, float* v_scale, const float* cos_table,
+                   const float* sin_table, const bqo_kv_run* runs, int num_runs,
+                   const int32_t* base_rows, int seq_len, int num_q, int num_kv,
+                   int head_dim, int rope_half, int pair_stride, float sqrt_n, float n_eps,
+                   int cache_degree, int rank, int page_shift, int row_mask, int page_mask) {
+    const int64_t qs = (int64_t)num_q * head_dim, kvs = (int64_t)num_kv * head_dim;
+    for (int tok = 0; tok < seq_len; ++tok) {
+        int r = run_of(runs, num_runs, tok);
+        int64_t pos = runs[r].base_pos + (tok - runs[r].buf_start);
+        const float* cs = cos_table + pos * rope_half;
+        const float* sn = sin_table + pos * rope_half;
+        for (int h = 0; h < num_q; ++h) {
+            float amax;
+            int32_t qsum;
+            prep_head(q_src + tok * qs + h * head_dim, q_norm, cs, sn, head_dim, rope_half,
+                      pair_stride, sqrt_n, n_eps, q_i8 + tok * qs + h * head_dim, &amax, &qsum);
+            qi_bias[(int64_t)tok * num_q + h] = (float)qsum * 128.0f;
+            f_q[(int64_t)tok * num_q + h] = amax;
+        }
+        if (pos % cache_degree != rank) continue;
+        int64_t slot = paged_slot(base_rows + runs[r].rows_off, page_shift, row_mask, page_mask,
+                                  pos / cache_degree);
+        for (int h = 0; h < num_kv; ++h) {
+            prep_head(k_src + tok * kvs + h * head_dim, k_norm, cs, sn, head_dim, rope_half,
+                      pair_stride, sqrt_n, n_eps, k_cache + slot * kvs + h * head_dim,
+                      k_scale + slot * num_kv + h, NULL);
+            prep_head(v_src + tok * kvs + h * head_dim, NULL, NULL, NULL, head_dim, 0, 0, sqrt_n,
+                      n_eps, v_cache + slot * kvs + h * head_dim, v_scale + slot * num_kv + h,
+                      NULL);
+        }
+    }
+}
+
+/* Splits of one query token's KV range of length L: S = min(s_max,
+ * max(1, ceil(L / min_split))) ranges, range s = worker_range(L, S, s)
+ * (kernels/helpers.mojo:182-190).  This is the GPU's partition (the
+ * reference's decode splits by its worker pool); it fixes the f32 merge
+ * order, so the oracle takes it as an input. */
+int bqo_attn_num_splits(int L, int s_max, int min_split) {
+    if (L <= 0) return 1;
+    int s = (L + min_split - 1) / min_split;
+    return s < s_max ? s : s_max;
+}
+
+static void worker_range(int total, int n, int id, int* s, int* e) {
+    int per = (total + n - 1) / n;
+    *s = id * per;
+    *e = *s + per < total ? *s + per : total;
+    if (*s >= total) *s = *e = total;
+}
+
+static inline float max87(float x) { return x > -87.0f ? x : -87.0f; }
+
+typedef struct { float m, l; } ml_t;
+
+/* attention.mojo:32-80 bq_process_kv_tile for one q head over positions
+ * [lo + pos, lo + pos + tile_len), plus the tile loop of attention.mojo:127-
+ * 136.  score = (f32(sum (k^0x80) * q) - qi_bias) * f_q * ks / 127^2 (the
+ * u8-shifted VNNI dot, butterquant/dot_products.mojo:41-60, of K against Q);
+ * online_softmax_tile (attention_ops.mojo:166-182); acc *= corr;
+ * l = l*corr + reduce_add(w); acc += (w*vs/127) * v (fma per element,
+ * helpers.mojo:48-66). */
+static void attn_range(const int8_t* q, float qb, float fq, const int8_t* k_cache,
+                       const float* k_scale, const int8_t* v_cache, const float* v_scale,
+                       const int32_t* rows, int shift, int row_mask, int page_mask,
+                       int64_t kvs, int num_kv, int kv_h, int hd, int64_t lo, int start,
+                       int end, ml_t* ml, float* acc) {
+    const float inv127 = 1.0f / 127.0f;
+    const float inv127sq = inv127 * inv127;
+    ml->m = -1e30f;
+    ml->l = 0.0f;
+    for (int j = 0; j < hd; ++j) acc[j] = 0.0f;
+    for (int pos = start; pos < end; pos += 16) {
+        int tl = end - pos < 16 ? end - pos : 16;
+        int64_t slots[16];
+        float sc[16], w[16];
+        for (int t = 0; t < 16; ++t) sc[t] = -1e30f;
+        for (int t = 0; t < tl; ++t) {
+            slots[t] = paged_slot(rows, shift, row_mask, page_mask, lo + pos + t);
+            const int8_t* kh = k_cache + slots[t] * kvs + (int64_t)kv_h * hd;
+            int32_t rr = 0;
+            for (int j = 0; j < hd; ++j) rr += (int32_t)((uint8_t)kh[j] ^ 0x80u) * q[j];
+            float ks = k_scale[slots[t] * num_kv + kv_h];
+            sc[t] = (((float)rr - qb) * fq) * ks * inv127sq;
+        }
+        float tmax = sc[0];
+        for (int t = 1; t < 16; ++t) tmax = sc[t] > tmax ? sc[t] : tmax;
+        float m_new = tmax > ml->m ? tmax : ml->m;
+        float corr = bqo_fast_exp_softmax_biased(max87(ml->m - m_new));
+        for (int t = 0; t < 16; ++t) w[t] = bqo_fast_exp_softmax_biased(max87(sc[t] - m_new));
+        for (int j = 0; j < hd; ++j) acc[j] = acc[j] * corr;
+        float wl[16];
+        memcpy(wl, w, sizeof(wl));
+        ml->l = ml->l * corr + tree16(wl);
+        ml->m = m_new;
+        for (int t = 0; t < tl; ++t) {
+            const int8_t* vh = v_cache + slots[t] * kvs + (int64_t)kv_h * hd;
+            float s = w[t] * v_scale[slots[t] * num_kv + kv_h] * inv127;
+            for (int j = 0; j < hd; ++j) acc[j] = fmaf((float)vh[j], s, acc[j]);
+        }
+    }
+}
+
+/* logsum_merge.mojo:29-122 merge_segments + write_finalized_head over the n
+ * split partials of one head, in split order */
+static void merge_write(const ml_t* ml, const float* acc, int n, int hd, uint16_t* dst,
+                        float* dst32) {
+    float gm = -1e30f;
+    for (int s = 0; s < n; ++s) if (ml[s].m > gm) gm = ml[s].m;
+    float gl = 0.0f, out[1024];
+    int first = 1;
+    for (int b0 = 0; b0 < n; b0 += 16) {
+        int bl = n - b0 < 16 ? n - b0 : 16;
+        float d[16], ls[16], c[16], prod[16];
+        for (int b = 0; b < 16; ++b) { d[b] = -1e30f; ls[b] = 0.0f; }
+        for (int b = 0; b < bl; ++b) { d[b] = ml[b0 + b].m - gm; ls[b] = ml[b0 + b].l; }
+        for (int b = 0; b < 16; ++b) {
+            c[b] = bqo_fast_exp_softmax_biased(max87(d[b]));
+            if (!(ls[b] > 0.0f)) c[b] = 0.0f;
+            prod[b] = ls[b] * c[b];
+        }
+        gl += tree16(prod);
+        for (int b = 0; b < bl; ++b) {
+            if (c[b] <= 0.0f) continue;
+            const float* src = acc + (size_t)(b0 + b) * hd;
+            if (first) { for (int j = 0; j < hd; ++j) out[j] = src[j] * c[b]; first = 0; }
+            else for (int j = 0; j < hd; ++j) out[j] = fmaf(src[j], c[b], out[j]);
+        }
+    }
+    if (gl <= 0.0f) {
+        for (int j = 0; j < hd; ++j) { dst[j] = 0; if (dst32) dst32[j] = 0.0f; }
+        return;
+    }
+    float inv_l = 1.0f / gl;
+    for (int j = 0; j < hd; ++j) {
+        float y = out[j] * inv_l;
+        dst[j] = bqo_f32_to_bf16(y);
+        if (dst32) dst32[j] = y;
+    }
+}
+
+/* attention.mojo:83-146 (decode, split + merge), :149-247 (sliding prefill:
+ * window [pos - window + 1, pos], out = acc * (1/l) or zeros) and :250-327
+ * (full prefill: rank-local rows [0, full_local_kv_count), attention_ops.mojo:
+ * 146-152, then the merge).  window > 0 selects the sliding form: a token
+ * whose range is one split is finalized directly as the sliding prefill
+ * kernel does; every other token goes through the merge.  out_f32 (may be
+ * NULL) receives the values before the bf16 cast. */
+void bqo_flash_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                         const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                         const float* v_scale, const bqo_kv_run* runs, int num_runs,
+                         const int32_t* base_rows, int seq_len, int num_q, int num_kv,
+                         int head_dim, int window, int degree, int rank, int page_shift,
+                         int row_mask, int page_mask, int s_max, int min_split,
+                         uint16_t* out, float* out_f32) {
+    const int gqa = num_q / num_kv;
+    const int64_t kvs = (int64_t)num_kv * head_dim, qs = (int64_t)num_q * head_dim;
+    ml_t* ml = (ml_t*)malloc(sizeof(ml_t) * (size_t)s_max);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)s_max * head_dim);
+    for (int tok = 0; tok < seq_len; ++tok) {
+        int r = run_of(runs, num_runs, tok);
+        int64_t pos = runs[r].base_pos + (tok - runs[r].buf_start);
+        const int32_t* rows = base_rows + runs[r].rows_off;
+        int64_t lo;
+        int L;
+        if (window > 0) {
+            lo = pos - window + 1 > 0 ? pos - window + 1 : 0;
+            L = (int)(pos + 1 - lo);
+        } else {
+            lo = 0;
+            L = pos < 0 ? 0 : (rank <= pos % degree ? (int)(pos / degree + 1) : (int)(pos / degree));
+        }
+        int S = bqo_attn_num_splits(L, s_max, min_split);
+        for (int h = 0; h < num_q; ++h) {
+            const int8_t* q = q_i8 + tok * qs + (int64_t)h * head_dim;
+            float qb = qi_bias[(int64_t)tok * num_q + h], fq = f_q[(int64_t)tok * num_q + h];
+            for (int s = 0; s < S; ++s) {
+                int a, e;
+                worker_range(L, S, s, &a, &e);
+                attn_range(q, qb, fq, k_cache, k_scale, v_cache, v_scale, rows, page_shift,
+                           row_mask, page_mask, kvs, num_kv, h / gqa, head_dim, lo, a, e, &ml[s],
+                           acc + (size_t)s * head_dim);
+            }
+            uint16_t* dst = out + tok * qs + (int64_t)h * head_dim;
+            float* d32 = out_f32 ? out_f32 + tok * qs + (int64_t)h * head_dim : NULL;
+            if (window > 0 && S == 1) {
+                float inv_l = ml[0].l > 0.0f ? 1.0f / ml[0].l : 0.0f;
+                for (int j = 0; j < head_dim; ++j) {
+                    float y = ml[0].l > 0.0f ? acc[j] * inv_l : 0.0f;
+                    dst[j] = ml[0].l > 0.0f ? bqo_f32_to_bf16(y) : 0;
+                    if (d32) d32[j] = y;
+                }
+            } else {
+                merge_write(ml, acc, S, head_dim, dst, d32);
+            }
+        }
+    }
+    free(ml);
+    free(acc);
+}

@@ -153,6 +153,28 @@ void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
                       const float* wscales, int hidden, int block, int shard_rows,
                       int rank, float scale, uint16_t* dst); /* embedding.mojo:21-96 */
 
+/* ---- int8-KV attention --------------------------------------------------- */
+typedef struct {              /* kernels/attention_ops.mojo:54-58 KVRun */
+    int32_t buf_start, base_pos, rows_off, page_count;
+} bqo_kv_run;
+void bqo_attn_prep(const uint16_t* q_src, const uint16_t* k_src, const uint16_t* v_src,
+                   const uint16_t* q_norm, const uint16_t* k_norm, int8_t* q_i8,
+                   float* qi_bias, float* f_q, int8_t* k_cache, float* k_scale,
+                   int8_t* v_cache, float* v_scale, const float* cos_table,
+                   const float* sin_table, const bqo_kv_run* runs, int num_runs,
+                   const int32_t* base_rows, int seq_len, int num_q, int num_kv,
+                   int head_dim, int rope_half, int pair_stride, float sqrt_n, float n_eps,
+                   int cache_degree, int rank, int page_shift, int row_mask,
+                   int page_mask);        /* butterquant_kernels/attention.mojo:474-534 */
+int bqo_attn_num_splits(int L, int s_max, int min_split);
+void bqo_flash_attention(const int8_t* q_i8, const float* qi_bias, const float* f_q,
+                         const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                         const float* v_scale, const bqo_kv_run* runs, int num_runs,
+                         const int32_t* base_rows, int seq_len, int num_q, int num_kv,
+                         int head_dim, int window, int degree, int rank, int page_shift,
+                         int row_mask, int page_mask, int s_max, int min_split,
+                         uint16_t* out, float* out_f32); /* attention.mojo:32-327 */
+
 /* ---- synthetic inputs ---------------------------------------------------- */
 uint64_t bqo_splitmix64(uint64_t* state);
 /* splitmix64 -> Box-Muller (f64) -> *sigma -> f32 -> bf16 RNE */

@@ -464,3 +464,72 @@ def embed_scale(hidden: int) -> float:
     """f32(bf16(sqrtf(hidden))) (gemma_4_moe_bq.mojo:965-966)."""
     s = np.sqrt(np.float32(hidden), dtype=np.float32)
     return float(bf16_to_f32(f32_to_bf16(np.array([s], np.float32)))[0])
+
+
+# --------------------------------------------------------------------------
+# int8-KV attention
+# --------------------------------------------------------------------------
+
+KV_RUN_DT = np.dtype([("buf_start", "<i4"), ("base_pos", "<i4"), ("rows_off", "<i4"),
+                      ("page_count", "<i4")])   # kernels/attention_ops.mojo:54-58 KVRun
+
+
+def kv_runs(runs) -> np.ndarray:
+    """[(buf_start, base_pos, rows_off, page_count), ...] -> KV_RUN_DT array."""
+    return np.array([tuple(int(v) for v in r) for r in runs], KV_RUN_DT)
+
+
+def attn_prep(q_src, k_src, v_src, q_norm, k_norm, k_cache, k_scale, v_cache, v_scale,
+              cos_table, sin_table, runs, base_rows, num_q, num_kv, head_dim, rope_half,
+              pair_stride, page_shift, row_mask, page_mask, cache_degree=1, rank=0,
+              sqrt_n=None, n_eps=None):
+    """BqAttnPrepKernel (butterquant_kernels/attention.mojo:474-534): returns
+    (q_i8 [T, num_q*hd], qi_bias [T, num_q], f_q [T, num_q]); writes the
+    token's K/V rows and scales into the caches (numpy arrays, in place)."""
+    T = q_src.shape[0]
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(head_dim)
+    q = _c(q_src, np.uint16); k = _c(k_src, np.uint16); v = _c(v_src, np.uint16)
+    qn = _c(q_norm, np.uint16); kn = _c(k_norm, np.uint16)
+    cs = _c(cos_table, np.float32); sn = _c(sin_table, np.float32)
+    rr = np.ascontiguousarray(runs, KV_RUN_DT); br = _c(base_rows, np.int32)
+    for a in (k_cache, k_scale, v_cache, v_scale):
+        assert a.flags.c_contiguous
+    qi = np.zeros((T, num_q * head_dim), np.int8)
+    qb = np.zeros((T, num_q), np.float32)
+    fq = np.zeros((T, num_q), np.float32)
+    f = lib().bqo_attn_prep
+    f.argtypes = ([C.c_void_p] * 15 + [C.c_int, C.c_void_p] + [C.c_int] * 6
+                  + [C.c_float, C.c_float] + [C.c_int] * 5)
+    f(_p(q), _p(k), _p(v), _p(qn), _p(kn), _p(qi), _p(qb), _p(fq), _p(k_cache), _p(k_scale),
+      _p(v_cache), _p(v_scale), _p(cs), _p(sn), _p(rr), len(rr), _p(br), T, num_q, num_kv,
+      head_dim, rope_half, pair_stride, sqrt_n, n_eps, cache_degree, rank, page_shift,
+      row_mask, page_mask)
+    return qi, qb, fq
+
+
+def attn_num_splits(L: int, s_max: int, min_split: int) -> int:
+    return int(lib().bqo_attn_num_splits(int(L), int(s_max), int(min_split)))
+
+
+def flash_attention(q_i8, qi_bias, f_q, k_cache, k_scale, v_cache, v_scale, runs, base_rows,
+                    num_q, num_kv, head_dim, window, page_shift, row_mask, page_mask,
+                    s_max=1, min_split=32, degree=1, rank=0, with_f32=False):
+    """int8-KV flash attention (butterquant_kernels/attention.mojo:32-327 with
+    the merge of kernels/logsum_merge.mojo:29-122) -> bf16 [T, num_q*hd].
+    window > 0: sliding; window == 0: full.  s_max / min_split fix the split
+    of each token's KV range (and with it the f32 merge order).  with_f32:
+    also return the f32 values before the bf16 cast."""
+    qi = _c(q_i8, np.int8); qb = _c(qi_bias, np.float32); fq = _c(f_q, np.float32)
+    kc = _c(k_cache, np.int8); ks = _c(k_scale, np.float32)
+    vc = _c(v_cache, np.int8); vs = _c(v_scale, np.float32)
+    rr = np.ascontiguousarray(runs, KV_RUN_DT); br = _c(base_rows, np.int32)
+    T = qi.shape[0]
+    out = np.zeros((T, num_q * head_dim), np.uint16)
+    o32 = np.zeros((T, num_q * head_dim), np.float32)
+    f = lib().bqo_flash_attention
+    f.argtypes = [C.c_void_p] * 8 + [C.c_int, C.c_void_p] + [C.c_int] * 12 + [C.c_void_p] * 2
+    f(_p(qi), _p(qb), _p(fq), _p(kc), _p(ks), _p(vc), _p(vs), _p(rr), len(rr), _p(br), T,
+      num_q, num_kv, head_dim, window, degree, rank, page_shift, row_mask, page_mask, s_max,
+      min_split, _p(out), _p(o32))
+    return (out, o32) if with_f32 else out

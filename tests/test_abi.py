@@ -90,6 +90,35 @@ def test_validation_errors(L):
                                 C.c_void_p(100), 1 << 30, None) == 1
 
 
+
+def test_attention_validation(L):
+    f1 = C.c_float(1)
+    prep = lambda hd, rh, ps, deg=1, rank=0: L.bq_attn_prep(
+        *([P] * 15), 1, P, 16, 8, hd, rh, ps, f1, f1, deg, rank, 10, 1023, 1, 4, None)
+    assert prep(192, 64, 64) == 2                     # head_dim
+    assert prep(256, 96, 128) == 2                    # rope_half % 64
+    assert prep(256, 128, 192) == 2                   # pair_stride + rope_half > head_dim
+    assert prep(512, 64, 256, deg=2, rank=2) == 2     # rank >= cache_degree
+    assert L.bq_attn_prep(*([P] * 14), None, 1, P, 16, 8, 256, 128, 128, f1, f1, 1, 0, 10,
+                          1023, 1, 4, None) == 1
+    ws = C.c_void_p(256)
+    need = L.bq_attention_workspace_size(4, 16, 256, 8)
+    assert need == 4 * 16 * 8 * 258 * 4
+    slide = lambda nq, nkv, hd, window, wsb, s_max=8, wsp=ws: L.bq_sliding_attention(
+        *([P] * 8), wsp, wsb, P, 1, P, nq, nkv, hd, window, 10, 1023, 1, s_max, 4, None)
+    assert slide(16, 8, 256, 0, need) == 2            # window
+    assert slide(16, 6, 256, 1024, need) == 2         # num_q % num_kv
+    assert slide(96, 3, 256, 1024, need) == 2         # gqa 32
+    assert slide(16, 8, 320, 1024, need) == 2         # head_dim
+    assert slide(16, 8, 256, 1024, need - 4) == 2     # workspace
+    assert slide(16, 8, 256, 1024, need, wsp=C.c_void_p(264)) == 1
+    assert L.bq_full_attention(*([P] * 8), ws, need, P, 1, P, 16, 2, 512, 10, 1023, -1, 0, 4,
+                               None) == 2              # s_max
+    assert L.bq_attention_splits(1, 8, 1024) == 32
+    assert L.bq_attention_splits(2048, 8, 1024) == 1
+    assert L.bq_attention_splits(16, 2, 100) == 4
+
+
 def test_empty_batches_are_noops(L):
     # seq_len <= 0 returns early (linear.mojo:134-135, 255-256; moe.mojo:317-318)
     assert L.bq_linear(None, None, None, None, None, None, 64, 0, 128, None) == 0
@@ -101,6 +130,8 @@ def test_empty_batches_are_noops(L):
                                   C.c_float(1), None) == 0
     assert L.bq_moe_phase2_down(None, None, None, None, None, None, None, None, 128, 0, 8, 2816,
                                 704, 64, None, 0, None) == 0
+    assert L.bq_full_attention(*([None] * 9), 0, None, 1, None, 16, 2, 512, 10, 1023, -1, 1, 0,
+                               None) == 0
 
 
 def test_workspace_size(L):
