@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16", "head",
-                             "load"])
+                             "attn", "load"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
@@ -344,6 +344,101 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
                 stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3))
 
 
+def bench_attn(bq, torch, steps):
+    """int8-KV attention at the model's shapes (modeling/gemma4_common.mojo):
+    sliding layers (16 q heads, 8 kv heads, head_dim 256, window 1024, two
+    1024-row ring pages per sequence) and full layers (16 q / 2 kv heads,
+    head_dim 512).  Decode: a batch of 16 sequences, one token each, at a
+    full window (sliding) or 4096 positions (full); prefill: one 2048-token
+    chunk.  Caches are uniform random int8 codes with positive scales;
+    every sequence owns its own pages, so a decode batch reads
+    16 x L x kv_heads x (2 head_dim + 8) distinct bytes; decode calls rotate
+    over cache replicas (>= 640 MB in total) so the KV streams from HBM.  The
+    attention prep (per-head RMS, RoPE, FWHT, int8) is timed for the decode
+    batch."""
+    import numpy as np
+    d = "cuda"
+    g = torch.Generator(device=d).manual_seed(3)
+    res = {}
+
+    def make(nq, nkv, hd, window, seqs, page):
+        runs, rows, buf, off, npg = [], [], 0, 0, 0
+        for b, n in seqs:
+            need = 2 if window else (b + n) // page + 1
+            runs.append((buf, b, off, need))
+            rows += list(range(npg, npg + need))
+            npg, off, buf = npg + need, off + need, buf + n
+        T, slots, kvs = buf, npg * page, nkv * hd
+        ri = lambda *sh: torch.randint(-127, 128, sh, dtype=torch.int8, device=d, generator=g)
+        c = dict(kc=ri(slots, kvs), vc=ri(slots, kvs),
+                 ks=torch.rand(slots, nkv, device=d, generator=g) + 1,
+                 vs=torch.rand(slots, nkv, device=d, generator=g) + 1,
+                 q=ri(T, nq * hd), fq=torch.rand(T, nq, device=d, generator=g) + 1,
+                 runs=torch.tensor(runs, dtype=torch.int32, device=d),
+                 rows=torch.tensor([x * page for x in rows], dtype=torch.int32, device=d))
+        c["qb"] = (c["q"].view(T, nq, hd).int().sum(-1) * 128).float()
+        kvbytes = sum(min(window, b + t + 1) if window else b + t + 1
+                      for b, n in seqs for t in range(n)) * nkv * (2 * hd + 8)
+        return c, T, kvbytes
+
+    shapes = {
+        "sliding_decode_b16": (16, 8, 256, 1024, [(3000 + 37 * i, 1) for i in range(16)], 1024),
+        "full_decode_b16_ctx4096": (16, 2, 512, 0, [(4095, 1)] * 16, 1024),
+        "sliding_prefill_2048": (16, 8, 256, 1024, [(0, 2048)], 1024),
+        "full_prefill_2048": (16, 2, 512, 0, [(0, 2048)], 1024),
+    }
+    for name, (nq, nkv, hd, window, seqs, page) in shapes.items():
+        c, T, kvbytes = make(nq, nkv, hd, window, seqs, page)
+        decode = T <= 16
+        # decode: distinct cache replicas, one call each, so every call reads
+        # its KV from HBM (past the 256 MB Infinity Cache) and the graph's
+        # launch cost is spread over several calls
+        nrep = min(8, max(1, -(-640_000_000 // (2 * c["kc"].numel())))) if decode else 1
+        reps = [c] + [dict(c, kc=c["kc"].clone(), vc=c["vc"].clone()) for _ in range(nrep - 1)]
+        maxlen = window if window else max(b + n for b, n in seqs)
+        s_max = bq.attention_splits(T, nkv, maxlen)
+        ws = bq.attention_workspace(T, nq, hd, s_max)
+        out = torch.empty(T, nq * hd, dtype=torch.bfloat16, device=d)
+        geo = (nq, nkv, hd, window, int(np.log2(page)), page - 1, 1 if window else -1)
+        call = lambda i: bq.attention(
+            reps[i]["q"], reps[i]["qb"], reps[i]["fq"], reps[i]["kc"], reps[i]["ks"],
+            reps[i]["vc"], reps[i]["vs"], reps[i]["runs"], reps[i]["rows"], *geo, s_max=s_max,
+            workspace=ws, out=out)
+        gr = graph_of(call, nrep)
+        n = max(64, steps // 4) if decode else max(5, steps // 128)
+        ms, _, _ = time_graph(gr, nrep, n, max(8, n // 8))
+        r = {"us": round(ms * 1e3, 2), "s_max": s_max, "kv_bytes_read": kvbytes,
+             "kv_GBs": round(kvbytes / (ms * 1e-3) / 1e9, 1)}
+        if decode:
+            r["hbm_frac"] = round(kvbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            r["cache_replicas"] = nrep
+            # the prep of the same batch: q/k/v projections' bf16 rows -> codes + cache rows
+            bfr = lambda *sh: torch.randn(*sh, device=d, generator=g).to(torch.bfloat16)
+            src = (bfr(T, nq * hd), bfr(T, nkv * hd), bfr(T, nkv * hd))
+            gam = (bfr(hd), bfr(hd))
+            rope_half = hd // 2 if window else 64
+            maxpos = max(b + n for b, n in seqs) + 1
+            cos = torch.rand(maxpos, rope_half, device=d, generator=g)
+            sin = torch.rand(maxpos, rope_half, device=d, generator=g)
+            qo = (torch.empty(T, nq * hd, dtype=torch.int8, device=d),
+                  torch.empty(T, nq, device=d), torch.empty(T, nq, device=d))
+            sqrt_n = float(np.sqrt(np.float32(hd), dtype=np.float32))
+            n_eps = float(np.float32(hd) * np.float32(1e-6))
+            gp = graph_of(lambda i: bq.attn_prep(*src, *gam, c["kc"], c["ks"], c["vc"], c["vs"],
+                                                 cos, sin, c["runs"], c["rows"], nq, nkv, hd,
+                                                 rope_half, hd // 2, int(np.log2(page)),
+                                                 page - 1, 1 if window else -1, sqrt_n=sqrt_n,
+                                                 n_eps=n_eps, out=qo), 8)
+            pms, _, _ = time_graph(gp, 8, n, max(8, n // 8))
+            r["prep_us"] = round(pms * 1e3, 2)
+        else:
+            # PV is an f32 fma per (position, column) on the vector ALUs
+            flops = 2.0 * kvbytes / (2 * hd + 8) * (nq // nkv) * hd * 2
+            r["tflops_qk_pv"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        res[name] = r
+    return res
+
+
 # ---------------------------------------------------------------------------
 def cpu_baseline_gemv(codes, scales, seconds):
     """The reference CPU path (VNNI u8 x i8, 32-row tiles over worker_range),
@@ -487,6 +582,8 @@ def main():
             res["layer16"] = bench_layer16(bq, torch, Wgu, Wd, max(10, args.steps // 32))
     if wl in ("all", "head"):
         res["head"] = bench_head(bq, torch, args.steps)
+    if wl in ("all", "attn"):
+        res["attn"] = bench_attn(bq, torch, args.steps)
     if wl == "load":
         res["load"] = bench_load(bq, torch)
     if args.calib_copy:
@@ -546,6 +643,8 @@ def main():
                          "hbm_frac": round(v["gbs"] / HBM_PEAK_GBS, 4)}
             for R, v in hd["rows"].items()}
         line["head_flash_sample_v262144"]["alg_bytes"] = hd["alg_bytes"]
+    if "attn" in res:
+        line["attention_int8_kv"] = res["attn"]
     if "gemv" in res and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_gemv(res["gemv"]["codes"], res["gemv"]["scales"],
                                                  args.cpu_seconds)

@@ -282,55 +282,79 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
 
   const int8_t* kbase = a.k_cache + (int64_t)kvh * HD;
   const int8_t* vbase = a.v_cache + (int64_t)kvh * HD + lane * C;
-  for (int p0 = start; p0 < end; p0 += 16) {
-    const int tl = end - p0 < 16 ? end - p0 : 16;
-    // slots of the tile (lane p16); idle lanes repeat the first position
-    const int pp = p16 < tl ? p16 : 0;
-    const int64_t slot = paged_slot(tr.rows, a.page_shift, a.row_mask, a.page_mask,
-                                    tr.lo + p0 + pp);
+  // Slots of 64 consecutive positions [sb, sb + 64) of the split, one per
+  // lane (lanes past the end repeat the last position); slots fit in 32 bits.
+  auto slot_batch = [&](int sb) -> int {
+    const int pj = sb + lane < end ? sb + lane : end - 1;
+    return (int)paged_slot(tr.rows, a.page_shift, a.row_mask, a.page_mask, tr.lo + pj);
+  };
+  // One tile's operands: lane (p + 16 g) holds K row p's bytes [c*64 + g*16,
+  // +16) for every chunk c, its ks and vs; every lane holds its C bytes of
+  // each V row.  Idle positions repeat the tile's first row.
+  struct Tile {
     v4i kb[C];
-    const int8_t* krow = kbase + slot * kvs + grp * 16;
-#pragma unroll
-    for (int c = 0; c < C; ++c) kb[c] = ld16(krow + c * 64);
-    const float ks = a.k_scale[slot * a.num_kv + kvh];
-    const float vs = a.v_scale[slot * a.num_kv + kvh];
-    // V rows of the tile, this lane's C bytes of each
     uint32_t vraw[16][(C + 3) / 4];
-    const int slot_lo = (int)slot;  // slots fit in 32 bits (checked by the host)
+    float ks, vs;
+  };
+  auto load_tile = [&](Tile& t, int p0, int slots, int sb) {
+    const int tl = end - p0 < 16 ? end - p0 : 16;
+    const int off = p0 - sb;
+    const int my = __shfl(slots, off + (p16 < tl ? p16 : 0), kWave);
+    const int8_t* krow = kbase + (int64_t)my * kvs + grp * 16;
+#pragma unroll
+    for (int c = 0; c < C; ++c) t.kb[c] = ld16(krow + c * 64);
+    t.ks = a.k_scale[(int64_t)my * a.num_kv + kvh];
+    t.vs = a.v_scale[(int64_t)my * a.num_kv + kvh];
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
-      if (p < tl) {
-        const int sp = __builtin_amdgcn_readlane(slot_lo, p);
+      {
+        const int sp = __builtin_amdgcn_readlane(slots, off + (p < tl ? p : 0));
         const int8_t* vr = vbase + (int64_t)sp * kvs;
         if constexpr (C >= 8) {
           const uint2 w = *reinterpret_cast<const uint2*>(vr);
-          vraw[p][0] = w.x; vraw[p][1] = w.y;
+          t.vraw[p][0] = w.x; t.vraw[p][1] = w.y;
         } else if constexpr (C == 4) {
-          vraw[p][0] = *reinterpret_cast<const uint32_t*>(vr);
+          t.vraw[p][0] = *reinterpret_cast<const uint32_t*>(vr);
         } else if constexpr (C == 2) {
-          vraw[p][0] = *reinterpret_cast<const uint16_t*>(vr);
+          t.vraw[p][0] = *reinterpret_cast<const uint16_t*>(vr);
         } else {
-          vraw[p][0] = (uint8_t)*vr;
+          t.vraw[p][0] = (uint8_t)*vr;
         }
       }
     }
+  };
+
+  // (loading the next tile before this tile's arithmetic measured no faster:
+  // the kernel is bound by VALU issue once several waves share a SIMD)
+  Tile cur;
+  int sb = start, slots = 0;
+  if (start < end) slots = slot_batch(sb);
+  for (int p0 = start; p0 < end; p0 += 16) {
+    const int tl = end - p0 < 16 ? end - p0 : 16;
+    if (p0 - sb >= 64) {
+      sb = p0;
+      slots = slot_batch(sb);
+    }
+    load_tile(cur, p0, slots, sb);
     v4i d = zero4;
 #pragma unroll
-    for (int c = 0; c < C; ++c) d = mfma16x16x64(qa[c], kb[c], d);
+    for (int c = 0; c < C; ++c) d = mfma16x16x64(qa[c], cur.kb[c], d);
     const int dv[4] = {d.x, d.y, d.z, d.w};
+    // per head of this lane's group (heads 4 g + i, only i < G exist)
+    constexpr int NI = G < 4 ? G : 4;
     float sc[4], corr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
       float sco = -1e30f;
       if (4 * grp + i < G && p16 < tl)
-        sco = (((float)(dv[i] + qsum128[i]) - qb[i]) * fq[i]) * ks * inv127sq;
+        sco = (((float)(dv[i] + qsum128[i]) - qb[i]) * fq[i]) * cur.ks * inv127sq;
       const float tmax = group_max(sco, 16);
       const float m_new = tmax > m[i] ? tmax : m[i];
       corr[i] = fast_exp_softmax_biased(max87(m[i] - m_new));
       const float w = fast_exp_softmax_biased(max87(sco - m_new));
       l[i] = l[i] * corr[i] + tree16(w);
       m[i] = m_new;
-      sc[i] = p16 < tl ? w * vs * inv127 : 0.0f;
+      sc[i] = p16 < tl ? w * cur.vs * inv127 : 0.0f;
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -338,19 +362,20 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
 #pragma unroll
       for (int c = 0; c < C; ++c) acc[h][c] = acc[h][c] * ch;
     }
+    // positions past the tile's end carry weight 0: acc + v*0 leaves acc
+    // unchanged bit for bit (acc is never -0: it starts at +0 and only an
+    // exact -0 product added to -0 gives -0), so the loop needs no branch
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
-      if (p < tl) {
-        float vf[C];
+      float vf[C];
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-          vf[c] = (float)(int8_t)(vraw[p][c / 4] >> (8 * (c % 4)));
+      for (int c = 0; c < C; ++c)
+        vf[c] = (float)(int8_t)(cur.vraw[p][c / 4] >> (8 * (c % 4)));
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float w = readlane_f(sc[h % 4], p + 16 * (h / 4));
+      for (int h = 0; h < G; ++h) {
+        const float w = readlane_f(sc[h % 4], p + 16 * (h / 4));
 #pragma unroll
-          for (int c = 0; c < C; ++c) acc[h][c] = fmaf(vf[c], w, acc[h][c]);
-        }
+        for (int c = 0; c < C; ++c) acc[h][c] = fmaf(vf[c], w, acc[h][c]);
       }
     }
   }
@@ -391,10 +416,12 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
 // ---------------------------------------------------------------------------
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
-  constexpr int C = HD / 64;
+  // one wave per (token, query head, 128-column slice); lane owns CL columns
+  constexpr int CW = HD < 128 ? HD : 128, CL = CW / 64, NW = HD / CW;
   const int wave = threadIdx.x >> 6, lane = lane_id();
-  const int item = blockIdx.x * 4 + wave;
-  if (item >= a.T * a.num_q) return;
+  const int witem = blockIdx.x * 4 + wave;
+  if (witem >= a.T * a.num_q * NW) return;
+  const int item = witem / NW, col0 = (witem % NW) * CW + lane * CL;
   const int tok = item / a.num_q;
   const TokRange tr = token_range(a, tok);
   const int S = num_splits(tr.L, a.s_max);
@@ -406,40 +433,134 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     const float v = s0 + lane < S ? ml[(s0 + lane) * 2] : -1e30f;
     gm = fmaxf(gm, wave_max(v));
   }
-  // global l: batches of 16 splits, each a 16-lane tree of l * c
-  float gl = 0.0f;
+  float gl = 0.0f, out[CL];
+  bool first = true;
   for (int s0 = 0; s0 < S; s0 += kWave) {
+    // the corrections of 64 splits, lane-parallel; masked by l > 0
     const int sidx = s0 + lane;
     float d = -1e30f, ls = 0.0f;
     if (sidx < S) { d = ml[sidx * 2] - gm; ls = ml[sidx * 2 + 1]; }
     float c = fast_exp_softmax_biased(max87(d));
     if (!(ls > 0.0f)) c = 0.0f;
+    // global l: batches of 16 splits, each a 16-lane tree of l * c
     const float bsum = tree16(ls * c);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (s0 + 16 * q < S) gl = gl + readlane_f(bsum, 16 * q);
-  }
-  float out[C];
-  bool first = true;
-  for (int s = 0; s < S; ++s) {
-    const float ls = ml[s * 2 + 1];
-    float c = fast_exp_softmax_biased(max87(ml[s * 2] - gm));
-    if (!(ls > 0.0f)) c = 0.0f;
-    if (c <= 0.0f) continue;
-    const float* src = a.ws_acc + (base + s) * HD + lane * C;
+    // acc: splits in order, 8 rows in flight
+    const int n = S - s0 < kWave ? S - s0 : kWave;
+    const float* src0 = a.ws_acc + (base + s0) * HD + col0;
+    for (int b0 = 0; b0 < n; b0 += 8) {
+      float rows[8][CL];
 #pragma unroll
-    for (int cc = 0; cc < C; ++cc) out[cc] = first ? src[cc] * c : fmaf(src[cc], c, out[cc]);
-    first = false;
+      for (int b = 0; b < 8; ++b)
+        if (b0 + b < n) {
+#pragma unroll
+          for (int cc = 0; cc < CL; ++cc) rows[b][cc] = src0[(int64_t)(b0 + b) * HD + cc];
+        }
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        if (b0 + b >= n) break;
+        const float cb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), b0 + b));
+        if (cb <= 0.0f) continue;
+#pragma unroll
+        for (int cc = 0; cc < CL; ++cc)
+          out[cc] = first ? rows[b][cc] * cb : fmaf(rows[b][cc], cb, out[cc]);
+        first = false;
+      }
+    }
   }
-  uint16_t* dst = a.out + (int64_t)item * HD + lane * C;
+  uint16_t* dst = a.out + (int64_t)item * HD + col0;
   if (!(gl > 0.0f)) {
 #pragma unroll
-    for (int cc = 0; cc < C; ++cc) dst[cc] = 0;
+    for (int cc = 0; cc < CL; ++cc) dst[cc] = 0;
     return;
   }
   const float inv_l = 1.0f / gl;
 #pragma unroll
-  for (int cc = 0; cc < C; ++cc) dst[cc] = f32_to_bf16(out[cc] * inv_l);
+  for (int cc = 0; cc < CL; ++cc) dst[cc] = f32_to_bf16(out[cc] * inv_l);
+}
+
+// Merge for many splits: one workgroup per (token, query head, 64-column
+// slice).  The four waves stage up to 240 splits (their (m, l) and the slice
+// of their acc rows) in LDS with all loads in flight at once; wave 0 then runs
+// the ordered chain from LDS, eight rows per batch.
+constexpr int kMergeStage = 240;  // 240 x 66 floats: under 64 KiB of LDS
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_merge_lds(AttnArgs a) {
+  constexpr int NW = HD / 64;
+  extern __shared__ float stage[];  // [n][64] acc slice, then [n] m, [n] l
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int item = blockIdx.x / NW, col = (blockIdx.x % NW) * 64 + lane;
+  const int tok = item / a.num_q;
+  const TokRange tr = token_range(a, tok);
+  const int S = num_splits(tr.L, a.s_max);
+  if (a.window > 0 && S == 1) return;  // finalized by the attention wave
+  const int64_t base = (int64_t)item * a.s_max;
+  const float* ml = a.ws_ml + base * 2;
+  const int cap = a.s_max < kMergeStage ? a.s_max : kMergeStage;
+  float* sm = stage + cap * 64;
+  float* sl = sm + cap;
+  // global max over all splits (every wave, lane-parallel)
+  float gm = -1e30f;
+  for (int s0 = 0; s0 < S; s0 += kWave) {
+    const float v = s0 + lane < S ? ml[(s0 + lane) * 2] : -1e30f;
+    gm = fmaxf(gm, wave_max(v));
+  }
+  float gl = 0.0f, out = 0.0f;
+  bool first = true;
+  for (int c0 = 0; c0 < S; c0 += kMergeStage) {
+    const int n = S - c0 < kMergeStage ? S - c0 : kMergeStage;
+    __syncthreads();
+    for (int r = wave; r < n; r += 4) stage[r * 64 + lane] = a.ws_acc[(base + c0 + r) * HD + col];
+    for (int r = threadIdx.x; r < n; r += 256) {
+      sm[r] = ml[(c0 + r) * 2];
+      sl[r] = ml[(c0 + r) * 2 + 1];
+    }
+    __syncthreads();
+    if (wave != 0) continue;
+    for (int s0 = 0; s0 < n; s0 += kWave) {
+      const int m = n - s0 < kWave ? n - s0 : kWave;
+      float d = -1e30f, ls = 0.0f;
+      if (lane < m) { d = sm[s0 + lane] - gm; ls = sl[s0 + lane]; }
+      float c = fast_exp_softmax_biased(max87(d));
+      if (!(ls > 0.0f)) c = 0.0f;
+      // global l: batches of 16 splits, each a 16-lane tree of l * c
+      const float bsum = tree16(ls * c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (16 * q < m) gl = gl + readlane_f(bsum, 16 * q);
+      const unsigned long long live = __ballot(lane < m && c > 0.0f);
+      const unsigned long long all = m == 64 ? ~0ull : ((1ull << m) - 1);
+      int b = 0;
+      if (first && (live & 1ull)) {  // the first contributing split is multiplied
+        out = stage[s0 * 64 + lane] * readlane_f(c, 0);
+        first = false;
+        b = 1;
+      }
+      if (!first && live == all) {
+        // every split contributes: branch-free chain, eight LDS rows per batch
+        for (; b + 8 <= m; b += 8) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = stage[(s0 + b + u) * 64 + lane];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) out = fmaf(v[u], readlane_f(c, b + u), out);
+        }
+      }
+      for (; b < m; ++b) {
+        const float cb = readlane_f(c, b);
+        if (cb <= 0.0f) continue;
+        const float v = stage[(s0 + b) * 64 + lane];
+        out = first ? v * cb : fmaf(v, cb, out);
+        first = false;
+      }
+    }
+  }
+  if (wave != 0) return;
+  uint16_t* dst = a.out + (int64_t)item * HD + col;
+  *dst = gl > 0.0f ? f32_to_bf16(out * (1.0f / gl)) : (uint16_t)0;
 }
 
 // ---------------------------------------------------------------------------
@@ -473,8 +594,14 @@ static hipError_t launch_attn_hd(const AttnArgs& a, int gqa, hipStream_t st) {
     case 16: hipLaunchKernelGGL((k_flash_attn<HD, 16>), g, b, 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
-  const dim3 gm((a.T * a.num_q + 3) / 4);
-  hipLaunchKernelGGL(k_attn_merge<HD>, gm, b, 0, st, a);
+  if (a.s_max > 8) {
+    const size_t lds = (size_t)(a.s_max < kMergeStage ? a.s_max : kMergeStage) * 66 * sizeof(float);
+    hipLaunchKernelGGL(k_attn_merge_lds<HD>, dim3(a.T * a.num_q * (HD / 64)), b, lds, st, a);
+  } else {
+    constexpr int NW = HD < 128 ? 1 : HD / 128;
+    const dim3 gm((a.T * a.num_q * NW + 3) / 4);
+    hipLaunchKernelGGL(k_attn_merge<HD>, gm, b, 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -82,6 +82,14 @@ def test_attention_many_splits(gpu, O):
     check(gpu, O, c, 64)
 
 
+def test_attention_splits_beyond_one_stage(gpu, O):
+    # 282 splits for the long token: the many-split merge stages them in two
+    # LDS passes (240 + 42)
+    c = make_case(O, 12, num_q=2, num_kv=1, head_dim=64, page_len=64, window=0,
+                  seqs=[(9000, 1), (100, 1)])
+    check(gpu, O, c, 300)
+
+
 def prep_case(O, seed, hd, rope_half, ps, nq, nkv, seqs, page, degree=1, rank=0,
               k_eq_v=False):
     rng = np.random.default_rng(seed)
