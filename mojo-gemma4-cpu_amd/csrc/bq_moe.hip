@@ -388,7 +388,8 @@ int moe_tile_bm(int max_routes, int experts) {
   const int per = max_routes / (experts > 0 ? experts : 1);
   if (per < 24) return 16;
   const double hi = per + 4.0 * __builtin_sqrt((double)per);
-  if (hi > 128.0) return 256;
+  if (hi > 192.0) return 256;
+  if (hi > 128.0) return 192;  // 2048 tokens x top-8 / 128 experts: 128 + 45
   if (hi > 64.0) return 128;
   return 64;
 }
@@ -425,7 +426,9 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
   if (max_routes > 0) {
     const int bm = moe_tile_bm(max_routes, experts);
     if (bm >= 64 && hidden % 128 == 0) {
-      const int bm_down = getenv("BQ_MOE_BM") ? bm : 64;  // see launch_moe_down_tiled
+      // see launch_moe_down_tiled; BQ_MOE_BM_DOWN overrides the down tile alone
+      const char* bd = getenv("BQ_MOE_BM_DOWN");
+      const int bm_down = bd ? atoi(bd) : getenv("BQ_MOE_BM") ? bm : 64;
       hipError_t e = launch_moe_down_tiled(bucket_i8, bucket_sa, eo, routes, w_down, down_scale, y,
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;

@@ -453,6 +453,15 @@ static void launch_bm(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t 
     }
     launch_cfg<MODE, 256, 128, 4, 2, PB>(nbuf, g, dyn, st, t);
   }
+  else if (bm >= 192) {
+    // 192-record m-tiles (4 x 2 waves of 48 x 64 or 48 x 128): one tile per
+    // expert at ~128 routes per expert with two thirds of the rows live,
+    // where 256-record tiles carry half of them empty
+    if constexpr (!PB) {
+      if (bn >= 256) { launch_cfg<MODE, 192, 256, 4, 2, PB>(nbuf, g, dyn, st, t); return; }
+    }
+    launch_cfg<MODE, 192, 128, 4, 2, PB>(nbuf, g, dyn, st, t);
+  }
   else if (bm >= 128) launch_bn<MODE, 128, PB>(bn, nbuf, g, dyn, st, t);
   else if (bm >= 64) launch_bn<MODE, 64, PB>(bn, nbuf, g, dyn, st, t);
   else launch_bn<MODE, 32, PB>(bn, nbuf, g, dyn, st, t);
@@ -495,11 +504,11 @@ hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const
   t.a = x_i8; t.a_scale = x_sa; t.eo = eo; t.routes = routes; t.w = w_gu; t.ws = gu_scale;
   t.bucket = bucket; t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
   t.inter = inter; t.block = hidden;
-  const int bmv = bm >= 256 ? 256 : bm >= 128 ? 128 : 64;
+  const int bmv = bm >= 256 ? 256 : bm >= 192 ? 192 : bm >= 128 ? 128 : 64;
   // weight rows per tile: bn/2 gate + bn/2 up.  256-record tiles pair with
   // 256 weight rows: each expert's weights and each activation tile then
   // stream the fewest times (measured best at 2048 tokens x 128 experts).
-  const int bn = tile_bn(env_int("BQ_TILE_BN", bmv == 256 ? 256 : 128));
+  const int bn = tile_bn(env_int("BQ_TILE_BN", bmv >= 192 ? 256 : 128));
   const int nbuf = env_int("BQ_RING", 2);
   t.gn = (inter + bn / 2 - 1) / (bn / 2);
   t.gm = mtile_bound(max_routes, experts, bmv);
@@ -520,7 +529,7 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
   // the down projection's K (= inter) is short, and its per-block drains
   // keep f32 accumulators: 64-record tiles with a double-buffered stage run
   // fastest (more workgroups in flight per CU)
-  const int bmv = bm >= 256 ? 256 : bm >= 128 ? 128 : 64;
+  const int bmv = bm >= 256 ? 256 : bm >= 192 ? 192 : bm >= 128 ? 128 : 64;
   const int bn = tile_bn(env_int("BQ_TILE_BN", 128));
   const int nbuf = env_int("BQ_RING", 2);
   t.gn = (hidden + bn - 1) / bn;

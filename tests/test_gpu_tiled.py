@@ -70,7 +70,8 @@ def _tiny_moe(O, gpu, T, E=4, k=2, H=128, I=64, seed=5):
                                      (33, 64, None), (256, 128, 128), (256, 64, 64),
                                      (300, 128, 256), (300, 64, 256), (300, 256, None),
                                      (64, 256, None), (600, 256, None), (600, 256, 256),
-                                     (300, 256, 256)])
+                                     (300, 256, 256), (300, 192, None), (600, 192, 256),
+                                     (600, 192, 128), (64, 192, None)])
 def test_moe_tiled(gpu, O, monkeypatch, T, bm, bn):
     if bm is not None:
         monkeypatch.setenv("BQ_MOE_BM", str(bm))
@@ -94,10 +95,12 @@ def test_moe_tiled(gpu, O, monkeypatch, T, bm, bn):
     tol_check(host(accum), racc)
 
 
-def test_moe_gate_up_hidden2816(gpu, O):
-    # model hidden size (K/64 = 44) with 128-165 routes per expert: 256-record
-    # tiles with partial m-tiles and a partial gate/up n-tile (inter 192)
-    T, E, k, H, I = 600, 8, 2, 2816, 192
+@pytest.mark.parametrize("T", [600, 512])
+def test_moe_gate_up_hidden2816(gpu, O, T):
+    # model hidden size (K/64 = 44) with ~150 (T = 600: 256-record tiles) or
+    # ~128 (T = 512: 192-record tiles) routes per expert: partial m-tiles and a
+    # partial gate/up n-tile (inter 192)
+    E, k, H, I = 8, 2, 2816, 192
     logits = O.synth_normal_f32(21, 1.0, (T, E))
     idx, w = O.route_topk_softmax(logits, k)
     gu = O.bf16_to_f32(O.synth_normal_bf16(22, 0.02, (E * 2 * I, H)))
