@@ -211,6 +211,8 @@ template <int HD, int G>
 __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
   constexpr int C = HD / 64;  // 64-byte K chunks per row = V bytes per lane
   const int wave = threadIdx.x >> 6, lane = lane_id();
+  __shared__ __attribute__((aligned(16))) float s_w[4][16 * G];  // per wave: weights [p][head]
+  float* wsh = s_w[wave];
   const int per_tok = a.num_kv * a.s_max;
   const int item = blockIdx.x * 4 + wave;
   if (item >= a.T * per_tok) return;
@@ -364,23 +366,45 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
     }
     // positions past the tile's end carry weight 0: acc + v*0 leaves acc
     // unchanged bit for bit (acc is never -0: it starts at +0 and only an
-    // exact -0 product added to -0 gives -0), so the loop needs no branch
+    // exact -0 product added to -0 gives -0), so the loop needs no branch.
+    // The weights go through LDS as [p][head] and are read broadcast.
+    if constexpr (G >= 4) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        if (4 * grp + i < G) wsh[p16 * G + 4 * grp + i] = sc[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        if (grp == 0) wsh[p16 * G + i] = sc[i];
+    }
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       float vf[C];
 #pragma unroll
       for (int c = 0; c < C; ++c)
         vf[c] = (float)(int8_t)(cur.vraw[p][c / 4] >> (8 * (c % 4)));
+      float w[G];
+      if constexpr (G >= 4) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float w = readlane_f(sc[h % 4], p + 16 * (h / 4));
+        for (int h4 = 0; h4 < G / 4; ++h4) {
+          const float4 w4 = *reinterpret_cast<const float4*>(&wsh[p * G + 4 * h4]);
+          w[4 * h4] = w4.x; w[4 * h4 + 1] = w4.y; w[4 * h4 + 2] = w4.z; w[4 * h4 + 3] = w4.w;
+        }
+      } else {
 #pragma unroll
-        for (int c = 0; c < C; ++c) acc[h][c] = fmaf(vf[c], w, acc[h][c]);
+        for (int h = 0; h < G; ++h) w[h] = wsh[p * G + h];
       }
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[h][c] = fmaf(vf[c], w[h], acc[h][c]);
     }
   }
 
-  const bool direct = a.window > 0 && S == 1;
+  // finished here: a sliding token with one split (acc * (1/l)), and every
+  // token when the plan has one split (full layers: the merge of one split,
+  // (acc * c) * (1/(l * c)) with c = fast_exp(0))
+  const bool direct = S == 1 && (a.window > 0 || a.s_max == 1);
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float mh = readlane_f(m[h % 4], 16 * (h / 4));
@@ -388,13 +412,16 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
     const int64_t qrow = (int64_t)tok * a.num_q + qh0 + h;
     if (direct) {
       uint16_t o[C];
-      if (lh > 0.0f) {
-        const float inv_l = 1.0f / lh;
+      if (a.window > 0) {
+        const float inv_l = lh > 0.0f ? 1.0f / lh : 0.0f;
 #pragma unroll
-        for (int c = 0; c < C; ++c) o[c] = f32_to_bf16(acc[h][c] * inv_l);
+        for (int c = 0; c < C; ++c) o[c] = lh > 0.0f ? f32_to_bf16(acc[h][c] * inv_l) : 0;
       } else {
+        const float cm = lh > 0.0f ? fast_exp_softmax_biased(0.0f) : 0.0f;
+        const float gl = 0.0f + lh * cm;
+        const float inv_l = gl > 0.0f ? 1.0f / gl : 0.0f;
 #pragma unroll
-        for (int c = 0; c < C; ++c) o[c] = 0;
+        for (int c = 0; c < C; ++c) o[c] = gl > 0.0f ? f32_to_bf16((acc[h][c] * cm) * inv_l) : 0;
       }
       uint16_t* dst = a.out + qrow * HD + lane * C;
 #pragma unroll
@@ -408,6 +435,240 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
         a.ws_ml[(qrow * a.s_max + s) * 2 + 1] = lh;
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Single-split tokens (s_max == 1, prefill chunks): TPW = 16 / G query tokens
+// per wave share every K/V tile.  The wave takes the tokens tok0 + 16 k
+// (k < TPW) of one run: their ranges start at positions that are equal mod 16
+// (sliding: lo = pos - window + 1 once pos >= window - 1, else 0; full: 0),
+// so all their 16-position tiles sit on one grid and a tile of the grid is,
+// for each token, either one of its own tiles or outside its range.  Rows of
+// the MFMA are (token k, head h) = 16 rows; each row keeps its own m, l, acc
+// and runs the reference's tile recursion; the V conversion and the K/V loads
+// are shared by the 16 rows.  Tokens that do not share a grid (a group that
+// straddles pos = window - 1, or spans two runs) are processed one per pass.
+// Results are those of the one-split path: acc * (1/l) for sliding layers,
+// the one-split merge ((acc * c) * (1/(l * c)), c = fast_exp(0)) for full.
+// ---------------------------------------------------------------------------
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_flash_attn_mt(AttnArgs a) {
+  constexpr int C = HD / 64, TPW = 16 / G;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  __shared__ __attribute__((aligned(16))) float s_w[4][16 * 16];  // per wave: weights [p][row]
+  const int nblk = (a.T + 16 * TPW - 1) / (16 * TPW);
+  const int item = blockIdx.x * 4 + wave;
+  if (item >= nblk * a.num_kv * 16) return;
+  const int cls = item % 16, kvh = (item / 16) % a.num_kv, blk = item / (16 * a.num_kv);
+  const int tok0 = blk * 16 * TPW + cls;
+  const int64_t kvs = (int64_t)a.num_kv * HD;
+  const int p16 = lane & 15, grp = lane >> 4;
+
+  // per-token range (wave-uniform): run, [lo, hi) of positions
+  int run_k[TPW];
+  int lo_k[TPW], hi_k[TPW];  // positions fit in 32 bits
+  bool shared = true;
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    const int tok = tok0 + 16 * k;
+    run_k[k] = -1; lo_k[k] = 0; hi_k[k] = 0;
+    if (tok >= a.T) continue;
+    const TokRange tr = token_range(a, tok);
+    run_k[k] = run_of(a.runs, a.num_runs, tok);
+    lo_k[k] = (int)tr.lo;
+    hi_k[k] = (int)tr.lo + tr.L;
+    if (run_k[k] != run_k[0] || ((lo_k[k] - lo_k[0]) & 15) != 0) shared = false;
+  }
+
+  // A operand: row r = k * G + h (token k, head h); lane (r + 16 g) holds
+  // row r's bytes [c*64 + g*16, +16)
+  const v4i zero4 = {0, 0, 0, 0};
+  v4i qa[C];
+  {
+    const int r = lane & 15, k = r / G, h = r % G;
+    const int tok = tok0 + 16 * k;
+    const int8_t* qrow = a.q_i8 + ((int64_t)(tok < a.T ? tok : 0) * a.num_q + kvh * G + h) * HD +
+                         grp * 16;
+#pragma unroll
+    for (int c = 0; c < C; ++c) qa[c] = tok < a.T ? ld16(qrow + c * 64) : zero4;
+  }
+  // score layout: lane (p + 16 g), value i <-> row 4 g + i
+  float qb[4], fq[4];
+  int qsum128[4];
+  {
+    int part = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int w4[4] = {qa[c].x, qa[c].y, qa[c].z, qa[c].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        part += (int)(int8_t)w4[q] + (int)(int8_t)(w4[q] >> 8) + (int)(int8_t)(w4[q] >> 16) +
+                (w4[q] >> 24);
+    }
+    part += __shfl_xor(part, 16, kWave);
+    part += __shfl_xor(part, 32, kWave);  // lane r (and r + 16 g): sum of row r's codes
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * grp + i, k = r / G, h = r % G, tok = tok0 + 16 * k;
+      qsum128[i] = 128 * __shfl(part, r, kWave);
+      qb[i] = 0.0f; fq[i] = 0.0f;
+      if (tok < a.T) {
+        qb[i] = a.qi_bias[(int64_t)tok * a.num_q + kvh * G + h];
+        fq[i] = a.f_q[(int64_t)tok * a.num_q + kvh * G + h];
+      }
+    }
+  }
+
+  const float inv127 = 1.0f / 127.0f;
+  const float inv127sq = inv127 * inv127;
+  float m[4], l[4];
+  float acc[16][C];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { m[i] = -1e30f; l[i] = 0.0f; }
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = 0.0f;
+  const int8_t* kbase = a.k_cache + (int64_t)kvh * HD;
+  const int8_t* vbase = a.v_cache + (int64_t)kvh * HD + lane * C;
+
+  // one pass over all tokens (shared grid) or one pass per token
+  const int npass = shared ? 1 : TPW;
+  for (int pass = 0; pass < npass; ++pass) {
+    // active tokens of this pass and the position range they cover
+    unsigned amask = 0;
+    int pbeg = 0, pend = 0;
+    int run = -1;
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+      const bool on = run_k[k] >= 0 && (shared || k == pass) && hi_k[k] > lo_k[k];
+      if (!on) continue;
+      if (amask == 0) { pbeg = lo_k[k]; pend = hi_k[k]; run = run_k[k]; }
+      pbeg = lo_k[k] < pbeg ? lo_k[k] : pbeg;
+      pend = hi_k[k] > pend ? hi_k[k] : pend;
+      amask |= 1u << k;
+    }
+    if (amask == 0) continue;
+    const int32_t* rows = a.base_rows + a.runs[run].rows_off;
+    for (int P = pbeg; P < pend; P += 16) {
+      // rows taking part in this tile, and their tile lengths
+      unsigned rmask = 0;
+      int tl_k[TPW];
+#pragma unroll
+      for (int k = 0; k < TPW; ++k) {
+        tl_k[k] = 0;
+        if (!((amask >> k) & 1u) || P < lo_k[k] || P >= hi_k[k]) continue;
+        tl_k[k] = hi_k[k] - P < 16 ? hi_k[k] - P : 16;
+        rmask |= ((1u << G) - 1u) << (k * G);
+      }
+      const int tlen = pend - P < 16 ? pend - P : 16;
+      const int pp = p16 < tlen ? p16 : 0;
+      const int slot = (int)paged_slot(rows, a.page_shift, a.row_mask, a.page_mask, P + pp);
+      v4i kb[C];
+      const int8_t* krow = kbase + (int64_t)slot * kvs + grp * 16;
+#pragma unroll
+      for (int c = 0; c < C; ++c) kb[c] = ld16(krow + c * 64);
+      const float ks = a.k_scale[(int64_t)slot * a.num_kv + kvh];
+      const float vs = a.v_scale[(int64_t)slot * a.num_kv + kvh];
+      uint32_t vraw[16][(C + 3) / 4];
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const int sp = __builtin_amdgcn_readlane(slot, p < tlen ? p : 0);
+        const int8_t* vr = vbase + (int64_t)sp * kvs;
+        if constexpr (C >= 8) {
+          const uint2 w = *reinterpret_cast<const uint2*>(vr);
+          vraw[p][0] = w.x; vraw[p][1] = w.y;
+        } else if constexpr (C == 4) {
+          vraw[p][0] = *reinterpret_cast<const uint32_t*>(vr);
+        } else if constexpr (C == 2) {
+          vraw[p][0] = *reinterpret_cast<const uint16_t*>(vr);
+        } else {
+          vraw[p][0] = (uint8_t)*vr;
+        }
+      }
+      v4i d = zero4;
+#pragma unroll
+      for (int c = 0; c < C; ++c) d = mfma16x16x64(qa[c], kb[c], d);
+      const int dv[4] = {d.x, d.y, d.z, d.w};
+      float sc[4], corr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * grp + i;
+        const bool on = (rmask >> r) & 1u;
+        // this row's tile length (lane-varying through the token index)
+        int tl = 0;
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) tl = r / G == k ? tl_k[k] : tl;
+        float sco = -1e30f;
+        if (on && p16 < tl)
+          sco = (((float)(dv[i] + qsum128[i]) - qb[i]) * fq[i]) * ks * inv127sq;
+        const float tmax = group_max(sco, 16);
+        const float m_new = tmax > m[i] ? tmax : m[i];
+        const float cr = fast_exp_softmax_biased(max87(m[i] - m_new));
+        const float w = fast_exp_softmax_biased(max87(sco - m_new));
+        const float wsum = tree16(w);
+        corr[i] = on ? cr : 1.0f;
+        if (on) {
+          l[i] = l[i] * cr + wsum;
+          m[i] = m_new;
+        }
+        sc[i] = on && p16 < tl ? w * vs * inv127 : 0.0f;
+      }
+      // every row takes part in the update: a row outside this tile has
+      // corr 1 and weights 0, which leave its acc bit for bit (acc * 1 = acc,
+      // acc + v*0 = acc since acc is never -0), so the loops need no branches.
+      // The weights go through LDS as [p][row]; every lane reads them
+      // broadcast, four rows per read.
+      float* wsh = s_w[wave];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wsh[p16 * 16 + 4 * grp + i] = sc[i];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float ch = readlane_f(corr[r % 4], 16 * (r / 4));
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[r][c] = acc[r][c] * ch;
+      }
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        float vf[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) vf[c] = (float)(int8_t)(vraw[p][c / 4] >> (8 * (c % 4)));
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 w4 = *reinterpret_cast<const float4*>(&wsh[p * 16 + 4 * r4]);
+          const float wr[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+              acc[4 * r4 + q][c] = fmaf(vf[c], wr[q], acc[4 * r4 + q][c]);
+        }
+      }
+    }
+  }
+
+  // finalize every row of a real token
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int k = r / G, h = r % G, tok = tok0 + 16 * k;
+    if (tok >= a.T) continue;
+    const float lr = readlane_f(l[r % 4], 16 * (r / 4));
+    uint16_t o[C];
+    if (a.window > 0) {  // sliding prefill: acc * (1/l), or zeros
+      const float inv_l = lr > 0.0f ? 1.0f / lr : 0.0f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) o[c] = lr > 0.0f ? f32_to_bf16(acc[r][c] * inv_l) : 0;
+    } else {             // the merge of one split
+      const float cm = lr > 0.0f ? fast_exp_softmax_biased(0.0f) : 0.0f;
+      const float gl = 0.0f + lr * cm;
+      const float inv_l = gl > 0.0f ? 1.0f / gl : 0.0f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) o[c] = gl > 0.0f ? f32_to_bf16((acc[r][c] * cm) * inv_l) : 0;
+    }
+    uint16_t* dst = a.out + ((int64_t)tok * a.num_q + kvh * G + h) * HD + lane * C;
+#pragma unroll
+    for (int c = 0; c < C; ++c) dst[c] = o[c];
   }
 }
 
@@ -584,8 +845,23 @@ hipError_t launch_attn_prep(const PrepArgs& args, int head_dim, hipStream_t st) 
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int gqa, hipStream_t st) {
+  const dim3 b(256);
+  if (a.s_max == 1 && gqa <= 8 && HD <= 256) {
+    // one split per token: 16/G tokens per wave, finalized in the wave
+    const int tpw = 16 / gqa;
+    const int items = (a.T + 16 * tpw - 1) / (16 * tpw) * a.num_kv * 16;
+    const dim3 g((items + 3) / 4);
+    switch (gqa) {
+      case 1: hipLaunchKernelGGL((k_flash_attn_mt<HD, 1>), g, b, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((k_flash_attn_mt<HD, 2>), g, b, 0, st, a); break;
+      case 4: hipLaunchKernelGGL((k_flash_attn_mt<HD, 4>), g, b, 0, st, a); break;
+      case 8: hipLaunchKernelGGL((k_flash_attn_mt<HD, 8>), g, b, 0, st, a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const int items = a.T * a.num_kv * a.s_max;
-  const dim3 g((items + 3) / 4), b(256);
+  const dim3 g((items + 3) / 4);
   switch (gqa) {
     case 1: hipLaunchKernelGGL((k_flash_attn<HD, 1>), g, b, 0, st, a); break;
     case 2: hipLaunchKernelGGL((k_flash_attn<HD, 2>), g, b, 0, st, a); break;
@@ -594,6 +870,7 @@ static hipError_t launch_attn_hd(const AttnArgs& a, int gqa, hipStream_t st) {
     case 16: hipLaunchKernelGGL((k_flash_attn<HD, 16>), g, b, 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
+  if (a.s_max == 1) return hipGetLastError();  // every token finished in the wave
   if (a.s_max > 8) {
     const size_t lds = (size_t)(a.s_max < kMergeStage ? a.s_max : kMergeStage) * 66 * sizeof(float);
     hipLaunchKernelGGL(k_attn_merge_lds<HD>, dim3(a.T * a.num_q * (HD / 64)), b, lds, st, a);

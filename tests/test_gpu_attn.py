@@ -90,6 +90,20 @@ def test_attention_splits_beyond_one_stage(gpu, O):
     check(gpu, O, c, 300)
 
 
+@pytest.mark.parametrize("gqa,hd", [(1, 64), (2, 128), (2, 256), (4, 128), (8, 64), (8, 256)])
+@pytest.mark.parametrize("window,seqs", [
+    (40, [(50, 70)]),             # every token past the window start: shifted tile grids
+    (40, [(5, 70), (200, 3)]),    # a run straddling pos = window - 1, then a short run
+    (0, [(0, 130), (37, 20)]),    # full attention, two runs
+])
+def test_attention_single_split_groups(gpu, O, gqa, hd, window, seqs):
+    # one split per token (s_max = 1): tokens t, t + 16, ... of a run share a
+    # wave when their tile grids coincide; the rest run one per pass
+    c = make_case(O, gqa * 3 + hd + window, num_q=2 * gqa, num_kv=2, head_dim=hd, page_len=64,
+                  window=window, ring_pages=4, seqs=seqs)
+    check(gpu, O, c, 1)
+
+
 def prep_case(O, seed, hd, rope_half, ps, nq, nkv, seqs, page, degree=1, rank=0,
               k_eq_v=False):
     rng = np.random.default_rng(seed)
