@@ -216,7 +216,9 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
   const int per_tok = a.num_kv * a.s_max;
   const int item = blockIdx.x * 4 + wave;
   if (item >= a.T * per_tok) return;
-  const int tok = item / per_tok, rem = item % per_tok;
+  // later buffer rows first: in a prefill chunk they have the longest KV
+  // ranges, so the long waves start early and the short ones fill the tail
+  const int tok = a.T - 1 - item / per_tok, rem = item % per_tok;
   const int kvh = rem / a.s_max, s = rem % a.s_max;
   const TokRange tr = token_range(a, tok);
   const int S = num_splits(tr.L, a.s_max);
@@ -460,7 +462,9 @@ __global__ __launch_bounds__(256) void k_flash_attn_mt(AttnArgs a) {
   const int nblk = (a.T + 16 * TPW - 1) / (16 * TPW);
   const int item = blockIdx.x * 4 + wave;
   if (item >= nblk * a.num_kv * 16) return;
-  const int cls = item % 16, kvh = (item / 16) % a.num_kv, blk = item / (16 * a.num_kv);
+  // later token blocks first (the longest KV ranges of a prefill chunk)
+  const int cls = item % 16, kvh = (item / 16) % a.num_kv;
+  const int blk = nblk - 1 - item / (16 * a.num_kv);
   const int tok0 = blk * 16 * TPW + cls;
   const int64_t kvs = (int64_t)a.num_kv * HD;
   const int p16 = lane & 15, grp = lane >> 4;
