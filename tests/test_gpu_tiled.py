@@ -36,6 +36,26 @@ def test_dense_tiles(gpu, O, monkeypatch, bm, bn, M, K, B):
     np.testing.assert_array_equal(host(ob), rb)
 
 
+@pytest.mark.parametrize("M,K,N", [(200, 512, 384), (77, 2816, 384), (512, 4096, 4096),
+                                   (64, 128, 256), (130, 704, 256), (33, 192, 128)])
+def test_dense_split_k(gpu, O, monkeypatch, M, K, N):
+    # per-row 64 x 128 tiles with two K groups per workgroup (odd, even and
+    # single-stage K: the groups get equal stage counts, one more, or none)
+    monkeypatch.setenv("BQ_TILE_BM", "64")
+    monkeypatch.setenv("BQ_TILE_BN", "128")
+    monkeypatch.setenv("BQ_TILE_KSP", "2")
+    wf = O.bf16_to_f32(O.synth_normal_bf16(3, 0.02, (N, K)))
+    q, s = O.rotate_and_quant(wf, 64)
+    W = gpu.ButterquantWeight(gpu.retile(dev(q.reshape(-1)), N, K), dev(s), N, K)
+    x = O.synth_normal_bf16(4, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 64)
+    ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+    p, cs = O.pack_and_colsum(q)
+    rb, rf = O.linear(xq, sa, p, s, cs, N)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
 def test_dense_qkv_tiled(gpu, O):
     K, M = 512, 100
     Ws, qs = [], []
