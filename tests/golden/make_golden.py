@@ -85,6 +85,62 @@ def make():
              moe_gq=gq, moe_gs=gs, moe_dq=dq, moe_ds=ds, moe_x=xm, moe_xq=mxq, moe_xsa=mxs,
              moe_bucket=bucket, moe_bucket_i8=bkq, moe_bucket_sa=bks, moe_accum=acc,
              moe_out=out)
+
+    # router: logits (T=3, E=8, H=256) and top-2 softmax with a per-expert scale
+    rx = O.synth_normal_bf16(9, 1.0, (3, 256))
+    rproj = O.synth_normal_bf16(10, 0.05, (8, 256))
+    rsc = O.f32_to_bf16(np.linspace(0.5, 1.5, 256).astype(np.float32))
+    rlog = O.router_logits(rx, rproj, rsc)
+    pes = O.f32_to_bf16(np.linspace(0.75, 1.25, 8).astype(np.float32))
+    ridx, rwt = O.route_topk_softmax(rlog, 2, pes)
+    g.update(router_x=rx, router_proj=rproj, router_scale=rsc, router_logits=rlog,
+             router_pes=pes, router_idx=ridx, router_w=rwt)
+
+    # vocabulary head: V=160, H=256, B=128, two rows (one greedy), and the
+    # embedding rows of the same table
+    rng = np.random.default_rng(11)
+    hw = rng.integers(-127, 128, (160, 256), dtype=np.int8)
+    hws = (rng.random((160, 2)) / 127 / 30).astype(np.float32)
+    hx = O.synth_normal_bf16(12, 1.0, (2, 256))
+    hxq, hxs = O.norm_quant(hx, np.full(256, ONE, np.uint16), 128, per_block=True)
+    hp = O.sampling_params(2, temperature=[0.8, 1.0], top_k=[20, 0], seed=[7, 8], n_keep=[16, 4],
+                           greedy=[False, True])
+    hout = O.flash_sample(hxq, hxs, hw, hws, hp)
+    etok = np.array([0, 159, 42, 42], np.int32)
+    emb = O.embed_lookup(etok, hw, hws, 128, scale=O.embed_scale(2816))
+    g.update(head_w=hw, head_ws=hws, head_xq=hxq, head_xsa=hxs,
+             head_params=np.frombuffer(hp.tobytes(), np.uint8),
+             head_outcome=np.frombuffer(hout.tobytes(), np.uint8), embed_tokens=etok, embed_out=emb)
+
+    # int8-KV attention: prep of 5 tokens (two runs) into a 6-page cache of
+    # 16 rows (head_dim 128, 4 q / 2 kv heads, RoPE on 64 of 64 pairs), then
+    # sliding (window 20) and full attention with one and two splits
+    nq, nkv, hd, page = 4, 2, 128, 16
+    ax = lambda seed, n: O.synth_normal_bf16(seed, 1.0, (5, n))
+    aq, ak, av = ax(13, nq * hd), ax(14, nkv * hd), ax(15, nkv * hd)
+    qn = O.f32_to_bf16(np.linspace(0.5, 1.5, hd).astype(np.float32))
+    kn = O.f32_to_bf16(np.linspace(1.5, 0.5, hd).astype(np.float32))
+    ang = np.arange(64)[:, None] * (1.0 / 10000.0 ** (np.arange(64) / 64.0))[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    runs = O.kv_runs([(0, 14, 0, 2), (3, 7, 2, 1)])  # positions 14-16 and 7-8: pages 0, 1
+    rows = np.array([2 * page, 5 * page, 0], np.int32)
+    crng = np.random.default_rng(16)
+    kc = crng.integers(-127, 128, (6 * page, nkv * hd), dtype=np.int8)
+    vc = crng.integers(-127, 128, (6 * page, nkv * hd), dtype=np.int8)
+    ks = crng.uniform(1, 6, (6 * page, nkv)).astype(np.float32)
+    vs = crng.uniform(0.5, 3, (6 * page, nkv)).astype(np.float32)
+    g.update(attn_q=aq, attn_k=ak, attn_v=av, attn_qn=qn, attn_kn=kn, attn_cos=cos,
+             attn_sin=sin, attn_runs=np.frombuffer(runs.tobytes(), np.int32).reshape(-1, 4),
+             attn_rows=rows, attn_kc_in=kc.copy(), attn_vc_in=vc.copy(), attn_ks_in=ks.copy(),
+             attn_vs_in=vs.copy())
+    qi, qb, fq = O.attn_prep(aq, ak, av, qn, kn, kc, ks, vc, vs, cos, sin, runs, rows, nq, nkv,
+                             hd, 64, 64, 4, page - 1, -1)
+    g.update(attn_qi=qi, attn_qb=qb, attn_fq=fq, attn_kc=kc, attn_ks=ks, attn_vc=vc, attn_vs=vs)
+    for name, window, pm in (("sliding", 20, 1), ("full", 0, -1)):
+        for s_max in (1, 2):
+            g[f"attn_out_{name}_s{s_max}"] = O.flash_attention(
+                qi, qb, fq, kc, ks, vc, vs, runs, rows, nq, nkv, hd, window, 4, page - 1, pm,
+                s_max=s_max, min_split=32)
     return g
 
 
