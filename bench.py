@@ -631,6 +631,17 @@ def main():
                 "int8_tops": round(m["ops"] / (m["ms"] * 1e-3) / 1e12, 1)}
     if "layer16" in res:
         line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()}
+        if "attn" in res:
+            # the same stack with each layer's attention step (prep + int8-KV
+            # attention at decode batch 16: sliding layers at a full 1024
+            # window, full layers at 4096 positions)
+            a = res["attn"]
+            sl = (a["sliding_decode_b16"]["us"] + a["sliding_decode_b16"]["prep_us"]) * 1e-3
+            fl = (a["full_decode_b16_ctx4096"]["us"] + a["full_decode_b16_ctx4096"]["prep_us"]) * 1e-3
+            l16 = res["layer16"]
+            stack = 25 * (l16["sliding_layer_ms"] + sl) + 5 * (l16["full_layer_ms"] + fl)
+            line["decoder_layer_b16"]["stack_with_attention_ms"] = round(stack, 4)
+            line["decoder_layer_b16"]["stack_with_attention_tokens_per_s"] = round(16 / (stack * 1e-3), 1)
     if "load" in res:
         ld = res["load"]
         line["load_safetensors_gate_up_507MB"] = {"ms": round(ld["ms"], 2),
