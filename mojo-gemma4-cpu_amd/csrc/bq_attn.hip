@@ -24,10 +24,13 @@
 // acc += (w * vs / 127) * v position by position, each lane owning head_dim/64
 // consecutive output columns of every head.  A token whose range is one split
 // of a sliding layer is finalized in the wave (acc * (1/l), the sliding
-// prefill kernel); every other token's splits are written as (m, l, acc)
-// partials and merged by k_attn_merge in split order with the reference's
-// merge (corrections masked by l > 0, a 16-lane tree per batch of 16 splits,
-// the first contributing split multiplied, the rest fma-accumulated).
+// prefill kernel), and so is every token of a one-split plan (full layers:
+// the merge of one split); every other token's splits are written as
+// (m, l, acc) partials and merged by k_attn_merge / k_attn_merge_lds in split
+// order with the reference's merge (corrections masked by l > 0, a 16-lane
+// tree per batch of 16 splits, the first contributing split multiplied, the
+// rest fma-accumulated).  One-split plans with head_dim <= 256 run
+// k_flash_attn_mt instead: 16/G tokens per wave on a shared tile grid.
 #include "bq_kernels.hpp"
 #include "bq_device.hpp"
 
