@@ -434,6 +434,242 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// Down projection with the weights streamed through registers (K = inter, at
+// most 64 * KMAX; per-block scales with block 64).  Persistent: one
+// workgroup per CU walks a contiguous range of (m-tile, n-tile) items, m-tile
+// major, so consecutive items mostly share their m-tile.
+//
+// Activations: the m-tile's whole block -- BM records x K bytes in the A
+// layout of k_tiled, one 128-byte stage after another -- is DMA'd into LDS
+// when the item's m-tile changes, with its per-block scales and route
+// weights.  Weights: each of the 8 waves owns NI 16-column strips of the
+// item's n-tile and holds all K of them in VGPRs; as soon as a k-step's
+// fragments have been multiplied they are reloaded with the next item's, so
+// the weight stream runs without a break and the bytes in flight per CU are
+// bounded by the register file (8 waves x NI x K/64 KiB), not by LDS.
+//
+// Every k-step is one drain block: its int32 product (an MFMA from zero) is
+// added to the f32 accumulator as fmaf(f32(dot), a_scale/127, acc), k-steps
+// in ascending order -- the per-block order of k_tiled's DOWN mode.
+constexpr int kBregMaxExperts = 256;
+
+template <int MI, int NI, int KMAX>
+__global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
+  constexpr int NW = 8, BM = 16 * MI, BN = NW * NI * 16, FA = BM / 8;
+  constexpr int SPT = (BM * KMAX + 64 * NW - 1) / (64 * NW);  // scales per thread
+  static_assert(MI % 2 == 0 && BM <= 64 * NW, "m-subtile pairs; one route weight per thread");
+  __shared__ __attribute__((aligned(16))) int8_t abuf[(KMAX + 1) / 2 * FA * 1024];
+  __shared__ __attribute__((aligned(16))) float sa[KMAX * BM];  // [k-step][record] x 1/127
+  __shared__ float s_rw[BM];                                     // route weights
+  __shared__ int s_tp[kBregMaxExperts + 1];  // m-tiles before each expert (exclusive prefix)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const v4i zero = {0, 0, 0, 0};
+  const int E = args.E, K = args.K, K64 = K >> 6, nstages = (K64 + 1) / 2, N = args.N;
+  const bool odd = K64 & 1;
+
+  // ---- m-tile table: as find_mtile enumerates them ------------------------
+  if (wave == 0) {
+    int carry = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int ex = base + lane;
+      const int tiles = ex < E ? max(0, (args.eo[ex + 1] - args.eo[ex] + BM - 1) / BM) : 0;
+      int inc = tiles;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += y;
+      }
+      if (ex < E) s_tp[ex] = carry + inc - tiles;
+      carry += __shfl(inc, 63, kWave);
+    }
+    if (lane == 0) s_tp[E] = carry;
+  }
+  lds_barrier();
+  const long items = (long)s_tp[E] * args.gn;
+  const int first = (int)(items * blockIdx.x / gridDim.x);
+  const int last = (int)(items * (blockIdx.x + 1) / gridDim.x);
+  if (first >= last) return;
+
+  // item -> expert (the last e with s_tp[e] <= mt), n-strip base
+  auto expert_of = [&](int mt) {
+    int lo = 0, hi = E;  // s_tp[lo] <= mt < s_tp[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_tp[mid] <= mt) lo = mid; else hi = mid;
+    }
+    return __builtin_amdgcn_readfirstlane(lo);
+  };
+  auto strips = [&](int item, const int8_t*& wb, int& ns0) {
+    const int mt = item / args.gn, nt = item - mt * args.gn;
+    wb = args.w + (size_t)expert_of(mt) * N * K;
+    ns0 = nt * (BN / 16) + wave * NI;
+  };
+  // a uniform (scalar) strip base plus one 32-bit lane offset per load
+  const uint32_t lane16 = (uint32_t)lane * 16u;
+  auto load_strip = [&](const int8_t* wb, int ns0, int j, int ks) {
+    const int ns = (ns0 + j) * 16 < N ? ns0 + j : 0;  // strips past N are never stored
+    const uint64_t ob = (uint64_t)(wb - args.w) + ((uint64_t)ns * K64 + min(ks, K64 - 1)) * 1024u;
+    const uint64_t ou = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ob >> 32)) << 32) |
+                        __builtin_amdgcn_readfirstlane((uint32_t)ob);
+    return *reinterpret_cast<const v4i*>(args.w + ou + lane16);
+  };
+
+  // ---- the first item's weights ------------------------------------------
+  v4i bw[KMAX][NI];
+  {
+    const int8_t* wb;
+    int ns0;
+    strips(first, wb, ns0);
+#pragma unroll
+    for (int ks = 0; ks < KMAX; ++ks)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb, ns0, j, ks);
+  }
+
+  // per-column weight scales of an item's strips
+  auto load_ep = [&](int item, float (&ep)[NI]) {
+    const int mt = item / args.gn, nt = item - mt * args.gn;
+    const int e = expert_of(mt), ns0 = nt * (BN / 16) + wave * NI;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      ep[j] = args.ws[(size_t)e * N + min((ns0 + j) * 16 + (lane & 15), N - 1)];
+  };
+  float ep_col[NI];
+  load_ep(first, ep_col);
+
+  int cur_mt = -1, r0 = 0, r1 = 0, nmi = 0;
+  const uint32_t a_lds = lds_addr(abuf);
+  for (int item = first; item < last; ++item) {
+    const int mt = item / args.gn, nt = item - mt * args.gn;
+    const int e = expert_of(mt);
+    const int ns0 = nt * (BN / 16) + wave * NI;
+    if (mt != cur_mt) {
+      // ---- a new m-tile: its activations, scales and route weights -------
+      cur_mt = mt;
+      r0 = args.eo[e] + (mt - s_tp[e]) * BM;
+      r1 = min(min(args.eo[e + 1], r0 + BM), args.max_routes);
+      r0 = __builtin_amdgcn_readfirstlane(r0);
+      r1 = __builtin_amdgcn_readfirstlane(r1);
+      if (r1 <= r0) continue;  // past max_routes: nothing to store (uniform)
+      nmi = (r1 - r0 + 15) >> 4;
+      lds_barrier();  // every wave is done with the previous m-tile's LDS
+      for (int q = wave; q < nstages * FA; q += NW) {
+        const int st = q / FA, f = q % FA;
+        const int r = lane >> 3, c = (lane & 7) ^ r ^ (f & 1);
+        int row = r0 + f * 8 + r;
+        if (row >= r1) row = r0;  // rows past the tile end are never stored
+        // a one-step tail stage reads its second half from the first (never used)
+        const int back = (odd && st == nstages - 1 && c >= 4) ? 64 : 0;
+        const int8_t* g = args.a + (size_t)row * K + st * 128 + c * 16 - back;
+        const uint32_t l = __builtin_amdgcn_readfirstlane(a_lds + (uint32_t)q * 1024u);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                     :: "s"(l), "v"(g) : "memory", "m0");
+#pragma clang diagnostic pop
+      }
+      // scales and route weights, loaded unmasked (clamped indices) after
+      // the DMAs: waiting for the first of them also retires this wave's
+      // DMAs, which return in issue order before it
+      const int nsc = BM * K64;
+      float sv[SPT];
+#pragma unroll
+      for (int i = 0; i < SPT; ++i) {
+        const int idx = min(tid + 64 * NW * i, nsc - 1);
+        const int m = idx / K64, b = idx - m * K64;
+        sv[i] = args.a_scale[(size_t)min(r0 + m, r1 - 1) * K64 + b];
+      }
+      const float rwv = args.routes[min(r0 + tid, r1 - 1)].weight;
+#pragma unroll
+      for (int i = 0; i < SPT; ++i) {
+        const int idx = tid + 64 * NW * i;
+        if (idx < nsc) {
+          const int m = idx / K64, b = idx - m * K64;
+          sa[b * BM + m] = r0 + m < r1 ? sv[i] * kInv127 : 0.0f;
+        }
+      }
+      if (tid < BM) s_rw[tid] = rwv;
+      asm volatile("" :: "v"(sv[0]));  // the first scale (and so every DMA) has landed
+      lds_barrier();
+    }
+    // the next item's strips (the last item reloads its own: never used)
+    const int8_t* wb_n;
+    int ns0_n;
+    strips(item + 1 < last ? item + 1 : item, wb_n, ns0_n);
+
+    // ---- multiply: k-steps in order, m-subtiles in pairs ------------------
+    float facc[MI][NI][4];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) facc[mi][j][v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KMAX; ++ks) {
+      const int st = ks >> 1, c = (ks & 1) * 4 + (lane >> 4);
+#pragma unroll
+      for (int mp = 0; mp < MI; mp += 2) {
+        // a pair past the tile's last record is skipped; the odd one out of
+        // a partial pair multiplies rows whose scales are 0
+        if (ks < K64 && mp < nmi) {  // wave-uniform
+          v4i a[2];
+          float4 adv[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int m = (mp + h) * 16 + (lane & 15), bb = m >> 3, r = m & 7;
+            a[h] = *reinterpret_cast<const v4i*>(
+                &abuf[(st * FA + bb) * 1024 + r * 128 + ((c ^ r ^ (bb & 1)) * 16)]);
+            adv[h] = *reinterpret_cast<const float4*>(
+                &sa[ks * BM + (mp + h) * 16 + 4 * (lane >> 4)]);
+          }
+          v4i t[2][NI];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) t[h][j] = mfma16x16x64(a[h], bw[ks][j], zero);
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+              float* f = facc[mp + h][j];
+              f[0] = fmaf((float)t[h][j][0], adv[h].x, f[0]);
+              f[1] = fmaf((float)t[h][j][1], adv[h].y, f[1]);
+              f[2] = fmaf((float)t[h][j][2], adv[h].z, f[2]);
+              f[3] = fmaf((float)t[h][j][3], adv[h].w, f[3]);
+            }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb_n, ns0_n, j, ks);
+    }
+
+    // ---- epilogue: y[rec, n] = (facc * ws[n]) * route_w -------------------
+    // (the column scales are waited for once here, not before every store:
+    // a wait inside the guarded stores would also wait for the stores)
+    asm volatile("" :: "v"(ep_col[0]), "v"(ep_col[NI - 1]));
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = r0 + mi * 16 + 4 * (lane >> 4) + v;
+        if (mi < nmi && row < r1) {
+          const float rw = s_rw[row - r0];
+#pragma unroll
+          for (int j = 0; j < NI; ++j) {
+            const int col = (ns0 + j) * 16 + (lane & 15);
+            if (col < N) args.y[(size_t)row * N + col] = facc[mi][j][v] * ep_col[j] * rw;
+          }
+        }
+      }
+    }
+    if (item + 1 < last) load_ep(item + 1, ep_col);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tile configuration: BM x BN output tile, NBUF-stage LDS ring.  Smaller
 // rings leave room for several workgroups per CU (more waves to overlap the
 // LDS-read -> MFMA -> barrier chain of each); overrides BQ_TILE_BN and
@@ -573,6 +809,20 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
   t.a = b_i8; t.a_scale = b_sa; t.eo = eo; t.routes = routes; t.w = w_d; t.ws = d_scale; t.y = y;
   t.E = experts; t.max_routes = max_routes; t.N = hidden; t.K = inter; t.inter = inter;
   t.block = block;
+  // block-64 scales and K up to 704 (the model's inter): weights in registers,
+  // 192-record m-tiles x 256 columns
+  if (block == 64 && inter % 64 == 0 && inter / 64 <= 11 && experts <= kBregMaxExperts &&
+      env_int("BQ_DOWN_BREG", 1)) {
+    constexpr int MI = 12, NI = 2;
+    t.gn = (hidden + 8 * NI * 16 - 1) / (8 * NI * 16);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    hipLaunchKernelGGL((k_down_breg<MI, NI, 11>), dim3(cus), dim3(512), 0, st, t);
+    return hipGetLastError();
+  }
   // the down projection's K (= inter) is short, and its per-block drains
   // keep f32 accumulators: 64-record tiles with a double-buffered stage run
   // fastest (more workgroups in flight per CU)

@@ -134,3 +134,46 @@ def test_moe_gate_up_hidden2816(gpu, O, T):
     gp, gcs = O.pack_and_colsum(gq)
     rb = O.moe_phase1(xq, xsa, reo, rroutes, gp, gs, gcs, I)
     np.testing.assert_array_equal(host(bucket), rb)
+
+
+@pytest.mark.parametrize("T,breg", [(64, "0"), (300, "0"), (600, "0"), (33, "1"), (300, "1")])
+def test_moe_down_paths(gpu, O, monkeypatch, T, breg):
+    # the down projection with weights in registers (default for block 64 and
+    # inter <= 704) and the LDS-ring k_tiled path it replaces
+    monkeypatch.setenv("BQ_DOWN_BREG", breg)
+    c = _tiny_moe(O, gpu, T)
+    E, H, I, k = c["E"], c["H"], c["I"], c["k"]
+    eo, routes = gpu.build_schedule(dev(c["idx"]), dev(c["w"]), E)
+    reo, rroutes = O.build_schedule(c["idx"], c["w"], E)
+    gp, gcs = O.pack_and_colsum(c["gq"])
+    rb = O.moe_phase1(c["xq"], c["xsa"], reo, rroutes, gp, c["gs"], gcs, I)
+    rbq, rbsa = O.block_quant(rb, 64, True)
+    accum, out = gpu.moe_phase2(dev(rbq), dev(rbsa), eo, routes, c["Wd"], E, T, k, H)
+    dp, dcs = O.pack_and_colsum(c["dq"], 64, False)
+    racc, rout = O.moe_phase2(rbq, rbsa, reo, rroutes, T, dp, c["ds"], dcs, H)
+    np.testing.assert_array_equal(host(accum), racc)
+    np.testing.assert_array_equal(host(out), rout)
+
+
+@pytest.mark.parametrize("T", [450, 200, 130])
+def test_moe_down_hidden2816(gpu, O, T):
+    # model shapes (hidden 2816 = 11 column tiles of 256, inter 704 = 11
+    # k-steps): T = 450 gives ~225 records per expert (a full and a partial
+    # 192-record m-tile), T = 200 one partial m-tile, T = 130 ~65 records
+    E, k, H, I = 4, 2, 2816, 704
+    rng = np.random.default_rng(T)
+    logits = O.synth_normal_f32(31, 1.0, (T, E))
+    idx, w = O.route_topk_softmax(logits, k)
+    dn = O.bf16_to_f32(O.synth_normal_bf16(32, 0.02, (E * H, I)))
+    dq, ds = O.rotate_and_quant(dn, 64)
+    Wd = gpu.ButterquantWeight(gpu.retile(dev(dq.reshape(-1)), E * H, I), dev(ds), E * H, I)
+    bucket = O.f32_to_bf16(rng.standard_normal((T * k, I)).astype(np.float32))
+    bq, bsa = O.block_quant(bucket, 64, True)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    print(f"moe down H={H} I={I} T={T}", flush=True)
+    accum, out = gpu.moe_phase2(dev(bq), dev(bsa), eo, routes, Wd, E, T, k, H)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    dp, dcs = O.pack_and_colsum(dq, 64, False)
+    racc, rout = O.moe_phase2(bq, bsa, reo, rroutes, T, dp, ds, dcs, H)
+    np.testing.assert_array_equal(host(accum), racc)
+    np.testing.assert_array_equal(host(out), rout)
