@@ -57,6 +57,17 @@ __device__ inline void wait_dma(int later) {
   }
 }
 
+// The same, for a wave that issues n (0..DMAX) DMAs per stage.
+template <int DMAX, int NBUF>
+__device__ inline void wait_dma_n(int later, int n) {
+  if constexpr (DMAX > 0) {
+    if (n == DMAX) { wait_dma<DMAX, NBUF>(later); return; }
+    wait_dma_n<DMAX - 1, NBUF>(later, n);
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
 // 32-bit LDS address of a __shared__ object (what M0 takes for LDS DMA)
 __device__ inline uint32_t lds_addr(const int8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
@@ -166,9 +177,16 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
   const int8_t* src[D];
   int dst_off[D];
   bool is_a[D], hi[D];  // hi: reads the second k-step of the stage
+  // A DMAs whose 8 rows all lie past the tile's last record are not issued
+  // (their LDS rows feed only outputs that are never stored)
+  bool skip[D];
+  const int live_rows = __builtin_amdgcn_readfirstlane(r1 - r0);
+  int n_issue = full_d ? D : D - 1;  // DMAs this wave issues per stage
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int f = min(wave + NW * d, FA + FB - 1);  // the clamped slot is never issued
+    skip[d] = f < FA && f * 8 >= live_rows;
+    if (skip[d] && (d < D - 1 || full_d)) --n_issue;
     if (f < FA) {
       const int r = lane >> 3, c = (lane & 7) ^ r ^ (f & 1);  // this lane's row, chunk
       int row = r0 + f * 8 + r;
@@ -221,6 +239,7 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       if (d == D - 1 && !full_d) break;
+      if (skip[d]) continue;
       // stage st starts at K byte 128*st (A) / fragment 2*st (B); in a
       // one-step tail stage the second-half reads fall back to the first half
       const int back = (odd && st == tail && hi[d]) ? (is_a[d] ? 64 : 1024) : 0;
@@ -363,8 +382,7 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
       const int sl = s0 + i;
       if (sl >= n_iter) break;
       const int later = max(0, min(NBUF - 2, n_loc - 1 - sl));
-      if (full_d) wait_dma<D, NBUF>(later);
-      else wait_dma<D - 1, NBUF>(later);
+      wait_dma_n<D, NBUF>(later, n_issue);
       lds_barrier();
       if (sl + NBUF - 1 < n_loc)
         issue(abuf_[(i + NBUF - 1) % NBUF], bbuf_[(i + NBUF - 1) % NBUF], s_lo + sl + NBUF - 1);
