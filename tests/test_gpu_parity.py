@@ -124,11 +124,13 @@ def test_norm_quant(gpu, O, H, B):
     np.testing.assert_array_equal(host(q), rq)
 
 
+@pytest.mark.parametrize("T", [259, 1795])
 @pytest.mark.parametrize("H,B", [(2816, 128), (4096, 128), (2112, 64), (512, 16), (4096, 512),
                                  (1024, 32), (768, 256), (1536, 512)])
-def test_norm_quant_long(gpu, O, H, B):
-    # seq_len >= 256 takes the one-wave-per-token kernel; 259 leaves a partial workgroup
-    x = O.synth_normal_bf16(11, 1.0, (259, H))
+def test_norm_quant_long(gpu, O, H, B, T):
+    # seq_len >= 1792 takes the one-wave-per-token kernel (1795 leaves a
+    # partial workgroup); 259 runs the workgroup-per-row kernel on many rows
+    x = O.synth_normal_bf16(11, 1.0, (T, H))
     g = O.f32_to_bf16(O.synth_normal_f32(12, 0.3, (H,)) + 1.0)
     q, sa = gpu.norm_quant(dev(x), dev(g), B)
     rq, rsa = O.norm_quant(x, g, B)
