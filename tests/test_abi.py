@@ -132,6 +132,19 @@ def test_empty_batches_are_noops(L):
                                 704, 64, None, 0, None) == 0
     assert L.bq_full_attention(*([None] * 9), 0, None, 1, None, 16, 2, 512, 10, 1023, -1, 1, 0,
                                None) == 0
+    assert L.bq_sliding_attention(*([None] * 9), 0, None, 1, None, 16, 8, 256, 1024, 10, 1023, 1,
+                                  1, 0, None) == 0
+    assert L.bq_qkv(*([None] * 11), 256, 128, 0, 2816, None) == 0
+    assert L.bq_moe_build_schedule(None, None, 0, 8, 0, 128, None, None, None) == 0
+    assert L.bq_moe_phase1_gate_up(*([None] * 7), 128, 0, 8, 2816, 704, None) == 0
+    assert L.bq_head_prep(None, None, None, None, 0, 2816, 128, C.c_float(1), C.c_float(1),
+                          None) == 0
+    assert L.bq_flash_sample(*([None] * 6), 0, 262144, 2816, 128, C.c_float(30), 0, None, 0,
+                             None) == 0
+    assert L.bq_embed_lookup(None, None, None, None, 0, 2816, 128, 262144, 0, C.c_float(1),
+                             None) == 0
+    assert L.bq_attn_prep(*([None] * 15), 1, None, 16, 8, 256, 128, 128, C.c_float(16),
+                          C.c_float(1), 1, 0, 10, 1023, 1, 0, None) == 0
 
 
 def test_workspace_size(L):
