@@ -160,15 +160,15 @@ __global__ __launch_bounds__(1024) void k_norm_quant_reg(
       v[q][i] = val;
     }
   }
-  for (int st = 1; st < block && st < kWave; st <<= 1) {
-    const XlaneStage x(st);
+  for_each_xlane_stride(block, [&](auto st) {
+    constexpr int ST = decltype(st)::value;
 #pragma unroll
     for (int q = 0; q < MAXSEG; ++q) {
       if (wave + q * nw >= nseg) continue;
 #pragma unroll
-      for (int i = 0; i < R; ++i) v[q][i] = x(v[q][i]);
+      for (int i = 0; i < R; ++i) v[q][i] = xlane_bfly<ST>(v[q][i]);
     }
-  }
+  });
 #pragma unroll
   for (int rs = 1; rs < R; rs <<= 1) {
     if (rs * kWave >= block) break;
@@ -279,13 +279,13 @@ __global__ __launch_bounds__(256) void k_norm_quant_wave(
       const float val = xv * inv_rms * g;
       v[q][r] = q < nseg ? val : 0.0f;
     }
-  for (int st = 1; st < block && st < kWave; st <<= 1) {
-    const XlaneStage x(st);
+  for_each_xlane_stride(block, [&](auto st) {
+    constexpr int ST = decltype(st)::value;
 #pragma unroll
     for (int q = 0; q < NSEG; ++q)
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[q][r] = x(v[q][r]);
-  }
+      for (int r = 0; r < R; ++r) v[q][r] = xlane_bfly<ST>(v[q][r]);
+  });
 #pragma unroll
   for (int rs = 1; rs < R; rs <<= 1) {
     if (rs * kWave >= block) continue;
@@ -371,20 +371,18 @@ __global__ __launch_bounds__(256) void k_block_quant(
         v[j] = a + b;
         v[j + s] = a - b;
       }
+    for_each_xlane_stride(LPB, [&](auto st) {
+      constexpr int ST = decltype(st)::value;
 #pragma unroll
-    for (int s = 1; s < LPB; s <<= 1) {
-      const XlaneStage x(s);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = x(v[j]);
-    }
+      for (int j = 0; j < 8; ++j) v[j] = xlane_bfly<ST>(v[j]);
+    });
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = v[j] * fwht_scale;
   }
   float m = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
-#pragma unroll
-  for (int s = 1; s < LPB; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, kWave));
+  for_each_xlane_stride(LPB, [&](auto st) { m = fmaxf(m, xlane_partner<decltype(st)::value>(m)); });
   const float inv = m > 0.0f ? 127.0f / m : 0.0f;
   uint32_t w[2] = {0u, 0u};
 #pragma unroll

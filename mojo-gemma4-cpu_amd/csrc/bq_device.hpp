@@ -199,23 +199,53 @@ __device__ inline float group_max(float v, int width) {
   return v;
 }
 
-// One element of a cross-lane FWHT stage of stride st: the lane with bit st
+// The value that lane (lane ^ ST) of the wave holds.  Strides 1 and 2 are one
+// DPP quad permutation, stride 8 one DPP row rotation by 8 (within a row of
+// 16 lanes that is lane ^ 8), stride 4 two DPP row shifts (lane + 4 for
+// lanes with bit 2 clear, lane - 4 otherwise) and a select; strides 16 and
+// 32 cross rows and go through ds_bpermute.
+template <int ST>
+__device__ inline float xlane_partner(float v) {
+  static_assert(ST >= 1 && ST <= 32 && (ST & (ST - 1)) == 0, "stride");
+  const int x = __float_as_int(v);
+  if constexpr (ST == 1) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  } else if constexpr (ST == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  } else if constexpr (ST == 4) {
+    const int up = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0xF, false);  // row_shl:4
+    const int dn = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    return __int_as_float((threadIdx.x & 4) ? dn : up);
+  } else if constexpr (ST == 8) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false));  // row_ror:8
+  } else {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(((int)(threadIdx.x & 63) ^ ST) << 2, x));
+  }
+}
+
+// One element of a cross-lane FWHT stage of stride ST: the lane with bit ST
 // clear holds a and gets a + b, its partner holds b and gets a - b.  Computed
 // as fmaf(s, v, p) with s = +1 / -1 and p the partner's value: s*v is exact,
 // so the one rounding gives exactly v + p (= a + b) or p - v (= a - b).
-struct XlaneStage {
-  int addr;  // byte address of the partner lane for ds_bpermute
-  float s;
-  __device__ explicit XlaneStage(int st) {
-    const int lane = (int)(threadIdx.x & 63);
-    addr = (lane ^ st) << 2;
-    s = (lane & st) ? -1.0f : 1.0f;
-  }
-  __device__ float operator()(float v) const {
-    const float p = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v)));
-    return fmaf(s, v, p);
-  }
-};
+template <int ST>
+__device__ inline float xlane_bfly(float v) {
+  return fmaf((threadIdx.x & ST) ? -1.0f : 1.0f, v, xlane_partner<ST>(v));
+}
+
+template <int ST>
+struct Stride { static constexpr int value = ST; };
+
+// f(Stride<ST>{}) for the cross-lane strides ST = 1, 2, 4, ... below
+// min(block, 64), in that order.
+template <typename F>
+__device__ inline void for_each_xlane_stride(int block, F&& f) {
+  if (block > 1) f(Stride<1>{});
+  if (block > 2) f(Stride<2>{});
+  if (block > 4) f(Stride<4>{});
+  if (block > 8) f(Stride<8>{});
+  if (block > 16) f(Stride<16>{});
+  if (block > 32) f(Stride<32>{});
+}
 
 // In-wave FWHT of one segment of S = R*64 values (R = max(1, B/64)), value
 // index r*64 + lane.  For B < 64 the wave holds 64/B independent blocks (one
@@ -224,11 +254,11 @@ struct XlaneStage {
 // reference's stage loop, so the result is bit-identical to it.
 template <int R>
 __device__ inline void fwht_wave(float (&v)[R], int block) {
-  for (int s = 1; s < block && s < kWave; s <<= 1) {
-    const XlaneStage x(s);
+  for_each_xlane_stride(block, [&](auto st) {
+    constexpr int ST = decltype(st)::value;
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = x(v[r]);
-  }
+    for (int r = 0; r < R; ++r) v[r] = xlane_bfly<ST>(v[r]);
+  });
 #pragma unroll
   for (int rs = 1; rs < R; rs <<= 1) {
     if (rs * kWave >= block) break;
