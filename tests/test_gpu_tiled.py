@@ -155,11 +155,12 @@ def test_moe_down_paths(gpu, O, monkeypatch, T, breg):
     np.testing.assert_array_equal(host(out), rout)
 
 
-@pytest.mark.parametrize("T", [450, 200, 130])
+@pytest.mark.parametrize("T", [450, 200, 130, 20])
 def test_moe_down_hidden2816(gpu, O, T):
     # model shapes (hidden 2816 = 11 column tiles of 256, inter 704 = 11
     # k-steps): T = 450 gives ~225 records per expert (a full and a partial
-    # 192-record m-tile), T = 200 one partial m-tile, T = 130 ~65 records
+    # 192-record m-tile), T = 200 one partial m-tile, T = 130 ~65 records,
+    # T = 20 ~10 records (the skinny 16-record kernel)
     E, k, H, I = 4, 2, 2816, 704
     rng = np.random.default_rng(T)
     logits = O.synth_normal_f32(31, 1.0, (T, E))
