@@ -557,7 +557,7 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
   float ep_col[NI];
   load_ep(first, ep_col);
 
-  int cur_mt = -1, r0 = 0, r1 = 0, nmi = 0;
+  int cur_mt = -1, lds_mt = -1, r0 = 0, r1 = 0, nmi = 0;
   const uint32_t a_lds = lds_addr(abuf);
   for (int item = first; item < last; ++item) {
     const int mt = item / args.gn, nt = item - mt * args.gn;
@@ -570,8 +570,13 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
       r1 = min(min(args.eo[e + 1], r0 + BM), args.max_routes);
       r0 = __builtin_amdgcn_readfirstlane(r0);
       r1 = __builtin_amdgcn_readfirstlane(r1);
-      if (r1 <= r0) continue;  // past max_routes: nothing to store (uniform)
-      nmi = (r1 - r0 + 15) >> 4;
+      // An m-tile past max_routes (only an expert_offset beyond the route
+      // count makes one) multiplies and stores nothing, but its items still
+      // run the k-step loop: that is where the next item's weights load.
+      nmi = r1 > r0 ? (r1 - r0 + 15) >> 4 : 0;
+    }
+    if (lds_mt != mt && nmi > 0) {  // wave-uniform
+      lds_mt = mt;
       lds_barrier();  // every wave is done with the previous m-tile's LDS
       for (int q = wave; q < nstages * FA; q += NW) {
         const int st = q / FA, f = q % FA;
