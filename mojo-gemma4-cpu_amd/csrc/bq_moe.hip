@@ -113,6 +113,67 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
   }
 }
 
+// Decode-sized schedules (at most 1024 slots): one workgroup, one thread per
+// slot.  A slot's record is its expert's offset plus the number of earlier
+// slots routed to the same expert -- the (expert, token, k) order of
+// k_build_schedule -- so one load, an LDS histogram, one scan and one
+// scatter replace the per-expert passes over every slot.
+constexpr int kSchedSmallSlots = 1024;
+
+__global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
+    const int32_t* __restrict__ route_idx, const float* __restrict__ route_w, int slots,
+    int top_k, int ebase, int E, int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
+  __shared__ int s_e[kSchedSmallSlots];
+  __shared__ int s_cnt[kMaxExperts];
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int sc = min(tid, slots - 1);  // unmasked loads (slots >= 1)
+  const int x = route_idx[sc];
+  const float w = route_w[sc];
+  const int e = (tid < slots && x >= ebase && x < ebase + E) ? x - ebase : -1;
+  s_e[tid] = e;
+  for (int i = tid; i < E; i += kSchedSmallSlots) s_cnt[i] = 0;
+  __syncthreads();
+  int rank = 0;
+  if (e >= 0) {
+    atomicAdd(&s_cnt[e], 1);
+#pragma unroll 8
+    for (int i = 0; i < tid; ++i) rank += s_e[i] == e ? 1 : 0;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the E <= 256 counts, 4 per lane
+    int v[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane * 4 + j;
+      v[j] = ex < E ? s_cnt[ex] : 0;
+      sum += v[j];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += y;
+    }
+    int off = inc - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane * 4 + j;
+      if (ex < E) {
+        s_cnt[ex] = off;
+        expert_offset[ex] = off;
+      }
+      off += v[j];
+    }
+    if (lane == 63) expert_offset[E] = inc;
+  }
+  __syncthreads();
+  if (e >= 0) {
+    const int pos = s_cnt[e] + rank;
+    routes[pos].token = tid / top_k;
+    routes[pos].weight = w;
+  }
+}
+
 // Skinny (16-record m-tile) kernels for decode-sized batches.  Each wave owns
 // one 16-column output subtile and streams its weight rows in chunks of U
 // k-steps through two register slots: chunk c+1's loads are in flight while
@@ -366,6 +427,11 @@ hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w,
                                  Route* routes, hipStream_t st) {
   if (seq_len <= 0) return hipSuccess;
   if (experts > kMaxExperts) return hipErrorInvalidValue;
+  if (seq_len * top_k <= kSchedSmallSlots) {
+    hipLaunchKernelGGL(k_build_schedule_small, dim3(1), dim3(kSchedSmallSlots), 0, st, route_idx,
+                       route_w, seq_len * top_k, top_k, expert_base, experts, expert_offset, routes);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_build_schedule, dim3(experts), dim3(kSchedThreads), 0, st, route_idx,
                      route_w, seq_len * top_k, top_k, expert_base, experts, expert_offset, routes);
   return hipGetLastError();

@@ -269,8 +269,10 @@ def route_table(O, T, E=128, k=8, seed=2):
     return O.route_topk_softmax(logits, k)
 
 
-@pytest.mark.parametrize("T", [1, 32, 1500, 2048])
+@pytest.mark.parametrize("T", [1, 32, 128, 129, 1500, 2048])
 def test_build_schedule(gpu, O, T):
+    # up to 1024 slots (T * 8) one workgroup builds it; 129 tokens and more take
+    # the per-expert kernel
     idx, w = route_table(O, T)
     eo, routes = gpu.build_schedule(dev(idx), dev(w), 128)
     reo, rroutes = O.build_schedule(idx, w, 128)
