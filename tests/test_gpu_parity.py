@@ -177,6 +177,16 @@ def test_block_quant_blocks(gpu, O, B, fwht):
     np.testing.assert_array_equal(host(q), rq)
 
 
+@pytest.mark.parametrize("cols,B,fwht", [(704, 64, True), (2048, 256, False)])
+def test_block_quant_large(gpu, O, cols, B, fwht):
+    # 4001 rows (the 2048-token MoE bucket's scale): 1375+ workgroups, the last partial
+    x = O.synth_normal_bf16(5, 1.0, (4001, cols))
+    q, sa = gpu.block_quant(dev(x), B, fwht)
+    rq, rsa = O.block_quant(x, B, fwht)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(q), rq)
+
+
 def test_block_quant_golden(gpu, G):
     q, sa = gpu.block_quant(dev(G["bq_x"]), 64, True)
     np.testing.assert_array_equal(host(q), G["bq_codes"])
