@@ -15,9 +15,12 @@
  * When the host lacks AVX-512 VNNI the scalar oracle runs instead and
  * bqcpu_isa() reports "scalar".
  */
+#define _GNU_SOURCE
 #include <immintrin.h>
 #include <math.h>
 #include <omp.h>
+#include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -41,6 +44,52 @@ static void worker_range(int total, int workers, int w, int* s, int* e) {
 }
 
 static inline uint16_t f2bf(float v) { return bqo_f32_to_bf16(v); }
+
+/* Worker-count policies of the reference's dispatchers, `capacity` being the
+ * pool size (the thread count the caller gives):
+ *   recommended_workers (kernels/helpers.mojo:204-218) with the constants of
+ *   kernels/dispatch_heuristics.mojo:9-14 -- the default policy (norm-quant,
+ *   block-quant), matmul_workers (helpers.mojo:289-292: linears),
+ *   saturate_workers (:284-286: MoE phases) and merge_workers
+ *   (kernels/logsum_merge.mojo:199-202: the router merge);
+ *   fanout_dispatch runs inline (one worker) when data_bytes <= its
+ *   inline threshold (helpers.mojo:309-315). */
+static int recommended_workers(long bw_product, long amortized, long data_bytes, int capacity) {
+    if (capacity <= 1) return capacity;
+    if (data_bytes >= amortized) return capacity;
+    long target = data_bytes / bw_product;
+    int n = 1;
+    while ((long)(n + 1) * (n + 1) <= target && n < capacity) ++n;
+    return n;
+}
+static int default_workers(long data_bytes, int capacity) {
+    return recommended_workers(2280, 1L << 20, data_bytes, capacity);
+}
+static int matmul_workers(long data_bytes, int capacity) {
+    return recommended_workers(22528, 1L << 30, data_bytes, capacity);
+}
+static int merge_workers(long data_bytes, int capacity) {
+    if (data_bytes >= (1L << 20)) return capacity;
+    return capacity < 8 ? capacity : 8;
+}
+static int min_i(int a, int b) { return a < b ? a : b; }
+
+/* Pin the OpenMP team of n threads (the calling thread is thread 0), thread
+ * i to CPU cpus[i] -- the reference pins one worker per core of its NUMA
+ * rank (threading/topological_dispatch.mojo).  libgomp keeps the team's
+ * threads for later parallel regions of at most n threads.  0 on success. */
+int bqcpu_pin(const int* cpus, int n) {
+    int bad = 0;
+#pragma omp parallel num_threads(n) reduction(+ : bad)
+    {
+        cpu_set_t set;
+        CPU_ZERO(&set);
+        CPU_SET(cpus[omp_get_thread_num()], &set);
+        bad += pthread_setaffinity_np(pthread_self(), sizeof(set), &set) != 0;
+        bad += omp_get_num_threads() != n;
+    }
+    return bad ? -1 : 0;
+}
 
 /* One 32-row tile x PR rows: accumulate_tiles (gemm.mojo:36-75) over K range
  * [k_base, k_base+k_len) starting at packed byte offset packed_base. */
@@ -140,7 +189,7 @@ void bqcpu_linear(const int8_t* act, const float* sa, int m, const int8_t* wp,
     if (m <= 0) return;
     if (!have_vnni()) { bqo_gemm_i8_per_row(act, sa, m, wp, wsc, cs, N, K, out, NULL); return; }
     int tiles = N / 32;
-    int workers = nthreads < tiles ? nthreads : tiles;
+    int workers = min_i(matmul_workers((long)N * K * m, nthreads), tiles);
 #pragma omp parallel num_threads(workers)
     {
         int s, e;
@@ -156,7 +205,7 @@ void bqcpu_block_linear(const int8_t* act, const float* sa, int m, const int8_t*
     if (m <= 0) return;
     if (!have_vnni()) { bqo_gemm_i8_per_block(act, sa, m, wp, wsc, cs, N, K, block, out, NULL); return; }
     int tiles = N / 32;
-    int workers = nthreads < tiles ? nthreads : tiles;
+    int workers = min_i(matmul_workers((long)N * K * m, nthreads), tiles);
 #pragma omp parallel num_threads(workers)
     {
         int s, e;
@@ -165,11 +214,14 @@ void bqcpu_block_linear(const int8_t* act, const float* sa, int m, const int8_t*
     }
 }
 
-/* dispatch_bq_norm_quant (linear.mojo:58-82): tokens over workers */
+/* dispatch_bq_norm_quant (linear.mojo:58-82): tokens over workers, inline
+ * up to NORM_INLINE_TOKENS = 16 tokens */
 void bqcpu_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8,
                       float* sa, int m, int hidden, int block, float sqrt_n,
                       float n_eps, int nthreads) {
-#pragma omp parallel for num_threads(nthreads) schedule(static)
+    long bytes = (long)m * hidden * 6;
+    int workers = bytes <= 16L * hidden * 6 ? 1 : min_i(default_workers(bytes, nthreads), m);
+#pragma omp parallel for num_threads(workers) schedule(static)
     for (int t = 0; t < m; ++t)
         bqo_prepare_norm_activation(src + (size_t)t * hidden, gamma, x_i8 + (size_t)t * hidden,
                                     sa + t, hidden, block, sqrt_n, n_eps, 0);
@@ -179,7 +231,9 @@ void bqcpu_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8,
 void bqcpu_block_quant(const uint16_t* src, int8_t* x_i8, float* sa, int rows,
                        int cols, int block, int apply_fwht, int nthreads) {
     int nb = cols / block;
-#pragma omp parallel for num_threads(nthreads) schedule(static)
+    long bytes = (long)rows * cols * 6;
+    int workers = bytes <= 16L * cols * 6 ? 1 : min_i(default_workers(bytes, nthreads), rows);
+#pragma omp parallel for num_threads(workers) schedule(static)
     for (int t = 0; t < rows; ++t)
         bqo_prepare_block_activation(src + (size_t)t * cols, x_i8 + (size_t)t * cols,
                                      sa + (size_t)t * nb, cols, block, apply_fwht);
@@ -322,4 +376,43 @@ void bqcpu_moe_phase2(const int8_t* bi8, const float* bsa, int inter, int block,
         worker_range(tiles, workers, omp_get_thread_num(), &s, &e);
         phase2_tiles(bi8, bsa, inter, block, eo, routes, E, T, wd, dsc, dcs, hidden, accum, out, s, e);
     }
+}
+
+/* The router merge's top-k + softmax (kernels/moe_router.mojo:248-293) from
+ * logits, tokens over merge_workers. */
+void bqcpu_route_topk(const float* logits, int T, int E, int top_k, const uint16_t* pes,
+                      int32_t* route_idx, float* route_w, int nthreads) {
+    int workers = min_i(merge_workers((long)T * E * 4, nthreads), T);
+#pragma omp parallel num_threads(workers)
+    {
+        int s, e;
+        worker_range(T, workers, omp_get_thread_num(), &s, &e);
+        if (e > s)
+            bqo_route_topk_softmax(logits + (size_t)s * E, e - s, E, top_k, pes,
+                                   route_idx + (size_t)s * top_k, route_w + (size_t)s * top_k);
+    }
+}
+
+/* One MoE expert layer from router logits, in the model's order
+ * (modeling/gemma_4_moe_bq.mojo:666-704): route top-k + softmax, expert
+ * schedule (one worker, kernels/moe_router.mojo:108-145), norm-quant,
+ * phase 1, FWHT64 block-quant of the bucket, phase 2.  Caller-owned
+ * buffers: route_idx/route_w [T*top_k], eo [E+1], routes [T*top_k], xq
+ * [T,hidden], xsa [T], bucket [T*top_k, inter], bi8 [T*top_k, inter], bsa
+ * [T*top_k, inter/64], accum/out [T, hidden]. */
+void bqcpu_moe_layer(const float* logits, const uint16_t* pes, const uint16_t* x,
+                     const uint16_t* gamma, int T, int E, int top_k, int hidden, int inter,
+                     float sqrt_n, float n_eps, const int8_t* wgu, const float* gsc,
+                     const float* gcs, const int8_t* wd, const float* dsc, const float* dcs,
+                     int32_t* route_idx, float* route_w, int32_t* eo, bqo_route* routes,
+                     int8_t* xq, float* xsa, uint16_t* bucket, int8_t* bi8, float* bsa,
+                     float* accum, uint16_t* out, int nthreads) {
+    if (T <= 0) return;
+    bqcpu_route_topk(logits, T, E, top_k, pes, route_idx, route_w, nthreads);
+    bqo_build_schedule(route_idx, route_w, T, top_k, E, eo, routes);
+    bqcpu_norm_quant(x, gamma, xq, xsa, T, hidden, 128, sqrt_n, n_eps, nthreads);
+    bqcpu_moe_phase1(xq, xsa, hidden, eo, routes, E, wgu, gsc, gcs, inter, bucket, nthreads);
+    bqcpu_block_quant(bucket, bi8, bsa, eo[E], inter, 64, 1, nthreads);
+    bqcpu_moe_phase2(bi8, bsa, inter, 64, eo, routes, E, T, wd, dsc, dcs, hidden, accum, out,
+                     nthreads);
 }

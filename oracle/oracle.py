@@ -533,3 +533,125 @@ def flash_attention(q_i8, qi_bias, f_q, k_cache, k_scale, v_cache, v_scale, runs
       num_q, num_kv, head_dim, window, degree, rank, page_shift, row_mask, page_mask, s_max,
       min_split, _p(out), _p(o32))
     return (out, o32) if with_f32 else out
+
+
+# ---------------------------------------------------------------- CPU baseline (VNNI port)
+# oracle/cpu_baseline.c: the reference's VNNI branch with OpenMP workers and the
+# reference's worker policies; bench.py times it, tests pin it to the oracle.
+def cpu_pin(cpus) -> None:
+    """Pin the OpenMP team: thread i (0 = the caller) to CPU cpus[i]."""
+    c = np.ascontiguousarray(cpus, np.int32)
+    if cpu().bqcpu_pin(_p(c), int(c.size)) != 0:
+        raise OSError(f"could not pin {c.size} OpenMP threads to CPUs {list(c)}")
+
+
+def cpu_linear(act, sa, wpacked, wsc, colsum, n_rows: int, nthreads: int = 4):
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    m, K = act.shape
+    out = np.empty((m, n_rows), np.uint16)
+    cpu().bqcpu_linear(_p(act), _p(sa), m, _p(_c(wpacked, np.int8)), _p(_c(wsc, np.float32)),
+                       _p(_c(colsum, np.float32)), n_rows, K, _p(out), nthreads)
+    return out
+
+
+def cpu_block_linear(act, sa, wpacked, wsc, colsum, n: int, block: int, nthreads: int = 4):
+    act = _c(act, np.int8); sa = _c(sa, np.float32)
+    m, K = act.shape
+    out = np.empty((m, n), np.uint16)
+    cpu().bqcpu_block_linear(_p(act), _p(sa), m, _p(_c(wpacked, np.int8)),
+                             _p(_c(wsc, np.float32)), _p(_c(colsum, np.float32)), n, K, block,
+                             _p(out), nthreads)
+    return out
+
+
+def cpu_norm_quant(x_bf16, gamma_bf16, block: int = 128, nthreads: int = 4):
+    x = _c(x_bf16, np.uint16); g = _c(gamma_bf16, np.uint16)
+    m, hidden = x.shape
+    sqrt_n, n_eps = norm_consts(hidden)
+    q = np.empty((m, hidden), np.int8)
+    sa = np.empty(m, np.float32)
+    cpu().bqcpu_norm_quant(_p(x), _p(g), _p(q), _p(sa), m, hidden, block, C.c_float(sqrt_n),
+                           C.c_float(n_eps), nthreads)
+    return q, sa
+
+
+def cpu_block_quant(x_bf16, block: int, apply_fwht: bool, nthreads: int = 4):
+    x = _c(x_bf16, np.uint16)
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.int8)
+    sa = np.empty((rows, cols // block), np.float32)
+    cpu().bqcpu_block_quant(_p(x), _p(q), _p(sa), rows, cols, block, int(apply_fwht), nthreads)
+    return q, sa
+
+
+def cpu_route_topk(logits, top_k: int = 8, per_expert_scale=None, nthreads: int = 4):
+    lg = _c(logits, np.float32)
+    T, E = lg.shape
+    idx = np.empty((T, top_k), np.int32)
+    w = np.empty((T, top_k), np.float32)
+    sc = None if per_expert_scale is None else _c(per_expert_scale, np.uint16)
+    cpu().bqcpu_route_topk(_p(lg), T, E, top_k, _p(sc) if sc is not None else None, _p(idx),
+                           _p(w), nthreads)
+    return idx, w
+
+
+def cpu_moe_phase1(x_i8, x_sa, expert_offset, routes, w_gu_packed, gu_scale, gu_colsum,
+                   inter: int, nthreads: int = 4):
+    x_i8 = _c(x_i8, np.int8); x_sa = _c(x_sa, np.float32)
+    eo = _c(expert_offset, np.int32); routes = np.ascontiguousarray(routes, ROUTE_DTYPE)
+    E = eo.size - 1
+    bucket = np.zeros((max(int(eo[E]), 1), inter), np.uint16)
+    cpu().bqcpu_moe_phase1(_p(x_i8), _p(x_sa), x_i8.shape[1], _p(eo), _p(routes), E,
+                           _p(_c(w_gu_packed, np.int8)), _p(_c(gu_scale, np.float32)),
+                           _p(_c(gu_colsum, np.float32)), inter, _p(bucket), nthreads)
+    return bucket[: int(eo[E])]
+
+
+def cpu_moe_phase2(bucket_i8, bucket_sa, expert_offset, routes, T: int, w_d_packed, d_scale,
+                   d_colsum, hidden: int, block: int = 64, nthreads: int = 4):
+    bi = _c(bucket_i8, np.int8); bs = _c(bucket_sa, np.float32)
+    eo = _c(expert_offset, np.int32); routes = np.ascontiguousarray(routes, ROUTE_DTYPE)
+    E = eo.size - 1
+    accum = np.empty((T, hidden), np.float32)
+    out = np.empty((T, hidden), np.uint16)
+    cpu().bqcpu_moe_phase2(_p(bi), _p(bs), bi.shape[1], block, _p(eo), _p(routes), E, T,
+                           _p(_c(w_d_packed, np.int8)), _p(_c(d_scale, np.float32)),
+                           _p(_c(d_colsum, np.float32)), hidden, _p(accum), _p(out), nthreads)
+    return accum, out
+
+
+class CpuMoeLayer:
+    """The whole MoE layer of oracle/cpu_baseline.c (bqcpu_moe_layer) from
+    router logits, with every buffer allocated once: route top-k + softmax,
+    schedule, norm-quant, phase 1, FWHT64 block-quant, phase 2."""
+
+    def __init__(self, T, E, top_k, hidden, inter, gp, gsc, gcs, dp, dsc, dcs):
+        self.T, self.E, self.k, self.H, self.I = T, E, top_k, hidden, inter
+        self.w = [_c(a, t) for a, t in ((gp, np.int8), (gsc, np.float32), (gcs, np.float32),
+                                        (dp, np.int8), (dsc, np.float32), (dcs, np.float32))]
+        R = T * top_k
+        self.idx = np.empty((T, top_k), np.int32)
+        self.rw = np.empty((T, top_k), np.float32)
+        self.eo = np.empty(E + 1, np.int32)
+        self.routes = np.zeros(R, ROUTE_DTYPE)
+        self.xq = np.empty((T, hidden), np.int8)
+        self.xsa = np.empty(T, np.float32)
+        self.bucket = np.empty((R, inter), np.uint16)
+        self.bi8 = np.empty((R, inter), np.int8)
+        self.bsa = np.empty((R, inter // 64), np.float32)
+        self.accum = np.empty((T, hidden), np.float32)
+        self.out = np.empty((T, hidden), np.uint16)
+        self.sqrt_n, self.n_eps = norm_consts(hidden)
+
+    def __call__(self, logits, x_bf16, gamma_bf16, pes=None, nthreads: int = 4):
+        lg = _c(logits, np.float32); x = _c(x_bf16, np.uint16); g = _c(gamma_bf16, np.uint16)
+        assert lg.shape == (self.T, self.E) and x.shape == (self.T, self.H)
+        sc = None if pes is None else _c(pes, np.uint16)
+        gp, gsc, gcs, dp, dsc, dcs = self.w
+        cpu().bqcpu_moe_layer(
+            _p(lg), _p(sc) if sc is not None else None, _p(x), _p(g), self.T, self.E, self.k,
+            self.H, self.I, C.c_float(self.sqrt_n), C.c_float(self.n_eps), _p(gp), _p(gsc),
+            _p(gcs), _p(dp), _p(dsc), _p(dcs), _p(self.idx), _p(self.rw), _p(self.eo),
+            _p(self.routes), _p(self.xq), _p(self.xsa), _p(self.bucket), _p(self.bi8),
+            _p(self.bsa), _p(self.accum), _p(self.out), nthreads)
+        return self.accum, self.out
