@@ -241,22 +241,91 @@ def test_block_linear_closed_form(O, B):
     np.testing.assert_array_equal(sf, of)
 
 
-def test_fast_math_bounds(O):
-    x = np.linspace(-87, 0, 20001).astype(np.float32)
-    e = O.exp_fast(x)
-    rel = np.abs(e.astype(np.float64) / np.exp(x.astype(np.float64)) - 1)
-    assert rel.max() < 4e-3
+def _f32(v):
+    return np.float32(v)
+
+
+def _bits(v):
+    return int(np.array([v], np.float32).view(np.uint32)[0])
+
+
+def test_exp_fast_coefficients(O):
+    """exp_f32_fast (simd_math/ops.mojo:73-96) on |x| < ln2/2 has n = 0 and
+    2^n = 1, so it is exactly its cubic 1 + r(c1 + r(c2 + r c3)) with r = x.
+    Even and odd parts of oracle outputs at +-h recover the coefficients:
+    p(h) + p(-h) = 2 + 2 c2 h^2 and (p(h) - p(-h)) / 2h = c1 + c3 h^2.  They
+    must be the reference's 0.9999 / 0.4985 / 0.1681 (ops.mojo:88-90), not
+    the Taylor 1 / 0.5 / 1/6 that the accurate exp_f32 approximates."""
+    e = lambda v: float(O.lib().bqo_exp_f32_fast(float(v)))
+    h1, h2 = 0.25, 0.125
+    c2 = np.mean([(e(h) + e(-h) - 2.0) / (2 * h * h) for h in (h1, h2)])
+    d1, d2 = ((e(h) - e(-h)) / (2 * h) for h in (h1, h2))
+    c3 = (d1 - d2) / (h1 * h1 - h2 * h2)
+    c1 = d2 - c3 * h2 * h2
+    assert abs(c1 - 0.9999) < 2e-5, c1
+    assert abs(c2 - 0.4985) < 2e-5, c2
+    assert abs(c3 - 0.1681) < 2e-4, c3
+
+
+def test_exp_fast_reduction_and_error(O):
+    """Range reduction n = roundeven(x/ln2), r = x - n ln2, result p(r) 2^n
+    (ops.mojo:83-95): fast(x) == fast(r) * 2^n exactly, with r the f32
+    reduction; the input clamp at -87 (:82); and the error against exp is the
+    polynomial's own, above the 1e-3 that an accurate exp would meet and
+    below the documented ~0.3% (:76)."""
     lib = O.lib()
-    xs = np.linspace(-12, 12, 4801).astype(np.float32)
-    t = np.array([lib.bqo_tanh_f32(float(v)) for v in xs])
-    assert np.abs(t - np.tanh(xs.astype(np.float64))).max() < 4e-3
-    assert lib.bqo_tanh_f32(-1.0) < 0 < lib.bqo_tanh_f32(1.0)
-    g = O.gelu_tanh(xs)
-    xd = xs.astype(np.float64)
+    LN2, INV_LN2 = _f32(0.6931471805599453), _f32(1.4426950408889634)
+    for x in (-0.5, -1.0, -3.3, -7.0, -20.25, -60.0, -86.9):
+        xf = _f32(x)
+        n = int(np.rint(_f32(xf * INV_LN2)))
+        r = _f32(xf - _f32(_f32(n) * LN2))
+        assert abs(r) <= 0.35
+        assert _f32(lib.bqo_exp_f32_fast(float(xf))) == _f32(lib.bqo_exp_f32_fast(float(r))) * _f32(2.0 ** n)
+    assert lib.bqo_exp_f32_fast(-100.0) == lib.bqo_exp_f32_fast(-87.0)
+    x = np.linspace(-87, 0, 20001).astype(np.float32)
+    rel = np.abs(O.exp_fast(x).astype(np.float64) / np.exp(x.astype(np.float64)) - 1)
+    assert 1e-3 < rel.max() < 4e-3, rel.max()
+
+
+def test_tanh_gelu_closed_forms(O):
+    """tanh_f32 (ops.mojo:128-141) is sign(x) (1 - E)/(1 + E) with E the
+    pinned fast exp of -2|x|, and gelu_tanh_f32 (:145-156) is
+    0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))) on that tanh, both in
+    f32 with the reference's op order; exact tanh-GELU within 4e-3 |x|."""
+    lib = O.lib()
+    xs = np.concatenate([np.linspace(-12, 12, 4801), [0.0, -0.0, 1e-8, -3e-5, 40.0]]).astype(np.float32)
+    for x in xs:
+        E = _f32(lib.bqo_exp_f32_fast(float(_f32(-2.0) * _f32(abs(x)))))
+        t = _f32(_f32(1.0 - E) / _f32(1.0 + E))
+        t = -t if np.signbit(x) else t
+        assert _bits(lib.bqo_tanh_f32(float(x))) == _bits(t), x
+        x3 = _f32(_f32(x * x) * x)
+        inner = _f32(_f32(0.7978845608028654) * _f32(x + _f32(_f32(0.044715) * x3)))
+        g = _f32(_f32(_f32(0.5) * x) * _f32(1.0 + _f32(lib.bqo_tanh_f32(float(inner)))))
+        assert _bits(lib.bqo_gelu_tanh_f32(float(x))) == _bits(g), x
+    g = O.gelu_tanh(xs[:4801])
+    xd = xs[:4801].astype(np.float64)
     exact = 0.5 * xd * (1 + np.tanh(math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)))
     assert (np.abs(g - exact) <= 4e-3 * np.abs(xd) + 1e-6).all()
-    # the softmax exp is used on top-8 logit differences; away from f32
-    # underflow (x > -60) it is within 1% of exp
+
+
+def test_softmax_exp_known_values(O):
+    """fast_exp_softmax_biased (simd_math/exponential.mojo:178-194) by hand:
+    v = f32(12102203.16156148 x + 1059208216), i = trunc(v), k = the f32 with
+    bits i, f = (i & 0x7FFFFF) / 2^23, result k (1.6501418 + f (-0.3755484 +
+    f 0.3869647)).
+      x =  0: v = 1059208192 = 0x3F223C00 (the bias rounded to f32's 64-step
+              grid), k = 0.6337280, f = 0x223C00/2^23 = 0.2674561
+              -> 0.99962980 (0x3F7FE7BD)
+      x = -1: A x rounds to -12102203, v = 1047105989 -> f32 1047106048
+              = 0x3E6991C0, k = 0.2280951, f = 0.8247604
+              -> 0.36577994 (0x3EBB4782)
+      x = -5: v = 998697177 -> f32 998697152 = 0x3B86E8C0, k = 0.0041171,
+              f = 0.0539780 -> 0.0067149843 (0x3BDC095F)
+    and within 1% of exp on the top-8 logit differences it sees (x > -60)."""
+    lib = O.lib()
+    for x, want in ((0.0, 0x3F7FE7BD), (-1.0, 0x3EBB4782), (-5.0, 0x3BDC095F)):
+        assert _bits(lib.bqo_fast_exp_softmax_biased(x)) == want, (x, hex(_bits(lib.bqo_fast_exp_softmax_biased(x))))
     xs2 = np.linspace(-60, 0, 3001).astype(np.float32)
     sb = np.array([lib.bqo_fast_exp_softmax_biased(float(v)) for v in xs2])
     assert (np.abs(sb / np.exp(xs2.astype(np.float64)) - 1) < 1e-2).all()
