@@ -159,8 +159,9 @@ int bq_moe_route_topk(const float* logits, const uint16_t* per_expert_scale, int
 
 /* dispatch_build_expert_schedules (kernels/moe_router.mojo:60-145): routes
  * of experts [expert_base, expert_base+experts) into expert_offset[experts+1]
- * and routes[] sorted by (expert, token, k).  Each token's top_k experts must
- * be distinct (top-k routing).  experts <= 256; routes holds seq_len*top_k. */
+ * and routes[] sorted by (expert, token, k).  A token may list an expert more
+ * than once (the router pads with expert 0); its records then sit in k order.
+ * experts <= 256; routes holds seq_len*top_k. */
 int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
                           int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
                           void* stream);
@@ -187,8 +188,8 @@ size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden);
  * f32 [seq_len, hidden]; moe_out = bf16(moe_accum).  w_down rows are
  * [experts_per_rank*hidden, inter] (expert stride hidden*inter).
  * Each expert's route records must be in ascending token order (the order
- * bq_moe_build_schedule and the reference's schedule produce), and a token
- * appears at most once per expert; top_k <= 16.
+ * bq_moe_build_schedule and the reference's schedule produce); a token's
+ * records within one expert are added in record order; top_k <= 16.
  * workspace: >= bq_moe_phase2_workspace_size() bytes, 256-byte aligned;
  * moe_accum and moe_out 16-byte aligned. */
 int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,

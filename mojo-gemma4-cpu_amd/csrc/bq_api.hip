@@ -3,6 +3,9 @@
 // become status codes), then kernel launches on the caller's stream.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+
+#include <mutex>
 
 #include "../../include/bq_api.h"
 #include "bq_kernels.hpp"
@@ -42,6 +45,46 @@ int api_failv(int code, const char* fmt, va_list ap) {
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   return code;
 }
+
+namespace {
+Tune g_tune{};
+std::once_flag g_tune_once;
+
+int env_int(const char* name) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : 0;
+}
+}  // namespace
+
+void tune_init(int device) {
+  Tune t{};
+  t.gemv_waves = env_int("BQ_GEMV_WAVES");
+  t.tile_bm = env_int("BQ_TILE_BM");
+  t.tile_bn = env_int("BQ_TILE_BN");
+  t.ring = env_int("BQ_RING");
+  t.tile_ksp = env_int("BQ_TILE_KSP");
+  t.moe_bm = env_int("BQ_MOE_BM");
+  t.moe_bm_down = env_int("BQ_MOE_BM_DOWN");
+  t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 2;
+  t.down_breg = getenv("BQ_DOWN_BREG") ? env_int("BQ_DOWN_BREG") : 1;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  t.cus = cus;
+  g_tune = t;
+}
+
+const Tune& tune() {
+  std::call_once(g_tune_once, [] {
+    if (g_tune.cus == 0) {
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+      tune_init(dev);
+    }
+  });
+  return g_tune;
+}
 }  // namespace bq
 
 extern "C" {
@@ -53,7 +96,10 @@ const char* bq_last_error(void) { return g_err; }
 int bq_init(int device) {
   int r = check_hip(hipSetDevice(device), "hipSetDevice");
   if (r) return r;
-  return check_hip(hipFree(nullptr), "hip runtime init");
+  r = check_hip(hipFree(nullptr), "hip runtime init");
+  if (r) return r;
+  bq::tune_init(device);
+  return BQ_OK;
 }
 
 int bq_stream_synchronize(void* stream) {

@@ -17,8 +17,6 @@
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
-#include <stdlib.h>
-
 namespace bq {
 
 __device__ inline const LinSeg& pick_seg(const LinArgs& a, int nt_global, int& nt_local) {
@@ -191,7 +189,7 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     // 8 waves split K so that each wave's whole slice (<= 8 fragments for
     // K <= 4096) is requested at once: the full weight is in flight within
     // the first memory latency.
-    const int waves = getenv("BQ_GEMV_WAVES") ? atoi(getenv("BQ_GEMV_WAVES")) : 8;
+    const int waves = tune().gemv_waves ? tune().gemv_waves : 8;
     const int nb = a.K / a.block;
     dim3 g(tiles);
     if (waves >= 16) {
@@ -215,7 +213,7 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
   int bm = 32;
   if (a.M > 64 && ((a.M + 127) / 128) * gn128 >= 256) bm = 128;
   else if (a.M > 32) bm = 64;
-  if (const char* s = getenv("BQ_TILE_BM")) bm = atoi(s);
+  if (tune().tile_bm) bm = tune().tile_bm;
   return launch_linear_tiled(a, per_block, bm, st);
 }
 

@@ -84,7 +84,9 @@ __global__ __launch_bounds__(256) void k_embed(
   constexpr int B = R * kWave;
   const int nb = hidden / B;
   const int tid = tokens[t];
-  const int owner = tid / shard_rows;
+  // the owner is Mojo's floor division tid // shard_rows (embedding.mojo:42):
+  // a negative id belongs to no rank and gives a zero row
+  const int owner = tid / shard_rows - ((tid % shard_rows != 0 && tid < 0) ? 1 : 0);
   uint16_t* d = dst + (size_t)t * hidden;
   if (owner != rank) {  // embedding.mojo:53: zero_row for another shard's token
     for (int k = threadIdx.x; k < hidden; k += blockDim.x) d[k] = 0;

@@ -9,6 +9,24 @@
 
 namespace bq {
 
+// Tuning switches (BQ_* environment variables, 0 = the launcher's default)
+// and the device's compute-unit count, read once: at bq_init, or at the
+// first launch of a process that never called it.
+struct Tune {
+  int gemv_waves;   // BQ_GEMV_WAVES: waves per decode-GEMV workgroup (4, 8, 16)
+  int tile_bm;      // BQ_TILE_BM: rows per tiled prefill tile (32, 64, 128)
+  int tile_bn;      // BQ_TILE_BN: columns per tiled tile (128, 256)
+  int ring;         // BQ_RING: LDS ring stages of the tiled kernels
+  int tile_ksp;     // BQ_TILE_KSP: K groups per 64 x 128 prefill tile (1, 2)
+  int moe_bm;       // BQ_MOE_BM: MoE m-tile records (16 = skinny kernels)
+  int moe_bm_down;  // BQ_MOE_BM_DOWN: the down projection's m-tile alone
+  int moe_order;    // BQ_MOE_ORDER: MoE work order of the LDS-ring kernels (0, 1, 2)
+  int down_breg;    // BQ_DOWN_BREG: 0 disables the register-streamed down kernel
+  int cus;          // compute units of the device
+};
+const Tune& tune();
+void tune_init(int device);
+
 // One output segment of a (possibly fused) per-row / per-block linear: the
 // fused q/k/v projection (butterquant_kernels/linear.mojo:273-326) runs as
 // three segments of one launch sharing the activation.

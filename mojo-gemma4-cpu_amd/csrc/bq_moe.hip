@@ -17,15 +17,14 @@
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
-#include <stdlib.h>
-
 namespace bq {
 
 constexpr int kMaxExperts = 256;
 
-// One workgroup per expert e.  Because each token's top-k experts are
-// distinct, the (expert, token, k) order puts route slot s = t*top_k + kk of
-// expert e at expert_offset[e] + (number of earlier slots routed to e), and
+// One workgroup per expert e.  The (expert, token, k) order puts route slot
+// s = t*top_k + kk of expert e at expert_offset[e] + (number of earlier slots
+// routed to e) -- slot order is (token, k) order, also for a token that lists
+// an expert twice -- and
 // expert_offset[e] = number of slots routed to experts below e.  Both counts
 // come from scanning route_idx: a chunk of kRows x 1024 slots is read
 // coalesced (thread tid takes slots j*1024 + tid, row j = 0..kRows-1), so
@@ -357,9 +356,12 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
 
 // Ordered combine, one workgroup per token t: accum[t, :] = (((0 + y[r1]) +
 // y[r2]) + ...) over t's records in ascending expert order (moe.mojo:259-282),
-// out = bf16(accum).  t's record in expert e's segment is found by binary
-// search (segments are in ascending token order); a ballot over experts
-// lists the records in ascending expert order.  At most kMaxTopK records.
+// out = bf16(accum).  t's records in expert e's segment are a run that starts
+// where a binary search for t lands (segments are in ascending token order);
+// a token that lists an expert twice (the router's padding repeats expert 0)
+// has a run of two, added in record order as the reference adds its routes.
+// A scan over experts lists the runs in ascending expert order.  At most
+// kMaxTopK records.
 constexpr int kMaxTopK = 16;
 
 __global__ __launch_bounds__(256) void k_combine(
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(256) void k_combine(
   int cnt = 0;
   for (int e0 = 0; e0 < E; e0 += 256) {
     const int e = e0 + tid;
-    int found = -1;
+    int first = 0, run = 0;
     if (e < E) {
       const int lo0 = max(0, min(eo[e], max_routes)), hi0 = max(0, min(eo[e + 1], max_routes));
       int lo = lo0, hi = hi0;
@@ -379,10 +381,17 @@ __global__ __launch_bounds__(256) void k_combine(
         const int mid = (lo + hi) >> 1;
         if (routes[mid].token < t) lo = mid + 1; else hi = mid;
       }
-      if (lo < hi0 && routes[lo].token == t) found = lo;
+      first = lo;
+      while (lo + run < hi0 && run < kMaxTopK && routes[lo + run].token == t) ++run;
     }
-    const unsigned long long m = __ballot(found >= 0);
-    if (lane == 0) wsum[wave] = __popcll(m);
+    // exclusive prefix of the run lengths over this chunk's experts
+    int inc = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += v;
+    }
+    if (lane == 63) wsum[wave] = inc;
     __syncthreads();
     int base = cnt, total = 0;
 #pragma unroll
@@ -390,10 +399,9 @@ __global__ __launch_bounds__(256) void k_combine(
       base += w < wave ? wsum[w] : 0;
       total += wsum[w];
     }
-    if (found >= 0) {
-      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-      if (pos < kMaxTopK) recs[pos] = found;
-    }
+    base += inc - run;
+    for (int j = 0; j < run; ++j)
+      if (base + j < kMaxTopK) recs[base + j] = first + j;
     cnt += total;
     __syncthreads();
   }
@@ -450,7 +458,7 @@ static inline int mtile_bound(int max_routes, int experts, int bm) {
 // deviations of a binomial count): then each expert's weights stream from
 // HBM once instead of once per m-tile.
 int moe_tile_bm(int max_routes, int experts) {
-  if (const char* s = getenv("BQ_MOE_BM")) return atoi(s);
+  if (tune().moe_bm) return tune().moe_bm;
   const int per = max_routes / (experts > 0 ? experts : 1);
   if (per < 24) return 16;
   const double hi = per + 4.0 * __builtin_sqrt((double)per);
@@ -493,8 +501,7 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     const int bm = moe_tile_bm(max_routes, experts);
     if (bm >= 64 && hidden % 128 == 0) {
       // see launch_moe_down_tiled; BQ_MOE_BM_DOWN overrides the down tile alone
-      const char* bd = getenv("BQ_MOE_BM_DOWN");
-      const int bm_down = bd ? atoi(bd) : getenv("BQ_MOE_BM") ? bm : 64;
+      const int bm_down = tune().moe_bm_down ? tune().moe_bm_down : tune().moe_bm ? bm : 64;
       hipError_t e = launch_moe_down_tiled(bucket_i8, bucket_sa, eo, routes, w_down, down_scale, y,
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;

@@ -19,8 +19,6 @@
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
-#include <stdlib.h>
-
 namespace bq {
 
 enum { MODE_DENSE = 0, MODE_GATE_UP = 1, MODE_DOWN = 2 };
@@ -695,12 +693,9 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
 // ---------------------------------------------------------------------------
 // Tile configuration: BM x BN output tile, NBUF-stage LDS ring.  Smaller
 // rings leave room for several workgroups per CU (more waves to overlap the
-// LDS-read -> MFMA -> barrier chain of each); overrides BQ_TILE_BN and
-// BQ_RING exist for tuning sweeps.
-static int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  return s ? atoi(s) : dflt;
-}
+// LDS-read -> MFMA -> barrier chain of each); the BQ_TILE_BN and BQ_RING
+// switches (Tune) exist for tuning sweeps.
+static inline int or_default(int v, int dflt) { return v ? v : dflt; }
 
 constexpr size_t kLdsBytes = 160 * 1024;
 
@@ -767,8 +762,8 @@ static void launch_bm(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t 
 static inline int tile_bn(int bn) { return bn >= 256 ? 256 : 128; }
 
 hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStream_t st) {
-  const int bn = tile_bn(env_int("BQ_TILE_BN", 128));
-  const int nbuf = env_int("BQ_RING", 3);
+  const int bn = tile_bn(or_default(tune().tile_bn, 128));
+  const int nbuf = or_default(tune().ring, 3);
   TiledArgs t{};
   t.lin = a;
   int gn = 0;
@@ -780,14 +775,16 @@ hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStrea
   const size_t dyn = per_block ? (size_t)bmv * (a.K / a.block) * sizeof(float) : 0;
   // per-row 64 x 128 tiles (chosen when larger tiles leave CUs idle) run with
   // two K groups per workgroup: 21.1 -> 19.4 us at M = 512, K = N = 4096
-  if (!per_block && bmv == 64 && bn == 128 && env_int("BQ_TILE_KSP", 2) == 2) {
+  if (!per_block && bmv == 64 && bn == 128 && or_default(tune().tile_ksp, 2) == 2) {
     if (nbuf >= 3 && try_launch<MODE_DENSE, 64, 128, 2, 4, false, 3, 2>(g, 0, st, t))
       return hipGetLastError();
     try_launch<MODE_DENSE, 64, 128, 2, 4, false, 2, 2>(g, 0, st, t);
     return hipGetLastError();
   }
-  if (per_block) launch_bm<MODE_DENSE, true>(bm, bn, nbuf, g, dyn, st, t);
-  else launch_bm<MODE_DENSE, false>(bm, bn, nbuf, g, dyn, st, t);
+  // the grid is sized for bmv-row tiles, so the tile height is bmv (a larger
+  // BQ_TILE_BM is clamped to it)
+  if (per_block) launch_bm<MODE_DENSE, true>(bmv, bn, nbuf, g, dyn, st, t);
+  else launch_bm<MODE_DENSE, false>(bmv, bn, nbuf, g, dyn, st, t);
   return hipGetLastError();
 }
 
@@ -814,11 +811,11 @@ hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const
   // 256 weight rows; 192-record tiles (2048 tokens x top-8 over 128 experts)
   // with 128, whose 80 KB ring leaves room for two workgroups per CU
   // (measured 1.5% faster for that layer than 256 rows).
-  const int bn = tile_bn(env_int("BQ_TILE_BN", bmv == 256 ? 256 : 128));
-  const int nbuf = env_int("BQ_RING", 2);
+  const int bn = tile_bn(or_default(tune().tile_bn, bmv == 256 ? 256 : 128));
+  const int nbuf = or_default(tune().ring, 2);
   t.gn = (inter + bn / 2 - 1) / (bn / 2);
   t.gm = mtile_bound(max_routes, experts, bmv);
-  t.order = env_int("BQ_MOE_ORDER", 2);
+  t.order = tune().moe_order;
   const dim3 g(moe_grid(t));
   launch_bm<MODE_GATE_UP, false>(bmv, bn, nbuf, g, 0, st, t);
   return hipGetLastError();
@@ -835,26 +832,21 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
   // block-64 scales and K up to 704 (the model's inter): weights in registers,
   // 192-record m-tiles x 256 columns
   if (block == 64 && inter % 64 == 0 && inter / 64 <= 11 && experts <= kBregMaxExperts &&
-      env_int("BQ_DOWN_BREG", 1)) {
+      tune().down_breg) {
     constexpr int MI = 12, NI = 2;
     t.gn = (hidden + 8 * NI * 16 - 1) / (8 * NI * 16);
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    hipLaunchKernelGGL((k_down_breg<MI, NI, 11>), dim3(cus), dim3(512), 0, st, t);
+    hipLaunchKernelGGL((k_down_breg<MI, NI, 11>), dim3(tune().cus), dim3(512), 0, st, t);
     return hipGetLastError();
   }
   // the down projection's K (= inter) is short, and its per-block drains
   // keep f32 accumulators: 64-record tiles with a double-buffered stage run
   // fastest (more workgroups in flight per CU)
   const int bmv = bm >= 256 ? 256 : bm >= 192 ? 192 : bm >= 128 ? 128 : 64;
-  const int bn = tile_bn(env_int("BQ_TILE_BN", 128));
-  const int nbuf = env_int("BQ_RING", 2);
+  const int bn = tile_bn(or_default(tune().tile_bn, 128));
+  const int nbuf = or_default(tune().ring, 2);
   t.gn = (hidden + bn - 1) / bn;
   t.gm = mtile_bound(max_routes, experts, bmv);
-  t.order = env_int("BQ_MOE_ORDER", 2);
+  t.order = tune().moe_order;
   const dim3 g(moe_grid(t));
   const size_t dyn = (size_t)bmv * (inter / block) * sizeof(float);
   launch_bm<MODE_DOWN, true>(bmv, bn, nbuf, g, dyn, st, t);

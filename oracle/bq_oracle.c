@@ -830,7 +830,9 @@ void bqo_flash_sample(const int8_t* x_i8, const float* x_sa, const int8_t* weigh
  * per token, the owning shard's row is dequantized per block (q * scale,
  * butterquant/dequantize.mojo:6-21), FWHT(block)-rotated and written as
  * bf16(x * scale) (dequantize.mojo:25-32); a token owned by another shard
- * gives a zero row.  weight int8 [shard_rows, hidden] row-major. */
+ * gives a zero row.  The owner is Mojo's floor division tid // shard_rows
+ * (embedding.mojo:42), so a negative id belongs to no rank >= 0.
+ * weight int8 [shard_rows, hidden] row-major. */
 void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
                       const float* wscales, int hidden, int block, int shard_rows,
                       int rank, float scale, uint16_t* dst) {
@@ -838,6 +840,7 @@ void bqo_embed_lookup(const int32_t* token_ids, int T, const int8_t* weight,
     float* ws = (float*)malloc(sizeof(float) * hidden);
     for (int t = 0; t < T; ++t) {
         int tid = token_ids[t], owner = tid / shard_rows;
+        if (tid % shard_rows != 0 && tid < 0) owner -= 1;  /* floor division */
         uint16_t* d = dst + (size_t)t * hidden;
         if (owner != rank) { for (int k = 0; k < hidden; ++k) d[k] = 0; continue; }
         int local = tid - owner * shard_rows;

@@ -117,3 +117,12 @@ def test_embed_lookup(gpu, O, H, B):
     got1 = gpu.embed_lookup(dev(tok), W1, W1.scale, B, scale=scale, shard_rows=48, rank=1)
     np.testing.assert_array_equal(host(got1), O.embed_lookup(tok, w[48:], ws[48:], B, scale=scale,
                                                              shard_rows=48, rank=1))
+    # negative (padding) ids and ids past every shard: zero rows at rank 0 and 1
+    odd = np.array([-1, -48, -49, -(2 ** 31), 96, 10 ** 6, 3], np.int32)
+    for rank, Wr in ((0, upload_head(gpu, np.ascontiguousarray(w[:48]), np.ascontiguousarray(ws[:48]))),
+                     (1, W1)):
+        g = host(gpu.embed_lookup(dev(odd), Wr, Wr.scale, B, scale=scale, shard_rows=48, rank=rank))
+        np.testing.assert_array_equal(g, O.embed_lookup(odd, w[48 * rank:48 * rank + 48],
+                                                        ws[48 * rank:48 * rank + 48], B,
+                                                        scale=scale, shard_rows=48, rank=rank))
+        assert (g[:6] == 0).all()

@@ -613,6 +613,14 @@ def test_embed_lookup(O):
     assert (out_r1[1] == 0).all()
     np.testing.assert_array_equal(out_r1[0], O.embed_lookup(np.array([40], np.int32), w, ws, B,
                                                             scale=scale)[0])
+    # the owner is Mojo's floor division (embedding.mojo:42): negative ids
+    # (padding) belong to no rank >= 0, ids past the last shard to none either
+    odd = np.array([-1, -32, -33, -(2 ** 31), 64, 10 ** 6, 7], np.int32)
+    for rank in (0, 1):
+        o = O.embed_lookup(odd, w[32 * rank:32 * rank + 32], ws[32 * rank:32 * rank + 32], B,
+                           scale=scale, shard_rows=32, rank=rank)
+        assert (o[:6] == 0).all()
+        assert (o[6] != 0).any() == (rank == 0)
 
 
 def test_head_prep_per_block(O):
