@@ -198,6 +198,21 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                        int experts_per_rank, int seq_len, int top_k, int hidden, int inter,
                        int block, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: bq_moe_phase2_down for callers that
+ * cannot allocate or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Same arguments and
+ * results as bq_moe_phase2_down without workspace/workspace_bytes: the
+ * per-route f32 rows live in the library's static per-GPU scratch of
+ * 24 MiB, so seq_len * top_k * hidden * 4 <= 24 MiB (at hidden 2816 and
+ * top_k 8: up to 279 tokens), else BQ_ERR_UNSUPPORTED.  Calls nothing that
+ * allocates.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (concurrent streams or threads) race. */
+int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
+                               const int32_t* expert_offset, const bq_route* routes,
+                               const int8_t* w_down, const float* down_scale, float* moe_accum,
+                               uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
+                               int hidden, int inter, int block, void* stream);
+
 /* ---- vocabulary head and embedding ----------------------------------------- */
 
 #define BQ_SAMPLE_NMAX 256 /* continuous_batching/schedule.mojo:9 MAXIMUM_SAMPLING_LOGITS */

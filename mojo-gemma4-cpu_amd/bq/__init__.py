@@ -65,6 +65,8 @@ SIGNATURES = {
     "bq_moe_phase2_workspace_size": [_i, _i, _i],
     "bq_moe_phase2_down": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                            _vp, _sz, _vp],
+    "bq_moe_phase2_down_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                   _i, _vp],
 }
 _RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
              "bq_moe_phase2_workspace_size": C.c_size_t,
@@ -347,6 +349,23 @@ def moe_phase2(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: int, seq
                                    _p(w_d.scale), _p(accum), _p(o), experts, seq_len, top_k,
                                    hidden, inter, block, _p(workspace), workspace.numel(),
                                    _stream()))
+    return accum, o
+
+
+def moe_phase2_noalloc(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: int,
+                       seq_len: int, top_k: int, hidden: int, block: int = 64, out=None):
+    """bq_moe_phase2_down_noalloc: phase 2 on the library's static scratch
+    (no workspace); seq_len * top_k * hidden * 4 bytes <= 24 MiB."""
+    inter = b_i8.shape[1]
+    dev = b_i8.device
+    if out is None:
+        accum = torch.empty((seq_len, hidden), dtype=torch.float32, device=dev)
+        o = torch.empty((seq_len, hidden), dtype=torch.bfloat16, device=dev)
+    else:
+        accum, o = out
+    _check(_lib.bq_moe_phase2_down_noalloc(_p(b_i8), _p(b_sa), _p(eo), _p(routes), _p(w_d.data),
+                                           _p(w_d.scale), _p(accum), _p(o), experts, seq_len,
+                                           top_k, hidden, inter, block, _stream()))
     return accum, o
 
 

@@ -50,11 +50,38 @@ namespace {
 Tune g_tune{};
 std::once_flag g_tune_once;
 
+// The allocation-free phase 2 (bq_moe_phase2_down_noalloc) keeps its
+// workspace -- the per-route f32 rows of the down projection -- in this
+// file-scope device array: every GPU the library runs on holds one copy, at
+// its own address, until the process ends.  Host code uses only the address
+// hipGetSymbolAddress returns for the current device (kept per device in
+// g_scratch), never the array's name.
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+void* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// the scratch address on `device` (the current device), looked up once
+hipError_t scratch_ptr(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return hipSuccess;
+}
+
 int env_int(const char* name) {
   const char* s = getenv(name);
   return s ? atoi(s) : 0;
 }
 }  // namespace
+
+hipError_t scratch_address(int device, void** out) { return scratch_ptr(device, out); }
 
 void tune_init(int device) {
   Tune t{};
@@ -99,7 +126,8 @@ int bq_init(int device) {
   r = check_hip(hipFree(nullptr), "hip runtime init");
   if (r) return r;
   bq::tune_init(device);
-  return BQ_OK;
+  void* sp = nullptr;
+  return check_hip(bq::scratch_address(device, &sp), "scratch symbol address");
 }
 
 int bq_stream_synchronize(void* stream) {
@@ -330,6 +358,39 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                                          down_scale, moe_accum, moe_out, experts_per_rank, seq_len,
                                          seq_len * top_k, hidden, inter, block, workspace,
                                          S(stream)), "moe_phase2");
+}
+
+int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
+                               const int32_t* expert_offset, const bq_route* routes,
+                               const int8_t* w_down, const float* down_scale, float* moe_accum,
+                               uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
+                               int hidden, int inter, int block, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (top_k <= 0 || top_k > 16 || hidden <= 0)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down_noalloc: top_k %d not in [1,16]", top_k);
+  // the workspace is seq_len*top_k f32 rows of hidden (bq_moe_phase2_workspace_size)
+  const size_t bytes = (size_t)seq_len * (size_t)top_k * (size_t)hidden * sizeof(float);
+  if (bytes > bq::kNoallocScratchBytes)
+    return fail(BQ_ERR_UNSUPPORTED,
+                "bq_moe_phase2_down_noalloc: seq_len*top_k*hidden*4 = %zu bytes exceeds the "
+                "%zu-byte static scratch (use bq_moe_phase2_down with a workspace)",
+                bytes, bq::kNoallocScratchBytes);
+  int device = 0;
+  int r = check_hip(hipGetDevice(&device), "hipGetDevice");
+  if (r) return r;
+  void* ws = nullptr;
+  r = check_hip(bq::scratch_address(device, &ws), "scratch symbol address");
+  if (r) return r;
+  r = bq_moe_phase2_down(bucket_i8, bucket_sa, expert_offset, routes, w_down, down_scale,
+                         moe_accum, moe_out, experts_per_rank, seq_len, top_k, hidden, inter,
+                         block, ws, bq::kNoallocScratchBytes, stream);
+  if (r && r != BQ_ERR_HIP) {
+    // re-label the shared validation's message with this entry point's name
+    char msg[sizeof(g_err)];
+    snprintf(msg, sizeof(msg), "%s", g_err);
+    return fail(r, "bq_moe_phase2_down_noalloc <- %s", msg);
+  }
+  return r;
 }
 
 }  // extern "C"

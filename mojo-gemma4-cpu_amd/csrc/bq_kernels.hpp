@@ -27,6 +27,11 @@ struct Tune {
 const Tune& tune();
 void tune_init(int device);
 
+// the allocation-free phase 2's static device scratch (bytes) and its
+// address on a device
+constexpr size_t kNoallocScratchBytes = size_t(24) << 20;
+hipError_t scratch_address(int device, void** out);
+
 // One output segment of a (possibly fused) per-row / per-block linear: the
 // fused q/k/v projection (butterquant_kernels/linear.mojo:273-326) runs as
 // three segments of one launch sharing the activation.
