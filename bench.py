@@ -141,9 +141,9 @@ def bench_prefill(bq, torch, steps, warmup, reps=32):
 
 class MoeLayer:
     """One quantized MoE expert layer from router logits: top-8 + softmax
-    routing -> norm-quant -> CSR schedule -> phase 1 (gate/up + GELU) ->
-    FWHT64 block-quant -> phase 2 (down + route-weighted, expert-ordered
-    combine)."""
+    routing -> norm-quant -> CSR schedule -> phase 1 (gate/up + GELU) with
+    the FWHT64 block-quant of the bucket fused -> phase 2 (down +
+    route-weighted, expert-ordered combine)."""
 
     def __init__(self, bq, torch, T, Wgu, Wd, gen_seed=1):
         self.bq, self.T = bq, T
@@ -169,13 +169,18 @@ class MoeLayer:
         self.accum = torch.empty(T, H, dtype=torch.float32, device=d)
         self.out = torch.empty(T, H, dtype=torch.bfloat16, device=d)
 
-    def __call__(self, _i=0):
+    def __call__(self, _i=0, fused=True):
         bq, T = self.bq, self.T
         bq.route_topk(self.logits, TOPK, self.pes, out=(self.idx, self.w))
         bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
         bq.build_schedule(self.idx, self.w, E, out=(self.eo, self.routes))
-        bq.moe_phase1(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I, out=self.bucket)
-        bq.block_quant(self.bucket, 64, True, out=(self.bi8, self.bsa))
+        if fused:  # phase 1 with the bucket's FWHT64 block-quant in its epilogue
+            bq.moe_phase1_quant(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I,
+                                out=(self.bi8, self.bsa, None))
+        else:
+            bq.moe_phase1(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I,
+                          out=self.bucket)
+            bq.block_quant(self.bucket, 64, True, out=(self.bi8, self.bsa))
         bq.moe_phase2(self.bi8, self.bsa, self.eo, self.routes, self.Wd, E, T, TOPK, H,
                       workspace=self.ws, out=(self.accum, self.out))
 

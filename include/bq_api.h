@@ -178,6 +178,25 @@ int bq_moe_phase1_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* 
                           const float* gate_up_scale, uint16_t* bucket, int experts_per_rank,
                           int seq_len, int top_k, int hidden, int inter, void* stream);
 
+/* dispatch_bq_phase1_gate_up (moe.mojo:132-164) followed by
+ * dispatch_bq_block_quant[block = 64, apply_fwht = True] of its bucket
+ * (modeling/gemma_4_moe_bq.mojo:689-700), in one call: for every route record
+ * rec of expert e, bucket[rec, i] = bf16(gelu_tanh(g)*u) as
+ * bq_moe_phase1_gate_up computes it, then per 64-column block of the bf16
+ * row FWHT(64) and per-block int8: bucket_i8 [seq_len*top_k, inter],
+ * bucket_sa [seq_len*top_k, inter/64] = block amax -- bit for bit what the
+ * two calls produce, for the rows of records [0, expert_offset[experts]).
+ * The block-quant runs in the GEMM's epilogue on the tile's bucket values
+ * kept in LDS; bucket (bf16) may be NULL, and is then never written to
+ * memory.  inter % 64 == 0, hidden % 64 == 0; x_i8, w_gate_up and bucket
+ * 16-byte, bucket_i8 8-byte, bucket_sa 4-byte aligned. */
+int bq_moe_phase1_gate_up_quant(const int8_t* x_i8, const float* x_sa,
+                                const int32_t* expert_offset, const bq_route* routes,
+                                const int8_t* w_gate_up, const float* gate_up_scale,
+                                uint16_t* bucket, int8_t* bucket_i8, float* bucket_sa,
+                                int experts_per_rank, int seq_len, int top_k, int hidden,
+                                int inter, void* stream);
+
 /* Bytes of device workspace bq_moe_phase2_down needs (the per-route f32
  * down-projection rows, seq_len*top_k x hidden). */
 size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden);

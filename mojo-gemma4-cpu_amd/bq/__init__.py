@@ -62,6 +62,7 @@ SIGNATURES = {
     "bq_load_quantized": [C.POINTER(C.c_void_p), _i, C.c_char_p, _i, _i, _i, _vp, _vp, _vp, _sz,
                           _vp],
     "bq_moe_phase1_gate_up": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "bq_moe_phase1_gate_up_quant": [_vp] * 9 + [_i] * 5 + [_vp],
     "bq_moe_phase2_workspace_size": [_i, _i, _i],
     "bq_moe_phase2_down": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                            _vp, _sz, _vp],
@@ -327,6 +328,26 @@ def moe_phase1(x_i8, x_sa, eo, routes, w_gu: ButterquantWeight, experts: int, se
                                       _p(w_gu.scale), _p(out), experts, seq_len, top_k, hidden,
                                       inter, _stream()))
     return out
+
+
+def moe_phase1_quant(x_i8, x_sa, eo, routes, w_gu: ButterquantWeight, experts: int,
+                     seq_len: int, top_k: int, inter: int, bucket=False, out=None):
+    """bq_moe_phase1_gate_up_quant: phase 1 with the bucket's FWHT64
+    block-quant fused -> (bucket_i8, bucket_sa[, bucket bf16 if bucket])."""
+    hidden = x_i8.shape[1]
+    dev = x_i8.device
+    R = seq_len * top_k
+    if out is None:
+        bi8 = torch.empty((R, inter), dtype=torch.int8, device=dev)
+        bsa = torch.empty((R, inter // 64), dtype=torch.float32, device=dev)
+        bb = torch.empty((R, inter), dtype=torch.bfloat16, device=dev) if bucket else None
+    else:
+        bi8, bsa, bb = out
+    _check(_lib.bq_moe_phase1_gate_up_quant(_p(x_i8), _p(x_sa), _p(eo), _p(routes),
+                                            _p(w_gu.data), _p(w_gu.scale), _p(bb), _p(bi8),
+                                            _p(bsa), experts, seq_len, top_k, hidden, inter,
+                                            _stream()))
+    return (bi8, bsa, bb) if bb is not None else (bi8, bsa)
 
 
 def moe_phase2_workspace_size(seq_len: int, top_k: int, hidden: int) -> int:

@@ -354,39 +354,10 @@ __global__ __launch_bounds__(256) void k_block_quant(
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t c = i < nchunks ? i : nchunks - 1;  // whole LPB groups are in or out
   const int lane = lane_id();
-  const v4i raw = *reinterpret_cast<const v4i*>(src + c * 8);
   float v[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[2 * j] = __uint_as_float((uint32_t)raw[j] << 16);
-    v[2 * j + 1] = __uint_as_float((uint32_t)raw[j] & 0xFFFF0000u);
-  }
-  if (apply_fwht) {
-#pragma unroll
-    for (int s = 1; s < 8; s <<= 1)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j & s) continue;
-        const float a = v[j], b = v[j + s];
-        v[j] = a + b;
-        v[j + s] = a - b;
-      }
-    for_each_xlane_stride(LPB, [&](auto st) {
-      constexpr int ST = decltype(st)::value;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = xlane_bfly<ST>(v[j]);
-    });
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = v[j] * fwht_scale;
-  }
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
-  for_each_xlane_stride(LPB, [&](auto st) { m = fmaxf(m, xlane_partner<decltype(st)::value>(m)); });
-  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
-  uint32_t w[2] = {0u, 0u};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) w[j >> 2] |= (uint32_t)(uint8_t)quantize_i8(v[j], inv) << (8 * (j & 3));
+  bf16x8_to_f32(*reinterpret_cast<const v4i*>(src + c * 8), v);
+  uint32_t w[2];
+  const float m = block_quant_lanes<LPB>(v, apply_fwht, fwht_scale, w);
   if (i < nchunks) {
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
     *reinterpret_cast<u2*>(xq + c * 8) = u2{w[0], w[1]};

@@ -324,8 +324,35 @@ int bq_moe_phase1_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* 
     return fail(BQ_ERR_INVALID, "bq_moe_phase1_gate_up: int8 operands must be 16-byte aligned");
   return check_hip(bq::launch_moe_phase1(x_i8, x_sa, expert_offset,
                                          reinterpret_cast<const bq::Route*>(routes), w_gate_up,
-                                         gate_up_scale, bucket, experts_per_rank, seq_len * top_k,
-                                         hidden, inter, S(stream)), "moe_phase1");
+                                         gate_up_scale, bucket, nullptr, nullptr,
+                                         experts_per_rank, seq_len * top_k, hidden, inter,
+                                         S(stream)), "moe_phase1");
+}
+
+int bq_moe_phase1_gate_up_quant(const int8_t* x_i8, const float* x_sa,
+                                const int32_t* expert_offset, const bq_route* routes,
+                                const int8_t* w_gate_up, const float* gate_up_scale,
+                                uint16_t* bucket, int8_t* bucket_i8, float* bucket_sa,
+                                int experts_per_rank, int seq_len, int top_k, int hidden,
+                                int inter, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !expert_offset || !routes || !w_gate_up || !gate_up_scale ||
+      !bucket_i8 || !bucket_sa)
+    return fail(BQ_ERR_INVALID, "bq_moe_phase1_gate_up_quant: null pointer");
+  if (experts_per_rank <= 0 || top_k <= 0 || hidden <= 0 || hidden % 64 || inter <= 0 ||
+      inter % 64)
+    return fail(BQ_ERR_SHAPE, "bq_moe_phase1_gate_up_quant: need hidden %% 64 == 0 and "
+                              "inter %% 64 == 0 (the 64-column block-quant)");
+  if (!a16(x_i8) || !a16(w_gate_up) || (reinterpret_cast<uintptr_t>(bucket_i8) & 7u) ||
+      (reinterpret_cast<uintptr_t>(bucket_sa) & 3u) || (bucket && !a16(bucket)))
+    return fail(BQ_ERR_INVALID, "bq_moe_phase1_gate_up_quant: x_i8, w_gate_up (and bucket) must "
+                                "be 16-byte, bucket_i8 8-byte, bucket_sa 4-byte aligned");
+  return check_hip(bq::launch_moe_phase1(x_i8, x_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_gate_up,
+                                         gate_up_scale, bucket, bucket_i8, bucket_sa,
+                                         experts_per_rank, seq_len * top_k, hidden, inter,
+                                         S(stream)),
+                   "moe_phase1_quant");
 }
 
 size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden) {

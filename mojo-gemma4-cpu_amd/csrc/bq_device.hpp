@@ -272,7 +272,55 @@ __device__ inline void fwht_wave(float (&v)[R], int block) {
   }
 }
 
-// Workgroup barrier for LDS producer/consumer hand-offs: waits for this
+// Block-quant of one block of B = 8*LPB values held 8 per lane by LPB
+// aligned lanes (lane i of the group owns values [8i, 8i+8)): bf16 values
+// widened to f32 in v, [FWHT(B): strides 1, 2, 4 inside the lane, 8 ... B/2
+// across lanes, ascending, then x fwht_scale], amax over the block, codes
+// q = rne(v * 127/amax) packed little-endian into w (bytes 8i .. 8i+7 of the
+// block).  Returns the amax (the block's activation scale).  The op order is
+// that of prepare_block_activation (butterquant/runtime.mojo:62-80).
+template <int LPB>
+__device__ inline float block_quant_lanes(float (&v)[8], bool apply_fwht, float fwht_scale,
+                                          uint32_t (&w)[2]) {
+  if (apply_fwht) {
+#pragma unroll
+    for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j & s) continue;
+        const float a = v[j], b = v[j + s];
+        v[j] = a + b;
+        v[j + s] = a - b;
+      }
+    for_each_xlane_stride(LPB, [&](auto st) {
+      constexpr int ST = decltype(st)::value;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = xlane_bfly<ST>(v[j]);
+    });
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * fwht_scale;
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+  for_each_xlane_stride(LPB, [&](auto st) { m = fmaxf(m, xlane_partner<decltype(st)::value>(m)); });
+  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+  w[0] = w[1] = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j >> 2] |= (uint32_t)(uint8_t)quantize_i8(v[j], inv) << (8 * (j & 3));
+  return m;
+}
+
+// 8 bf16 values (16 bytes) widened to f32
+__device__ inline void bf16x8_to_f32(v4i raw, float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float((uint32_t)raw[j] << 16);
+    v[2 * j + 1] = __uint_as_float((uint32_t)raw[j] & 0xFFFF0000u);
+  }
+}
+
+// Workgroup barrier for LDS producer/consumer hand-offs// Workgroup barrier for LDS producer/consumer hand-offs: waits for this
 // wave's LDS operations only.  (__syncthreads() also carries a release fence,
 // which on gfx9 waits for every outstanding global load -- it would drain the
 // global-load prefetch pipeline at each stage.)  Global loads land in private

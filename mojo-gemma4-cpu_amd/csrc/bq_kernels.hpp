@@ -76,8 +76,8 @@ struct Route { int32_t token; float weight; };
 hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStream_t st);
 hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
                                     const Route* routes, const int8_t* w_gu, const float* gu_scale,
-                                    uint16_t* bucket, int experts, int max_routes, int hidden,
-                                    int inter, int bm, hipStream_t st);
+                                    uint16_t* bucket, int8_t* bi8, float* bsa, int experts,
+                                    int max_routes, int hidden, int inter, int bm, hipStream_t st);
 hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const int32_t* eo,
                                  const Route* routes, const int8_t* w_d, const float* d_scale,
                                  float* y, int experts, int max_routes, int hidden, int inter,
@@ -123,10 +123,12 @@ hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, in
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);
+// bi8 / bsa non-null: the bucket's FWHT64 block-quant fused into the
+// epilogue (bucket may then be null); inter % 64 == 0 for that
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
                              const Route* routes, const int8_t* w_gu, const float* gu_scale,
-                             uint16_t* bucket, int experts, int max_routes, int hidden,
-                             int inter, hipStream_t st);
+                             uint16_t* bucket, int8_t* bi8, float* bsa, int experts,
+                             int max_routes, int hidden, int inter, hipStream_t st);
 size_t moe_phase2_workspace(int max_routes, int seq_len, int hidden);
 hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa,
                              const int32_t* expert_offset, const Route* routes,

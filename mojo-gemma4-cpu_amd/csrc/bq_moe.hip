@@ -180,18 +180,23 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
 // past K is skipped by a uniform test), and every epilogue operand is loaded
 // at kernel start.
 
-// Phase 1: blockIdx.y = m-tile, blockIdx.x = group of 4 intermediate subtiles.
+// Phase 1: blockIdx.y = m-tile, blockIdx.x = group of 4 intermediate subtiles
+// (64 columns).  With bi8 the workgroup's 16 x 64 bf16 bucket block goes
+// through LDS to the fused FWHT64 block-quant (inter % 64 == 0: no wave of
+// the group is idle).
 template <int U>
 __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
     const int8_t* __restrict__ x_i8, const float* __restrict__ x_sa,
     const int32_t* __restrict__ eo, const Route* __restrict__ routes,
     const int8_t* __restrict__ w_gu, const float* __restrict__ gu_scale,
-    uint16_t* __restrict__ bucket, int E, int hidden, int inter, int max_routes) {
+    uint16_t* __restrict__ bucket, int8_t* __restrict__ bi8, float* __restrict__ bsa,
+    float fwht64, int E, int hidden, int inter, int max_routes) {
+  __shared__ __attribute__((aligned(16))) uint16_t qtile[16 * 64];
   int e, r0, r1;
   if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
   const int isub = blockIdx.x * 4 + wave;
-  if (isub * 16 >= inter) return;
+  if (isub * 16 >= inter) return;  // never with bi8 (inter % 64 == 0)
   const int K = hidden, K64 = K >> 6;
   const size_t gate_up = (size_t)2 * inter;
   const int8_t* we = w_gu + (size_t)e * gate_up * K;
@@ -246,7 +251,26 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
     if (rec >= r1) continue;
     const float gv = (float)g4[v] * ad[v] * wsg;
     const float uv = (float)u4[v] * ad[v] * wsu;
-    bucket[(size_t)rec * inter + col] = f32_to_bf16(gelu_tanh_f32(gv) * uv);
+    const uint16_t hb = f32_to_bf16(gelu_tanh_f32(gv) * uv);
+    if (bi8) qtile[(rec - r0) * 64 + wave * 16 + (lane & 15)] = hb;
+    else bucket[(size_t)rec * inter + col] = hb;
+  }
+  if (!bi8) return;  // uniform
+  __syncthreads();
+  // 16 records x one 64-column block: 8 lanes per record (waves 0 and 1)
+  if (wave >= 2) return;
+  const int r = wave * 8 + (lane >> 3), i = lane & 7;
+  const v4i raw = *reinterpret_cast<const v4i*>(&qtile[r * 64 + i * 8]);
+  float v[8];
+  bf16x8_to_f32(raw, v);
+  uint32_t w[2];
+  const float m = block_quant_lanes<8>(v, true, fwht64, w);
+  if (r0 + r < r1) {
+    const size_t rec = (size_t)(r0 + r), c0 = (size_t)blockIdx.x * 64 + i * 8;
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(bi8 + rec * inter + c0) = u2{w[0], w[1]};
+    if (i == 0) bsa[rec * (inter / 64) + blockIdx.x] = m;
+    if (bucket) *reinterpret_cast<v4i*>(bucket + rec * inter + c0) = raw;
   }
 }
 
@@ -470,16 +494,18 @@ int moe_tile_bm(int max_routes, int experts) {
 
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
                              const Route* routes, const int8_t* w_gu, const float* gu_scale,
-                             uint16_t* bucket, int experts, int max_routes, int hidden,
-                             int inter, hipStream_t st) {
+                             uint16_t* bucket, int8_t* bi8, float* bsa, int experts,
+                             int max_routes, int hidden, int inter, hipStream_t st) {
   if (max_routes <= 0) return hipSuccess;
+  if (bi8 && inter % 64) return hipErrorInvalidValue;
   const int bm = moe_tile_bm(max_routes, experts);
   if (bm >= 64 && inter % 64 == 0)
-    return launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket, experts,
-                                    max_routes, hidden, inter, bm, st);
+    return launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket, bi8, bsa,
+                                    experts, max_routes, hidden, inter, bm, st);
   dim3 g((inter / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
   hipLaunchKernelGGL(k_moe_gate_up_skinny<4>, g, b, 0, st, x_i8, x_sa, eo, routes, w_gu,
-                     gu_scale, bucket, experts, hidden, inter, max_routes);
+                     gu_scale, bucket, bi8, bsa, fwht_scale_host(64), experts, hidden, inter,
+                     max_routes);
   return hipGetLastError();
 }
 

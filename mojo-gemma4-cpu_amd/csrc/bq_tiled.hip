@@ -32,7 +32,10 @@ struct TiledArgs {
   const Route* routes;
   const int8_t* w;          // expert weights, tile16x64, expert stride N*K
   const float* ws;          // per-row weight scales, expert stride N
-  uint16_t* bucket;         // GATE_UP output [routes, inter]
+  uint16_t* bucket;         // GATE_UP output [routes, inter] (or null with bi8)
+  int8_t* bi8;              // GATE_UP fused block-quant: [routes, inter] codes ...
+  float* bsa;               // ... and [routes, inter / 64] block scales (or null)
+  float fwht64;             // f32(1/f64(sqrtf(64)))
   float* y;                 // DOWN output [routes, N]
   int E, max_routes, N, K, inter, block;
   int gm, gn;               // grid decomposition: m-tiles, n-tiles
@@ -248,8 +251,14 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
       // else, so clobbering it is safe.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                   :: "s"(l), "v"(g) : "memory", "m0");
+      // weights are streamed once: non-temporal (measured 7.2 vs 6.0 TB/s
+      // for HBM-sourced DMA streams); activations are re-read by other tiles
+      if (is_a[d])
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                     :: "s"(l), "v"(g) : "memory", "m0");
+      else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                     :: "s"(l), "v"(g) : "memory", "m0");
 #pragma clang diagnostic pop
     }
   };
@@ -408,6 +417,14 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
   }
 
   // ---- epilogue ----------------------------------------------------------
+  // fused block-quant (GATE_UP with bi8): the tile's bf16 bucket values go to
+  // an LDS tile [BM][BN/2] over the A ring (free once every wave is done with
+  // the last stage), then whole 64-column blocks are block-quantized from it
+  [[maybe_unused]] uint16_t* qtile = reinterpret_cast<uint16_t*>(&abuf_all[0][0][0]);
+  if constexpr (MODE == MODE_GATE_UP) {
+    static_assert(BM * (BN / 2) * 2 <= NBUF * A_STAGE, "bucket tile fits the A ring");
+    if (args.bi8) lds_barrier();  // uniform
+  }
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
@@ -434,7 +451,9 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
           if (col >= args.inter) continue;
           const float g = (float)acc[mi][j][v] * ad * ep_col[j];
           const float u = (float)acc[mi][hn + j][v] * ad * ep_col[hn + j];
-          args.bucket[(size_t)row * args.inter + col] = f32_to_bf16(gelu_tanh_f32(g) * u);
+          const uint16_t hb = f32_to_bf16(gelu_tanh_f32(g) * u);
+          if (args.bi8) qtile[(row - r0) * (BN / 2) + (col - n0)] = hb;
+          else args.bucket[(size_t)row * args.inter + col] = hb;
         }
       } else {
         const float rw = ep_row[mi][v];
@@ -443,6 +462,31 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
           const int col = n0 + bsub[ni] * 16 + (lane & 15);
           if (col >= args.N) continue;
           args.y[(size_t)row * args.N + col] = facc[mi][ni][v] * ep_col[ni] * rw;
+        }
+      }
+    }
+  }
+  if constexpr (MODE == MODE_GATE_UP) {
+    if (args.bi8) {
+      // 8 lanes per (record, 64-column block), 8 values each, as bq_block_quant
+      lds_barrier();
+      const int live = r1 - r0, nblk = min(BN / 2, args.inter - n0) / 64;
+      const int units = live * nblk, nb_all = args.inter / 64;
+      for (int u0 = gwave * 8; u0 < units; u0 += NW * KSP * 8) {
+        const int uu = u0 + (lane >> 3);
+        const int u = min(uu, units - 1);  // groups past the end redo the last unit, unstored
+        const int r = u / nblk, b = u - r * nblk, i = lane & 7;
+        const v4i raw = *reinterpret_cast<const v4i*>(&qtile[r * (BN / 2) + b * 64 + i * 8]);
+        float v[8];
+        bf16x8_to_f32(raw, v);
+        uint32_t w[2];
+        const float m = block_quant_lanes<8>(v, true, args.fwht64, w);
+        if (uu < units) {
+          const size_t rec = (size_t)(r0 + r), col = (size_t)(n0 + b * 64 + i * 8);
+          typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u2*>(args.bi8 + rec * args.inter + col) = u2{w[0], w[1]};
+          if (i == 0) args.bsa[rec * nb_all + (n0 >> 6) + b] = m;
+          if (args.bucket) *reinterpret_cast<v4i*>(args.bucket + rec * args.inter + col) = raw;
         }
       }
     }
@@ -799,12 +843,13 @@ static inline int mtile_bound(int max_routes, int experts, int bm) {
 
 hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
                                     const Route* routes, const int8_t* w_gu,
-                                    const float* gu_scale, uint16_t* bucket, int experts,
-                                    int max_routes, int hidden, int inter, int bm,
-                                    hipStream_t st) {
+                                    const float* gu_scale, uint16_t* bucket, int8_t* bi8,
+                                    float* bsa, int experts, int max_routes, int hidden,
+                                    int inter, int bm, hipStream_t st) {
   TiledArgs t{};
   t.a = x_i8; t.a_scale = x_sa; t.eo = eo; t.routes = routes; t.w = w_gu; t.ws = gu_scale;
-  t.bucket = bucket; t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
+  t.bucket = bucket; t.bi8 = bi8; t.bsa = bsa; t.fwht64 = fwht_scale_host(64);
+  t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
   t.inter = inter; t.block = hidden;
   const int bmv = bm >= 256 ? 256 : bm >= 192 ? 192 : bm >= 128 ? 128 : 64;
   // weight rows per tile: bn/2 gate + bn/2 up.  256-record tiles pair with

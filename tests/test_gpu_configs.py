@@ -98,6 +98,9 @@ def test_moe_model_shape_batches(gpu, O, moe_model, T):
     rbq, rbsa = O.block_quant(rb, 64, True)
     np.testing.assert_array_equal(host(bi8), rbq)
     np.testing.assert_array_equal(host(bsa), rbsa)
+    fi8, fsa = gpu.moe_phase1_quant(xq, xsa, eo, routes, m["Wgu"], E, T, 8, I)
+    np.testing.assert_array_equal(host(fi8), rbq)
+    np.testing.assert_array_equal(host(fsa), rbsa)
     racc, rout = O.moe_phase2(rbq, rbsa, reo, rroutes, T, m["dp"], m["ds"], m["dcs"], H)
     np.testing.assert_array_equal(host(accum), racc)
     np.testing.assert_array_equal(host(out), rout)
@@ -128,6 +131,11 @@ def test_moe_prefill_full(gpu, O, moe_model):
     rbq, rbsa = O.cpu_block_quant(rb, 64, True, NCPU)
     np.testing.assert_array_equal(host(bi8), rbq)
     np.testing.assert_array_equal(host(bsa), rbsa)
+    # the fused phase 1 + block-quant (the benchmark's path) gives the same codes
+    print(f"moe prefill T={T}: fused phase 1 + block-quant", flush=True)
+    fi8, fsa = gpu.moe_phase1_quant(xq, xsa, eo, routes, m["Wgu"], E, T, 8, I)
+    np.testing.assert_array_equal(host(fi8), rbq)
+    np.testing.assert_array_equal(host(fsa), rbsa)
     racc, rout = O.cpu_moe_phase2(rbq, rbsa, reo, rroutes, T, m["dp"], m["ds"], m["dcs"], H, 64, NCPU)
     np.testing.assert_array_equal(host(accum), racc)
     np.testing.assert_array_equal(host(out), rout)

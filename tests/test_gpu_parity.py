@@ -330,6 +330,37 @@ def test_moe_golden(gpu, G):
     np.testing.assert_array_equal(host(out), G["moe_out"])
 
 
+@pytest.mark.parametrize("T,E,k,H,I", [(1, 4, 2, 1024, 128), (5, 8, 2, 768, 128),
+                                       (40, 8, 2, 1024, 192), (300, 4, 2, 1024, 128),
+                                       (600, 4, 2, 1024, 64), (129, 16, 4, 2816, 128),
+                                       (64, 8, 8, 2112, 128), (20, 4, 2, 512, 64)])
+def test_moe_phase1_quant(gpu, O, T, E, k, H, I):
+    """bq_moe_phase1_gate_up_quant = phase 1 then the FWHT64 block-quant of
+    its bucket (bit for bit), with and without the bf16 bucket: the skinny
+    16-record kernel (few routes per expert) and the LDS-tiled kernel (T =
+    300 / 600 over 4 experts: 150 / 300 records per expert, one and two
+    m-tiles), hidden a multiple of 128 or only of 64."""
+    import torch
+    idx, w = O.route_topk_softmax(O.synth_normal_f32(T + 3, 1.0, (T, E)), k)
+    gq, gs, Wgu = weight(gpu, O, E * 2 * I, H, 128 if H % 128 == 0 else 64, seed=9)
+    gp, gcs = O.pack_and_colsum(gq)
+    x = O.synth_normal_bf16(T, 1.0, (T, H))
+    xq, xsa = O.norm_quant(x, np.full(H, ONE, np.uint16), 128 if H % 128 == 0 else 64)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    rb = O.moe_phase1(xq, xsa, reo, rroutes, gp, gs, gcs, I)
+    rq, rsa = O.block_quant(rb, 64, True)
+    n = int(reo[-1])
+    bi8, bsa, bb = gpu.moe_phase1_quant(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I, bucket=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(bb)[:n], rb)
+    np.testing.assert_array_equal(host(bi8)[:n], rq)
+    np.testing.assert_array_equal(host(bsa)[:n], rsa)
+    bi8, bsa = gpu.moe_phase1_quant(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I)
+    np.testing.assert_array_equal(host(bi8)[:n], rq)
+    np.testing.assert_array_equal(host(bsa)[:n], rsa)
+
+
 def test_moe_duplicate_experts(gpu, O):
     """A token that lists an expert more than once (the router pads a token
     with fewer than top_k valid logits with expert 0, moe_router.mojo:266):
