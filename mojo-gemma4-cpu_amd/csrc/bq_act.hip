@@ -326,7 +326,146 @@ static void launch_nq_wave(dim3 g, size_t lds, hipStream_t st, const uint16_t* s
                      hidden, block, pu, sqrt_n, n_eps, sc);
 }
 
-// smallest instance holding nseg segments of R*64 values (hidden <= 4096)
+// Pair layout (hidden % 256 == 0, so the reference's sum of squares runs on
+// pu = 8 port-unrolled accumulators, i.e. 128 chains).  Lane L holds the
+// bf16 pair (128 q + 2 L, 128 q + 2 L + 1) of every 128-value segment q --
+// one coalesced 4-byte load per segment -- and with it exactly the pairs of
+// chains L (segments 0, 2, 4, ...) and L + 64 (segments 1, 3, 5, ...), in
+// chain order (rms_reduce_row: chain c takes pairs c, c + 128, c + 256, ...;
+// odd element first).  The FWHT of block B: stride 1 inside the pair,
+// strides 2 .. 64 across lanes (lane ^ s/2), strides 128 and 256 across
+// segments, ascending.
+//
+// A token takes WPT = ceil(nseg / SPW) waves: each loads the whole row and
+// computes the sum of squares (it is cheap, and it keeps the chain order),
+// then transforms and quantizes its own SPW segments; the row's amax is
+// exchanged through LDS (one barrier) when WPT > 1.  WPT = 1 runs four tokens
+// per workgroup without LDS or barriers.
+template <int NSEG, int SPW>
+__global__ __launch_bounds__(512) void k_norm_quant_pair(
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int T, int hidden, int block,
+    float sqrt_n, float n_eps, float fwht_scale) {
+  __shared__ float s_max[8];
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int nseg = hidden >> 7;
+  const int wpt = (nseg + SPW - 1) / SPW;  // waves per token
+  const bool one = SPW >= NSEG;            // one wave per token
+  const int t = one ? blockIdx.x * 4 + wave : blockIdx.x;
+  const int q0 = one ? 0 : wave * SPW;     // this wave's first segment
+  if (t >= T) return;                      // (one: whole waves, nothing synchronizes)
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(src + (size_t)t * hidden) + lane;
+  const uint32_t* gr = reinterpret_cast<const uint32_t*>(gamma) + lane;
+  uint32_t xp[NSEG], gp[SPW];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+    if (q < nseg) xp[q] = xr[64 * q];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i)
+    if (q0 + i < nseg) gp[i] = gr[64 * (q0 + i)];
+  // chains L (even segments) and L + 64 (odd segments)
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NSEG; q += 2) {
+    if (q >= nseg) break;
+    const float o0 = __uint_as_float(xp[q] & 0xFFFF0000u), e0 = __uint_as_float(xp[q] << 16);
+    const float o1 = __uint_as_float(xp[q + 1] & 0xFFFF0000u), e1 = __uint_as_float(xp[q + 1] << 16);
+    a0 = fmaf(o0, o0, a0);
+    a0 = fmaf(e0, e0, a0);
+    a1 = fmaf(o1, o1, a1);
+    a1 = fmaf(e1, e1, a1);
+  }
+  // s_j = sum over p of chain p*16 + j in p order, then the 16-lane halving tree
+  float sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int c = p * 16 + (lane & 15);
+    const float v0 = __shfl(a0, c & 63, kWave);
+    const float v1 = __shfl(a1, c & 63, kWave);
+    sum = sum + (c < 64 ? v0 : v1);
+  }
+#pragma unroll
+  for (int h = 8; h >= 1; h >>= 1) sum = sum + __shfl_down(sum, h, 16);
+  const float total = __shfl(sum, 0, kWave);
+  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+
+  float v[SPW][2];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int q = q0 + i;
+    uint32_t x = 0u;
+#pragma unroll
+    for (int k = 0; k < NSEG; ++k)  // static register index of segment q
+      if (k == q) x = xp[k];
+    if (q < nseg) {
+      const float e = __uint_as_float(x << 16), o = __uint_as_float(x & 0xFFFF0000u);
+      const float ge = __uint_as_float(gp[i] << 16), go = __uint_as_float(gp[i] & 0xFFFF0000u);
+      v[i][0] = e * inv_rms * ge;
+      v[i][1] = o * inv_rms * go;
+    } else {
+      v[i][0] = v[i][1] = 0.0f;
+    }
+  }
+  // stride 1 inside the pair
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const float x0 = v[i][0], x1 = v[i][1];
+    v[i][0] = x0 + x1;
+    v[i][1] = x0 - x1;
+  }
+  // strides 2 .. min(B/2, 64) across lanes: element bit k is lane bit k - 1
+  auto lanes = [&](auto st) {
+    constexpr int ST = decltype(st)::value;
+    if (block > 2 * ST) {
+#pragma unroll
+      for (int i = 0; i < SPW; ++i)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) v[i][r] = xlane_bfly<ST>(v[i][r]);
+    }
+  };
+  lanes(Stride<1>{}); lanes(Stride<2>{}); lanes(Stride<4>{});
+  lanes(Stride<8>{}); lanes(Stride<16>{}); lanes(Stride<32>{});
+  // strides 128 and 256 across segments (SPW and q0 are multiples of B/128)
+#pragma unroll
+  for (int ss = 1; ss <= 2; ss <<= 1) {
+    if (block <= 128 * ss) break;
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      if ((i & ss) || i + ss >= SPW) continue;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float x0 = v[i][r], x1 = v[i + ss][r];
+        v[i][r] = x0 + x1;
+        v[i + ss][r] = x0 - x1;
+      }
+    }
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      v[i][r] = v[i][r] * fwht_scale;
+      m = fmaxf(m, fabsf(v[i][r]));
+    }
+  float amax = wave_max(m);
+  if (!one) {
+    if (lane == 0) s_max[wave] = amax;
+    __syncthreads();
+    amax = s_max[0];
+    for (int w = 1; w < wpt; ++w) amax = fmaxf(amax, s_max[w]);
+  }
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  uint16_t* qrow = reinterpret_cast<uint16_t*>(xq + (size_t)t * hidden) + lane;
+#pragma unroll
+  for (int i = 0; i < SPW; ++i)
+    if (q0 + i < nseg)
+      qrow[64 * (q0 + i)] = (uint16_t)((uint8_t)quantize_i8(v[i][0], inv) |
+                                       ((uint16_t)(uint8_t)quantize_i8(v[i][1], inv) << 8));
+  if (lane == 0 && wave == (one ? wave : 0)) sa[t] = amax;
+}
+
+// smallest instance holding nseg segments of R*64 values (hidden <= 4096)// smallest instance holding nseg segments of R*64 values (hidden <= 4096)
 static bool launch_norm_quant_wave(int R, int nseg, const uint16_t* src, const uint16_t* gamma,
                                    int8_t* xq, float* sa, int T, int hidden, int block, int pu,
                                    float sqrt_n, float n_eps, float sc, hipStream_t st) {
@@ -384,6 +523,28 @@ hipError_t launch_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t*
   const int nseg = hidden / (R * 64);
   constexpr int MAXSEG = 4;
   const int waves = (nseg + MAXSEG - 1) / MAXSEG;
+  // pair-layout wave per token: hidden % 256 == 0 (128 sum-of-squares
+  // chains), up to 4096 values, 2-byte aligned codes
+  if (pu == 8 && hidden <= 4096 && tune().nq_pair && !(reinterpret_cast<uintptr_t>(xq) & 1u)) {
+    const int ns = hidden >> 7;
+    // many tokens: one wave each (4 per workgroup); few: a token over up to
+    // 8 waves of SPW segments (a multiple of B/128 segments: whole blocks)
+    if (seq_len >= 256) {
+      const dim3 g((seq_len + 3) / 4), b(256);
+#define BQ_NQP(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_quant_pair<N, N>), g, b, 0, st, src, gamma, xq, sa, seq_len, hidden, block, sqrt_n, n_eps, sc); return hipGetLastError(); }
+      BQ_NQP(4) BQ_NQP(8) BQ_NQP(12) BQ_NQP(16) BQ_NQP(22) BQ_NQP(24) BQ_NQP(32)
+#undef BQ_NQP
+    } else {
+      const int unit = block > 128 ? block / 128 : 1;
+      int spw = (ns + 7) / 8;
+      spw = (spw + unit - 1) / unit * unit;
+      const dim3 g(seq_len), b(64 * ((ns + spw - 1) / spw));
+#define BQ_NQP(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_quant_pair<N, S>), g, b, 0, st, src, gamma, xq, sa, seq_len, hidden, block, sqrt_n, n_eps, sc); return hipGetLastError(); }
+      BQ_NQP(8, 1) BQ_NQP(8, 2) BQ_NQP(8, 4) BQ_NQP(16, 2) BQ_NQP(16, 4)
+      BQ_NQP(24, 3) BQ_NQP(24, 4) BQ_NQP(32, 4)
+#undef BQ_NQP
+    }
+  }
   // one wave per token from 1792 tokens (hidden 2816: 13.6 vs 12.8 us at
   // 1536 tokens for the workgroup-per-row kernel, 14.3 vs 15.6 us at 2048)
   if (seq_len >= 1792 && hidden <= 4096 &&

@@ -94,6 +94,7 @@ void tune_init(int device) {
   t.moe_bm_down = env_int("BQ_MOE_BM_DOWN");
   t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 2;
   t.down_breg = getenv("BQ_DOWN_BREG") ? env_int("BQ_DOWN_BREG") : 1;
+  t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
       cus <= 0)

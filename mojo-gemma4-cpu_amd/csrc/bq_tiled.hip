@@ -573,7 +573,8 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
     const uint64_t ob = (uint64_t)(wb - args.w) + ((uint64_t)ns * K64 + min(ks, K64 - 1)) * 1024u;
     const uint64_t ou = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ob >> 32)) << 32) |
                         __builtin_amdgcn_readfirstlane((uint32_t)ob);
-    return *reinterpret_cast<const v4i*>(args.w + ou + lane16);
+    // streamed once: non-temporal
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(args.w + ou + lane16));
   };
 
   // ---- the first item's weights ------------------------------------------

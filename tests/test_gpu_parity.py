@@ -114,8 +114,11 @@ def test_quantize_weight_golden(gpu, G):
 
 # ---------------------------------------------------------------- activations
 @pytest.mark.parametrize("H,B", [(2816, 128), (4096, 128), (2112, 64), (512, 16), (4096, 512),
-                                 (1024, 32), (8192, 256)])
+                                 (1024, 32), (8192, 256), (2048, 512), (2048, 128), (3072, 256),
+                                 (3072, 128), (1024, 512), (256, 128), (2304, 256), (3584, 64)])
 def test_norm_quant(gpu, O, H, B):
+    # few tokens: a token's segments spread over up to 8 waves (whole FWHT
+    # blocks per wave, 1 to 4 segments of 128 values each)
     x = O.synth_normal_bf16(1, 1.0, (5, H))
     g = O.f32_to_bf16(O.synth_normal_f32(9, 0.3, (H,)) + 1.0)
     q, sa = gpu.norm_quant(dev(x), dev(g), B)
