@@ -95,6 +95,10 @@ void tune_init(int device) {
   t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 2;
   t.down_breg = getenv("BQ_DOWN_BREG") ? env_int("BQ_DOWN_BREG") : 1;
   t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
+  // 16x16x64 by default: these LDS-ring kernels wait on their operand
+  // stream, not on the MFMA rate (gate/up at 2048 tokens: 142 us with
+  // 16x16x64 on 8-wave workgroups, 158 us with 32x32x32 on 4-wave ones)
+  t.mf = env_int("BQ_MF") == 32 ? 32 : 16;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
       cus <= 0)

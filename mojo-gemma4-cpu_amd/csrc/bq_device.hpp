@@ -20,6 +20,7 @@
 namespace bq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 constexpr float kInv127 = 1.0f / 127.0f;
@@ -366,6 +367,15 @@ __device__ inline float wave_row_ssq(const uint32_t* __restrict__ pairs, int hid
 
 __device__ inline v4i mfma16x16x64(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// 32x32 output, 32 of K: A lane L = row L%32, K bytes 16*(L/32)..+16; B lane
+// L = column L%32, the same K bytes; D lane L register j = row
+// 8*(j/4) + 4*(L/32) + j%4, column L%32.  Twice the 16x16x64 product's work
+// in twice its cycles: the int8 peak rate (the 16x16x64 form reaches ~3.9
+// POPS with 16 independent chains per wave; this one ~4.8 with 4).
+__device__ inline v16i mfma32x32x32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
 // Map a global m-tile index (BM records per tile, tiles of consecutive

@@ -19,12 +19,24 @@
 
 namespace bq {
 
-__device__ inline const LinSeg& pick_seg(const LinArgs& a, int nt_global, int& nt_local) {
-  int s = 0;
-  if (a.nseg > 1 && nt_global >= a.seg[1].tile0) s = 1;
-  if (a.nseg > 2 && nt_global >= a.seg[2].tile0) s = 2;
-  nt_local = nt_global - a.seg[s].tile0;
-  return a.seg[s];
+// The segment of global n-tile nt_global, selected by value: the fields of
+// all three segments are read in one batch of scalar loads, so the first
+// weight load waits for one kernel-argument round trip.  (Indexing a.seg[s]
+// by address makes the compiler load nseg and the boundaries first and the
+// chosen segment's fields after them: two dependent round trips.)
+__device__ inline LinSeg pick_seg(const LinArgs& a, int nt_global, int& nt_local) {
+  const LinSeg s0 = a.seg[0], s1 = a.seg[1], s2 = a.seg[2];
+  const bool in1 = a.nseg > 1 && nt_global >= s1.tile0;
+  const bool in2 = a.nseg > 2 && nt_global >= s2.tile0;
+  LinSeg r;
+  r.w = in2 ? s2.w : in1 ? s1.w : s0.w;
+  r.ws = in2 ? s2.ws : in1 ? s1.ws : s0.ws;
+  r.out = in2 ? s2.out : in1 ? s1.out : s0.out;
+  r.out_f32 = in2 ? s2.out_f32 : in1 ? s1.out_f32 : s0.out_f32;
+  r.n = in2 ? s2.n : in1 ? s1.n : s0.n;
+  r.tile0 = in2 ? s2.tile0 : in1 ? s1.tile0 : s0.tile0;
+  nt_local = nt_global - r.tile0;
+  return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -34,7 +46,7 @@ template <int WAVES, bool PER_BLOCK, int U>
 __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
   extern __shared__ int lds[];  // per-row: WAVES*256 ints; per-block: nb*256 ints
   int nt;
-  const LinSeg& seg = pick_seg(args, blockIdx.x, nt);
+  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
   const int K = args.K, K64 = K >> 6, M = args.M;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fpb = args.block >> 6;  // fragments per K block (power of two)

@@ -23,6 +23,7 @@ struct Tune {
   int moe_order;    // BQ_MOE_ORDER: MoE work order of the LDS-ring kernels (0, 1, 2)
   int down_breg;    // BQ_DOWN_BREG: 0 disables the register-streamed down kernel
   int nq_pair;      // BQ_NQ_PAIR: 0 disables the pair-layout norm-quant
+  int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
   int cus;          // compute units of the device
 };
 const Tune& tune();

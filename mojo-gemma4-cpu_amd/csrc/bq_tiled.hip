@@ -16,6 +16,8 @@
 // MFMA fragment (lane L's 16 bytes land at L*16): A fragments gather 16 rows
 // x 64 K of the activation, B fragments are contiguous 1 KiB runs of the
 // tile16x64 weight layout.
+#include <type_traits>
+
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 
@@ -90,13 +92,20 @@ __device__ inline uint32_t lds_addr(const int8_t* p) {
 // first's through LDS before the epilogue.  Twice the waves and bytes in
 // flight per CU for the same tile, so one group computes while the other
 // waits for its operands.
-template <int MODE, int BM, int BN, int WM, int WN, bool PER_BLOCK, int NBUF, int KSP = 1>
+template <int MODE, int BM, int BN, int WM, int WN, bool PER_BLOCK, int NBUF, int KSP = 1,
+          int MF = 16>
 __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
   static_assert(KSP == 1 || (KSP == 2 && MODE == MODE_DENSE && !PER_BLOCK), "split-K: dense per-row");
+  static_assert(MF == 16 || MF == 32, "MFMA tile: 16x16x64 or 32x32x32");
   constexpr int KS = 2;                                     // k-steps per stage
   constexpr int NW = WM * WN, NT = 64 * NW * KSP;           // waves per K group, threads
-  constexpr int MI = BM / (16 * WM), NI = BN / (16 * WN);   // 16x16 tiles per wave
-  static_assert(MI >= 1 && NI >= 1 && (MODE != MODE_GATE_UP || NI % 2 == 0), "tile shape");
+  constexpr int MI = BM / (MF * WM), NI = BN / (MF * WN);   // MF x MF tiles per wave
+  constexpr int EV = MF * MF / 64;                          // accumulator elements per lane
+  constexpr int KH = MF == 32 ? 2 : 1;                      // MFMAs per tile and k-step of 64
+  constexpr int SPT = MF / 16;                              // 16-row weight strips per tile
+  using acc_t = std::conditional_t<MF == 32, v16i, v4i>;
+  static_assert(MI >= 1 && NI >= 1 && MI * MF * WM == BM && NI * MF * WN == BN &&
+                (MODE != MODE_GATE_UP || NI % 2 == 0), "tile shape");
   constexpr int FA = BM / 8, FB = (BN / 16) * KS;           // 1 KiB DMAs per stage
   constexpr int D = (FA + FB + NW - 1) / NW;                // DMAs per wave per stage
   constexpr int REM = (FA + FB) % NW;  // when nonzero, waves >= REM issue D - 1
@@ -117,24 +126,32 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
   auto& abuf_ = abuf_all[kg];
   auto& bbuf_ = bbuf_all[kg];
   const bool full_d = REM == 0 || wave < REM;  // wave-uniform
-  const v4i zero = {0, 0, 0, 0};
 
   // ---- work item -------------------------------------------------------
   int K, n0 = 0, r0 = 0, r1 = 0, e = 0;
-  const LinSeg* seg = nullptr;
+  LinSeg segv{};
+  const LinSeg* seg = &segv;
   const int8_t* wbase;
   if constexpr (MODE == MODE_DENSE) {
     const int total = args.gm * args.gn;
     int work = blockIdx.x;
     if ((total & 7) == 0) work = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
     const int mt = work % args.gm;
-    int nt_in = work / args.gm, s = 0;
-    for (int q = 0; q < args.lin.nseg; ++q) {
-      const int tiles = (args.lin.seg[q].n + BN - 1) / BN;
-      if (nt_in < tiles) { s = q; break; }
-      nt_in -= tiles;
-    }
-    seg = &args.lin.seg[s];
+    int nt_in = work / args.gm;
+    // the segment selected by value: the three segments' fields are read in
+    // one batch of scalar loads (indexing seg[s] by address would take a
+    // second, dependent kernel-argument round trip)
+    const LinSeg s0 = args.lin.seg[0], s1 = args.lin.seg[1], s2 = args.lin.seg[2];
+    const int t0 = (s0.n + BN - 1) / BN, t1 = (s1.n + BN - 1) / BN;
+    const bool in1 = args.lin.nseg > 1 && nt_in >= t0;
+    const bool in2 = args.lin.nseg > 2 && nt_in >= t0 + t1;
+    nt_in -= in2 ? t0 + t1 : in1 ? t0 : 0;
+    segv.w = in2 ? s2.w : in1 ? s1.w : s0.w;
+    segv.ws = in2 ? s2.ws : in1 ? s1.ws : s0.ws;
+    segv.out = in2 ? s2.out : in1 ? s1.out : s0.out;
+    segv.out_f32 = in2 ? s2.out_f32 : in1 ? s1.out_f32 : s0.out_f32;
+    segv.n = in2 ? s2.n : in1 ? s1.n : s0.n;
+    segv.tile0 = in2 ? s2.tile0 : in1 ? s1.tile0 : s0.tile0;
     K = args.lin.K;
     r0 = mt * BM;
     r1 = min(args.lin.M, r0 + BM);
@@ -263,73 +280,104 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
     }
   };
 
-  int bsub[NI];
+  // first 16-row weight strip (of the stage's BN/16) of this wave's tile ni;
+  // a 32-wide tile spans strips bstrip and bstrip + 1
+  int bstrip[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     if constexpr (MODE == MODE_GATE_UP) {
-      const int half = BN / 32, hn = NI / 2;  // gate subtiles [0, half), up [half, 2*half)
-      bsub[ni] = ni < hn ? wn * hn + ni : half + wn * hn + (ni - hn);
+      const int half = BN / (2 * MF), hn = NI / 2;  // gate tiles [0, half), up [half, 2*half)
+      bstrip[ni] = (ni < hn ? wn * hn + ni : half + wn * hn + (ni - hn)) * SPT;
     } else {
-      bsub[ni] = wn * NI + ni;
+      bstrip[ni] = (wn * NI + ni) * SPT;
     }
   }
+  // accumulator element v of tile (mi, .): row within the block tile; the
+  // lane's column within tile ni is bstrip[ni] * 16 + (lane & (MF - 1))
+  auto row_in = [&](int mi, int v) {
+    if constexpr (MF == 16) return (wm * MI + mi) * 16 + 4 * (lane >> 4) + v;
+    else return (wm * MI + mi) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+  };
+  const int lcol = lane & (MF - 1);
 
   // ---- epilogue operands, fetched now so their (dependent) loads are long
   // done at the epilogue: per output row an activation scale (x 1/127) or a
-  // route weight, per output column the weight scale
-  float ep_row[MI][4], ep_col[NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      int row = r0 + (wm * MI + mi) * 16 + 4 * (lane >> 4) + v;
-      row = row < r1 ? row : r0;
-      if constexpr (MODE == MODE_DENSE) ep_row[mi][v] = PER_BLOCK ? 0.0f : args.lin.sa[row] * kInv127;
-      else if constexpr (MODE == MODE_GATE_UP) ep_row[mi][v] = args.a_scale[args.routes[row].token] * kInv127;
-      else ep_row[mi][v] = args.routes[row].weight;
-    }
+  // route weight -- thread t holds row t's, staged through LDS for the
+  // epilogue -- and per output column the weight scale
+  static_assert(NT >= BM, "one thread per tile row");
+  float my_rs = 0.0f;
+  if (tid < BM) {
+    int row = r0 + tid;
+    row = row < r1 ? row : r0;
+    if constexpr (MODE == MODE_DENSE) my_rs = PER_BLOCK ? 0.0f : args.lin.sa[row] * kInv127;
+    else if constexpr (MODE == MODE_GATE_UP) my_rs = args.a_scale[args.routes[row].token] * kInv127;
+    else my_rs = args.routes[row].weight;
+  }
+  float ep_col[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     if constexpr (MODE == MODE_GATE_UP) {
       constexpr int hn = NI / 2;
-      const int col = min(n0 + (wn * hn + (ni % hn)) * 16 + (lane & 15), args.inter - 1);
+      const int col = min(n0 + (wn * hn + (ni % hn)) * MF + lcol, args.inter - 1);
       ep_col[ni] = args.ws[(size_t)e * args.N + (ni < hn ? col : args.inter + col)];
     } else if constexpr (MODE == MODE_DENSE) {
-      ep_col[ni] = seg->ws[min(n0 + bsub[ni] * 16 + (lane & 15), seg->n - 1)];
+      ep_col[ni] = seg->ws[min(n0 + bstrip[ni] * 16 + lcol, seg->n - 1)];
     } else {
-      ep_col[ni] = args.ws[(size_t)e * args.N + min(n0 + bsub[ni] * 16 + (lane & 15), args.N - 1)];
+      ep_col[ni] = args.ws[(size_t)e * args.N + min(n0 + bstrip[ni] * 16 + lcol, args.N - 1)];
     }
   }
 
-  v4i acc[MI][NI];
-  float facc[MI][NI][4];
+  acc_t acc[MI][NI];
+  float facc[MI][NI][EV];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      acc[mi][ni] = zero;
+      acc[mi][ni] = acc_t{};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) facc[mi][ni][v] = 0.0f;
+      for (int v = 0; v < EV; ++v) facc[mi][ni][v] = 0.0f;
     }
 
-  auto row_of = [&](int mi, int v) { return r0 + (wm * MI + mi) * 16 + 4 * (lane >> 4) + v; };
+  auto row_of = [&](int mi, int v) { return r0 + row_in(mi, v); };
 
-  // LDS offset of this lane's A operand (row m = (wm*MI+mi)*16 + lane%16,
-  // chunk ks*4 + lane/16) under the block swizzle
-  int a_off[MI][KS];
+  // LDS offset of this lane's A operand under the block swizzle: row
+  // m = (wm*MI+mi)*MF + lane%MF, 16-byte chunk ks*4 + lane/16 (16x16x64) or
+  // ks*4 + kh*2 + lane/32 (32x32x32, K half kh).  The swizzle term depends
+  // on the lane only (m & 7 and (m >> 3) & 1 do not change with mi), so tile
+  // mi adds the constant mi * MF * 128.
+  int a_off[KS][KH];
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
+  for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int m = (wm * MI + mi) * 16 + (lane & 15);
-      const int b = m >> 3, r = m & 7, c = ks * 4 + (lane >> 4);
-      a_off[mi][ks] = b * 1024 + r * 128 + ((c ^ r ^ (b & 1)) * 16);
+    for (int kh = 0; kh < KH; ++kh) {
+      const int m = wm * MI * MF + (lane & (MF - 1));
+      const int c = MF == 16 ? ks * 4 + (lane >> 4) : ks * 4 + kh * 2 + (lane >> 5);
+      const int b = m >> 3, r = m & 7;
+      a_off[ks][kh] = b * 1024 + r * 128 + ((c ^ r ^ (b & 1)) * 16);
+    }
+  // LDS offset (within the stage's B buffer, less ks * 1024) of this lane's B
+  // operand of tile ni: 16x16x64 lane L = tile16x64 fragment lane L of strip
+  // bstrip; 32x32x32 half kh: column L%32 (strip bstrip + (L/16)%2), K chunk
+  // 2*kh + L/32 of the fragment
+  int b_off[NI][KH];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh) {
+      if constexpr (MF == 16) {
+        b_off[ni][kh] = bstrip[ni] * 2048 + lane * 16;
+      } else {
+        const int strip = bstrip[ni] + ((lane >> 4) & 1);
+        b_off[ni][kh] = strip * 2048 + ((kh * 2 + (lane >> 5)) * 16 + (lane & 15)) * 16;
+      }
     }
 
-  // A wave whose 16*MI rows all lie past the tile's last record (a partial
+  // A wave whose MF*MI rows all lie past the tile's last record (a partial
   // m-tile of an expert with few records) still issues its DMAs and meets
   // every barrier, but skips its MFMAs: nothing it would compute is stored.
-  const bool busy = wm * MI * 16 < r1 - r0;
+  // Within a busy wave, tiles mi whose rows all lie past it are skipped too.
+  const int live = r1 - r0;
+  const bool busy = wm * MI * MF < live;
 
   auto compute = [&](const int8_t* abuf, const int8_t* bbuf, int st) {
     if constexpr (MODE != MODE_DENSE) {
@@ -338,17 +386,25 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == 1 && odd && st == tail) break;
-      v4i a[MI], b[NI];
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-        a[mi] = *reinterpret_cast<const v4i*>(&abuf[a_off[mi][ks]]);
+      for (int kh = 0; kh < KH; ++kh) {
+        v4i a[MI], b[NI];
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        b[ni] = *reinterpret_cast<const v4i*>(&bbuf[(bsub[ni] * 2 + ks) * 1024 + lane * 16]);
+        for (int mi = 0; mi < MI; ++mi)
+          a[mi] = *reinterpret_cast<const v4i*>(&abuf[a_off[ks][kh] + mi * MF * 128]);
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
+        for (int ni = 0; ni < NI; ++ni)
+          b[ni] = *reinterpret_cast<const v4i*>(&bbuf[b_off[ni][kh] + ks * 1024]);
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma16x16x64(a[mi], b[ni], acc[mi][ni]);
+        for (int mi = 0; mi < MI; ++mi) {
+          if (MI > 1 && (wm * MI + mi) * MF >= live) continue;  // wave-uniform
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni) {
+            if constexpr (MF == 16) acc[mi][ni] = mfma16x16x64(a[mi], b[ni], acc[mi][ni]);
+            else acc[mi][ni] = mfma32x32x32(a[mi], b[ni], acc[mi][ni]);
+          }
+        }
+      }
       if constexpr (PER_BLOCK) {
         const int kt = st * KS + ks;
         if (((kt + 1) & (fpb - 1)) == 0) {
@@ -356,15 +412,14 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
 #pragma unroll
           for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int m = (wm * MI + mi) * 16 + 4 * (lane >> 4) + v;
-              const float adv = lds_sa[m * nb + b_idx];
+            for (int v = 0; v < EV; ++v) {
+              const float adv = lds_sa[row_in(mi, v) * nb + b_idx];
 #pragma unroll
               for (int ni = 0; ni < NI; ++ni)
                 facc[mi][ni][v] = fmaf((float)acc[mi][ni][v], adv, facc[mi][ni][v]);
             }
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = zero;
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = acc_t{};
           }
         }
       }
@@ -396,16 +451,25 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
       if (sl < n_loc) compute(abuf_[i], bbuf_[i], s_lo + sl);
     }
   }
+  // the row scales into the first B ring (free once every wave is done with
+  // the last stage; the split-K partials use the second group's ring)
+  float* s_rs = reinterpret_cast<float*>(&bbuf_all[0][0][0]);
+  if constexpr (KSP == 1) {
+    lds_barrier();
+    if (tid < BM) s_rs[tid] = my_rs;
+    lds_barrier();
+  }
   if constexpr (KSP == 2) {
     // the second group's accumulators into its B ring, added by the first
     int* part = reinterpret_cast<int*>(&bbuf_all[1][0][0]);
     lds_barrier();
+    if (tid < BM) s_rs[tid] = my_rs;
     if (kg == 1) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
-          *reinterpret_cast<v4i*>(&part[(((wave * MI + mi) * NI + ni) * 64 + lane) * 4]) = acc[mi][ni];
+          *reinterpret_cast<acc_t*>(&part[(((wave * MI + mi) * NI + ni) * 64 + lane) * EV]) = acc[mi][ni];
     }
     lds_barrier();
     if (kg == 1) return;
@@ -413,7 +477,7 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] += *reinterpret_cast<const v4i*>(&part[(((wave * MI + mi) * NI + ni) * 64 + lane) * 4]);
+        acc[mi][ni] += *reinterpret_cast<const acc_t*>(&part[(((wave * MI + mi) * NI + ni) * 64 + lane) * EV]);
   }
 
   // ---- epilogue ----------------------------------------------------------
@@ -423,19 +487,18 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
   [[maybe_unused]] uint16_t* qtile = reinterpret_cast<uint16_t*>(&abuf_all[0][0][0]);
   if constexpr (MODE == MODE_GATE_UP) {
     static_assert(BM * (BN / 2) * 2 <= NBUF * A_STAGE, "bucket tile fits the A ring");
-    if (args.bi8) lds_barrier();  // uniform
   }
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < EV; ++v) {
       const int row = row_of(mi, v);
       if (row >= r1) continue;
       if constexpr (MODE == MODE_DENSE) {
-        const float ad = ep_row[mi][v];
+        const float ad = s_rs[row - r0];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
-          const int col = n0 + bsub[ni] * 16 + (lane & 15);
+          const int col = n0 + bstrip[ni] * 16 + lcol;
           if (col >= seg->n) continue;
           const float y = PER_BLOCK ? facc[mi][ni][v] * ep_col[ni]
                                     : (float)acc[mi][ni][v] * ad * ep_col[ni];
@@ -443,11 +506,11 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
           if (seg->out_f32) seg->out_f32[(size_t)row * seg->n + col] = y;
         }
       } else if constexpr (MODE == MODE_GATE_UP) {
-        const float ad = ep_row[mi][v];
+        const float ad = s_rs[row - r0];
         constexpr int hn = NI / 2;
 #pragma unroll
         for (int j = 0; j < hn; ++j) {
-          const int col = n0 + (wn * hn + j) * 16 + (lane & 15);
+          const int col = n0 + (wn * hn + j) * MF + lcol;
           if (col >= args.inter) continue;
           const float g = (float)acc[mi][j][v] * ad * ep_col[j];
           const float u = (float)acc[mi][hn + j][v] * ad * ep_col[hn + j];
@@ -456,10 +519,10 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
           else args.bucket[(size_t)row * args.inter + col] = hb;
         }
       } else {
-        const float rw = ep_row[mi][v];
+        const float rw = s_rs[row - r0];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
-          const int col = n0 + bsub[ni] * 16 + (lane & 15);
+          const int col = n0 + bstrip[ni] * 16 + lcol;
           if (col >= args.N) continue;
           args.y[(size_t)row * args.N + col] = facc[mi][ni][v] * ep_col[ni] * rw;
         }
@@ -744,15 +807,15 @@ static inline int or_default(int v, int dflt) { return v ? v : dflt; }
 
 constexpr size_t kLdsBytes = 160 * 1024;
 
-template <int MODE, int BM, int BN, int WM, int WN, bool PB, int NBUF, int KSP = 1>
+template <int MODE, int BM, int BN, int WM, int WN, bool PB, int NBUF, int KSP = 1, int MF = 16>
 static bool try_launch(dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
   constexpr size_t ring = (size_t)KSP * NBUF * (BM + BN) * 128;  // 128 bytes of K per stage
   if constexpr (ring > kLdsBytes) {
     return false;  // never instantiated: the ring alone exceeds LDS
   } else {
     if (ring + dyn > kLdsBytes) return false;
-    hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, NBUF, KSP>), g, dim3(64 * WM * WN * KSP),
-                       dyn, st, t);
+    hipLaunchKernelGGL((k_tiled<MODE, BM, BN, WM, WN, PB, NBUF, KSP, MF>), g,
+                       dim3(64 * WM * WN * KSP), dyn, st, t);
     return true;
   }
 }
@@ -760,48 +823,60 @@ static bool try_launch(dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
 // NBUF-stage ring: the largest of {6, 4, 3, 2} stages (at most `nbuf`) that
 // fits in LDS next to the per-block scales.  The bytes in flight per CU
 // ((NBUF-1) stages) must cover the L2/HBM latency at the MFMA's pace.
-template <int MODE, int BM, int BN, int WM, int WN, bool PB>
+template <int MODE, int BM, int BN, int WM, int WN, bool PB, int MF>
 static void launch_cfg(int nbuf, dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
-  if (nbuf >= 6 && try_launch<MODE, BM, BN, WM, WN, PB, 6>(g, dyn, st, t)) return;
-  if (nbuf >= 4 && try_launch<MODE, BM, BN, WM, WN, PB, 4>(g, dyn, st, t)) return;
-  if (nbuf >= 3 && try_launch<MODE, BM, BN, WM, WN, PB, 3>(g, dyn, st, t)) return;
-  try_launch<MODE, BM, BN, WM, WN, PB, 2>(g, dyn, st, t);
+  if (nbuf >= 6 && try_launch<MODE, BM, BN, WM, WN, PB, 6, 1, MF>(g, dyn, st, t)) return;
+  if (nbuf >= 4 && try_launch<MODE, BM, BN, WM, WN, PB, 4, 1, MF>(g, dyn, st, t)) return;
+  if (nbuf >= 3 && try_launch<MODE, BM, BN, WM, WN, PB, 3, 1, MF>(g, dyn, st, t)) return;
+  try_launch<MODE, BM, BN, WM, WN, PB, 2, 1, MF>(g, dyn, st, t);
 }
 
-// 8 waves (2 x 4) per workgroup for 128/256-wide tiles: each wave owns a
-// (BM/2) x (BN/4) block; two waves per SIMD keep MFMA and LDS reads
-// overlapped (one wave per SIMD leaves every latency exposed).
-template <int MODE, int BM, bool PB>
+// 128/256-wide tiles: 16x16x64 tiles on 8 waves (2 x 4), each owning a
+// (BM/2) x (BN/4) block -- two waves per SIMD keep MFMA and LDS reads
+// overlapped; 32x32x32 tiles on 4 waves (2 x 2) of (BM/2) x (BN/2), whose
+// larger blocks halve the LDS operand reads per product, with two or more
+// workgroups per CU for the overlap.
+template <int MODE, int BM, bool PB, int MF>
 static void launch_bn(int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st, const TiledArgs& t) {
-  if (bn >= 256) launch_cfg<MODE, BM, 256, 2, 4, PB>(nbuf, g, dyn, st, t);
-  else launch_cfg<MODE, BM, 128, 2, 4, PB>(nbuf, g, dyn, st, t);
+  constexpr int WN = MF == 32 ? 2 : 4;
+  if (bn >= 256) launch_cfg<MODE, BM, 256, 2, WN, PB, MF>(nbuf, g, dyn, st, t);
+  else launch_cfg<MODE, BM, 128, 2, WN, PB, MF>(nbuf, g, dyn, st, t);
 }
 
-template <int MODE, bool PB>
-static void launch_bm(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st,
-                      const TiledArgs& t) {
+template <int MODE, bool PB, int MF>
+static void launch_bm_mf(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st,
+                         const TiledArgs& t) {
   // 256-record m-tiles (MoE): 4 x 2 waves of 64 x 64, one tile per expert for
   // up to 256 routes, so each expert's weights stream from HBM once
   if (bm >= 256) {
     // 256 x 256 (4 x 2 waves of 64 x 128) halves the operand traffic again;
     // the per-block drains' f32 accumulators would not fit next to it
     if constexpr (!PB) {
-      if (bn >= 256) { launch_cfg<MODE, 256, 256, 4, 2, PB>(nbuf, g, dyn, st, t); return; }
+      if (bn >= 256) { launch_cfg<MODE, 256, 256, 4, 2, PB, MF>(nbuf, g, dyn, st, t); return; }
     }
-    launch_cfg<MODE, 256, 128, 4, 2, PB>(nbuf, g, dyn, st, t);
+    launch_cfg<MODE, 256, 128, 4, 2, PB, MF>(nbuf, g, dyn, st, t);
   }
   else if (bm >= 192) {
-    // 192-record m-tiles (4 x 2 waves of 48 x 64 or 48 x 128): one tile per
-    // expert at ~128 routes per expert with two thirds of the rows live,
-    // where 256-record tiles carry half of them empty
+    // 192-record m-tiles: one tile per expert at ~128 routes per expert with
+    // two thirds of the rows live, where 256-record tiles carry half of them
+    // empty.  16x16x64: 4 x 2 waves of 48 x 64 (or 48 x 128); 32x32x32: 2 x 2
+    // waves of 96 x 64 (or 96 x 128)
+    constexpr int WM = MF == 32 ? 2 : 4;
     if constexpr (!PB) {
-      if (bn >= 256) { launch_cfg<MODE, 192, 256, 4, 2, PB>(nbuf, g, dyn, st, t); return; }
+      if (bn >= 256) { launch_cfg<MODE, 192, 256, WM, 2, PB, MF>(nbuf, g, dyn, st, t); return; }
     }
-    launch_cfg<MODE, 192, 128, 4, 2, PB>(nbuf, g, dyn, st, t);
+    launch_cfg<MODE, 192, 128, WM, 2, PB, MF>(nbuf, g, dyn, st, t);
   }
-  else if (bm >= 128) launch_bn<MODE, 128, PB>(bn, nbuf, g, dyn, st, t);
-  else if (bm >= 64) launch_bn<MODE, 64, PB>(bn, nbuf, g, dyn, st, t);
-  else launch_bn<MODE, 32, PB>(bn, nbuf, g, dyn, st, t);
+  else if (bm >= 128) launch_bn<MODE, 128, PB, MF>(bn, nbuf, g, dyn, st, t);
+  else if (bm >= 64) launch_bn<MODE, 64, PB, MF>(bn, nbuf, g, dyn, st, t);
+  else launch_bn<MODE, 32, PB, 16>(bn, nbuf, g, dyn, st, t);  // 32 rows: 16x16 tiles
+}
+
+template <int MODE, bool PB>
+static void launch_bm(int bm, int bn, int nbuf, dim3 g, size_t dyn, hipStream_t st,
+                      const TiledArgs& t) {
+  if (tune().mf == 32) launch_bm_mf<MODE, PB, 32>(bm, bn, nbuf, g, dyn, st, t);
+  else launch_bm_mf<MODE, PB, 16>(bm, bn, nbuf, g, dyn, st, t);
 }
 
 static inline int tile_bn(int bn) { return bn >= 256 ? 256 : 128; }
@@ -821,6 +896,12 @@ hipError_t launch_linear_tiled(const LinArgs& a, int per_block, int bm, hipStrea
   // per-row 64 x 128 tiles (chosen when larger tiles leave CUs idle) run with
   // two K groups per workgroup: 21.1 -> 19.4 us at M = 512, K = N = 4096
   if (!per_block && bmv == 64 && bn == 128 && or_default(tune().tile_ksp, 2) == 2) {
+    if (tune().mf == 32) {  // 2 x (2 x 2) waves of 32 x 64
+      if (nbuf >= 3 && try_launch<MODE_DENSE, 64, 128, 2, 2, false, 3, 2, 32>(g, 0, st, t))
+        return hipGetLastError();
+      try_launch<MODE_DENSE, 64, 128, 2, 2, false, 2, 2, 32>(g, 0, st, t);
+      return hipGetLastError();
+    }
     if (nbuf >= 3 && try_launch<MODE_DENSE, 64, 128, 2, 4, false, 3, 2>(g, 0, st, t))
       return hipGetLastError();
     try_launch<MODE_DENSE, 64, 128, 2, 4, false, 2, 2>(g, 0, st, t);

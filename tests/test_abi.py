@@ -153,3 +153,21 @@ def test_workspace_size(L):
     n = L.bq_moe_phase2_workspace_size(T, k, H)
     assert n >= T * k * H * 4 and n % 256 == 0
     assert L.bq_moe_phase2_workspace_size(0, 8, H) == 0
+
+
+def test_calib_library_exports():
+    """libbq_calib.so (the benchmark's streaming-read and MFMA measurement
+    kernels) loads and rejects out-of-contract launches before any GPU call."""
+    path = os.path.join(ROOT, "mojo-gemma4-cpu_amd", "libbq_calib.so")
+    lib = C.CDLL(path)
+    for n in ("bqc_stream_read", "bqc_mfma_i8", "bqc_mfma_i8_ops"):
+        assert hasattr(lib, n)
+    lib.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.bqc_mfma_i8.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.bqc_mfma_i8_ops.argtypes = [C.c_int, C.c_int, C.c_int]
+    lib.bqc_mfma_i8_ops.restype = C.c_double
+    assert lib.bqc_stream_read(P, 256, 65, P, None) != 0      # K64 beyond the one-shot shape
+    assert lib.bqc_stream_read(C.c_void_p(17), 256, 64, P, None) != 0  # misaligned
+    assert lib.bqc_mfma_i8(24, 4, 8, P, None) != 0           # no such MFMA tile
+    assert lib.bqc_mfma_i8(17, 4, 7, P, None) != 0           # odd iterations on 16 chains
+    assert lib.bqc_mfma_i8_ops(32, 1024, 2048) == 262144.0 * 2048 * 1024 * 4

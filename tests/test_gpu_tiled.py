@@ -1,6 +1,8 @@
 """GPU parity of the LDS-tiled MFMA paths (prefill linears and the grouped MoE
-kernels) for every tile height, against the CPU oracle, bit-exact.  Tile
-heights are forced through the library's BQ_TILE_BM / BQ_MOE_BM switches."""
+kernels) for every tile height and both MFMA tiles (v_mfma_i32_16x16x64_i8
+and v_mfma_i32_32x32x32_i8), against the CPU oracle, bit-exact.  Tile heights
+and the MFMA tile are forced through the library's BQ_TILE_BM / BQ_MOE_BM /
+BQ_MF switches."""
 import numpy as np
 import pytest
 
@@ -10,12 +12,13 @@ pytestmark = pytest.mark.gpu
 ONE = 0x3F80
 
 
+@pytest.mark.parametrize("mf", [16, 32])
 @pytest.mark.parametrize("bn", [64, 128, 256])
 @pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("M,K,B", [(200, 512, None), (77, 2816, None), (150, 1024, 256),
                                    (96, 704, 64), (130, 2112, 64), (40, 4096, 64)])
-def test_dense_tiles(gpu, O, tune_env, bm, bn, M, K, B):
-    tune_env(BQ_TILE_BM=bm, BQ_TILE_BN=bn)
+def test_dense_tiles(gpu, O, tune_env, bm, bn, mf, M, K, B):
+    tune_env(BQ_TILE_BM=bm, BQ_TILE_BN=bn, BQ_MF=mf)
     N = 384  # 1.5 n-tiles at bn=256; N=2816 tails are covered in test_gpu_parity
     wf = O.bf16_to_f32(O.synth_normal_bf16(3, 0.02, (N, K)))
     q, s = O.rotate_and_quant(wf, B or 128)
@@ -35,12 +38,13 @@ def test_dense_tiles(gpu, O, tune_env, bm, bn, M, K, B):
     np.testing.assert_array_equal(host(ob), rb)
 
 
+@pytest.mark.parametrize("mf", [16, 32])
 @pytest.mark.parametrize("M,K,N", [(200, 512, 384), (77, 2816, 384), (512, 4096, 4096),
                                    (64, 128, 256), (130, 704, 256), (33, 192, 128)])
-def test_dense_split_k(gpu, O, tune_env, M, K, N):
+def test_dense_split_k(gpu, O, tune_env, mf, M, K, N):
     # per-row 64 x 128 tiles with two K groups per workgroup (odd, even and
     # single-stage K: the groups get equal stage counts, one more, or none)
-    tune_env(BQ_TILE_BM=64, BQ_TILE_BN=128, BQ_TILE_KSP=2)
+    tune_env(BQ_TILE_BM=64, BQ_TILE_BN=128, BQ_TILE_KSP=2, BQ_MF=mf)
     wf = O.bf16_to_f32(O.synth_normal_bf16(3, 0.02, (N, K)))
     q, s = O.rotate_and_quant(wf, 64)
     W = gpu.ButterquantWeight(gpu.retile(dev(q.reshape(-1)), N, K), dev(s), N, K)
@@ -89,7 +93,9 @@ def _tiny_moe(O, gpu, T, E=4, k=2, H=128, I=64, seed=5):
                                      (64, 256, None), (600, 256, None), (600, 256, 256),
                                      (300, 256, 256), (300, 192, None), (600, 192, 256),
                                      (600, 192, 128), (64, 192, None)])
-def test_moe_tiled(gpu, O, tune_env, T, bm, bn):
+@pytest.mark.parametrize("mf", [16, 32])
+def test_moe_tiled(gpu, O, tune_env, T, bm, bn, mf):
+    tune_env(BQ_MF=mf)
     if bm is not None:
         tune_env(BQ_MOE_BM=bm)
     if bn is not None:
@@ -133,11 +139,13 @@ def test_moe_gate_up_hidden2816(gpu, O, T):
     np.testing.assert_array_equal(host(bucket), rb)
 
 
-@pytest.mark.parametrize("T,breg", [(64, "0"), (300, "0"), (600, "0"), (33, "1"), (300, "1")])
-def test_moe_down_paths(gpu, O, tune_env, T, breg):
+@pytest.mark.parametrize("T,breg,mf", [(64, "0", 16), (300, "0", 16), (600, "0", 16),
+                                       (64, "0", 32), (300, "0", 32), (600, "0", 32),
+                                       (33, "1", 32), (300, "1", 32)])
+def test_moe_down_paths(gpu, O, tune_env, T, breg, mf):
     # the down projection with weights in registers (default for block 64 and
     # inter <= 704) and the LDS-ring k_tiled path it replaces
-    tune_env(BQ_DOWN_BREG=breg)
+    tune_env(BQ_DOWN_BREG=breg, BQ_MF=mf)
     c = _tiny_moe(O, gpu, T)
     E, H, I, k = c["E"], c["H"], c["I"], c["k"]
     eo, routes = gpu.build_schedule(dev(c["idx"]), dev(c["w"]), E)
