@@ -275,10 +275,12 @@ def bench_prefill(bq, torch, steps, warmup, reps=32):
 
 
 class MoeLayer:
-    """One quantized MoE expert layer from router logits: top-8 + softmax
-    routing -> norm-quant -> CSR schedule -> phase 1 (gate/up + GELU) with
-    the FWHT64 block-quant of the bucket fused -> phase 2 (down +
-    route-weighted, expert-ordered combine)."""
+    """One quantized MoE expert layer from router logits and hidden states:
+    top-8 + softmax routing and the CSR schedule (bq_moe_route_schedule),
+    the norm-quant of the hidden states, phase 1 (gate/up + GELU) with the
+    FWHT64 block-quant of the bucket fused, phase 2 (down + route-weighted,
+    expert-ordered combine) -- the reference's MoE block,
+    modeling/gemma_4_moe_bq.mojo:666-704, from its router logits on."""
 
     def __init__(self, bq, torch, T, Wgu, Wd, gen_seed=1):
         self.bq, self.T = bq, T
@@ -303,12 +305,31 @@ class MoeLayer:
                               dtype=torch.uint8, device=d)
         self.accum = torch.empty(T, H, dtype=torch.float32, device=d)
         self.out = torch.empty(T, H, dtype=torch.bfloat16, device=d)
+        self.side = torch.cuda.Stream()  # default priority
 
-    def __call__(self, _i=0, fused=True):
+    def __call__(self, _i=0, fused=True, overlap=1):
+        # overlap 1: bq_moe_route_schedule (one launch up to 16 tokens) then
+        # the norm-quant; 2: the norm-quant on a second stream beside it
+        # (measured slower: the graph's cross-stream joins cost more than the
+        # overlap saves); 0: the reference's three calls
+        import torch
         bq, T = self.bq, self.T
-        bq.route_topk(self.logits, TOPK, self.pes, out=(self.idx, self.w))
-        bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
-        bq.build_schedule(self.idx, self.w, E, out=(self.eo, self.routes))
+        if overlap == 2:
+            main = torch.cuda.current_stream()
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
+            bq.route_schedule(self.logits, TOPK, self.pes,
+                              out=(self.idx, self.w, self.eo, self.routes))
+            main.wait_stream(self.side)
+        elif overlap == 1:
+            bq.route_schedule(self.logits, TOPK, self.pes,
+                              out=(self.idx, self.w, self.eo, self.routes))
+            bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
+        else:
+            bq.route_topk(self.logits, TOPK, self.pes, out=(self.idx, self.w))
+            bq.norm_quant(self.x, self.gamma, 128, out=(self.xq, self.xsa))
+            bq.build_schedule(self.idx, self.w, E, out=(self.eo, self.routes))
         if fused:  # phase 1 with the bucket's FWHT64 block-quant in its epilogue
             bq.moe_phase1_quant(self.xq, self.xsa, self.eo, self.routes, self.Wgu, E, T, TOPK, I,
                                 out=(self.bi8, self.bsa, None))
@@ -693,7 +714,8 @@ def cpu_baseline_gemv(codes, scales, xq, sa, seconds, topo):
                 sample=f"decode GEMV M=1 K=N=4096 on the GPU run's codes and activation; "
                        f"p50 of {nd['samples']} calls after 30 warmups, {nd['threads']} threads "
                        f"pinned one per physical core on NUMA node {topo['node']}; "
-                       f"ISA {lib.bqcpu_isa().decode()}; gcc -O3 -fopenmp",
+                       f"ISA {lib.bqcpu_isa().decode()}; gcc -O3 -fopenmp, OMP_WAIT_POLICY="
+                       f"{os.environ.get('OMP_WAIT_POLICY')}",
                 p50_us=nd["p50_us"], min_us=nd["min_us"], all_cpus=legs["all"],
                 topology={k: topo[k] for k in ("cpu_model", "physical_cores", "numa_nodes",
                                                "logical_cpus_online", "allowed_logical_cpus",
@@ -740,7 +762,8 @@ def cpu_baseline_moe(bq, torch, Wgu, Wd, layers, seconds, topo):
                       f"on the GPU run's inputs; p50 (and min) of up to 600 calls after up to 30 "
                       f"warmups, ~{seconds / 2:.0f} s per T and leg; 'node': threads pinned one "
                       f"per physical core of NUMA node {topo['node']}, 'all': every allowed CPU "
-                      f"(at most 16, the box's CPU share); ISA {lib.bqcpu_isa().decode()}")
+                      f"(at most 16, the box's CPU share); ISA {lib.bqcpu_isa().decode()}; "
+                      f"OMP_WAIT_POLICY={os.environ.get('OMP_WAIT_POLICY')}")
     return res
 
 
@@ -816,6 +839,12 @@ def launch_histogram(path, reps=64):
 
 def main():
     args = parse()
+    # the CPU legs' OpenMP team sleeps between parallel regions instead of
+    # spinning: on a box whose CPU share equals the team size, spinning
+    # threads exhaust the share and the process is throttled (the 32-token
+    # MoE layer measured 290 ms spinning, 15.6 ms sleeping).  Read by libgomp
+    # when the CPU port first loads, which is after this point.
+    os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
     if args.launch_histogram:
         print(launch_histogram(args.launch_histogram))
         return

@@ -166,6 +166,20 @@ int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int se
                           int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
                           void* stream);
 
+/* dispatch_merge_router_candidates (kernels/moe_router.mojo:333-389)
+ * followed by dispatch_build_expert_schedules (:60-145) over all experts
+ * (expert_base 0) -- the two calls the reference's MoE block makes around
+ * its norm-quant (modeling/gemma_4_moe_bq.mojo:673-688) -- in one call:
+ * route_idx / route_w exactly as bq_moe_route_topk writes them, and
+ * expert_offset[experts+1] / routes[] exactly as bq_moe_build_schedule.
+ * Up to 16 tokens (and seq_len * top_k <= 1024) one workgroup keeps the
+ * routes in LDS and builds the schedule from there (one launch); larger
+ * calls run the two kernels.  experts <= 256, top_k <= 16; routes holds
+ * seq_len*top_k. */
+int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale, int seq_len,
+                          int experts, int top_k, int32_t* route_idx, float* route_w,
+                          int32_t* expert_offset, bq_route* routes, void* stream);
+
 /* dispatch_bq_phase1_gate_up[hidden, gate_up, inter] (moe.mojo:132-164):
  * for every route record rec of expert e (rows of w_gate_up: gate
  * [0,inter), up [inter, 2*inter) of expert e, expert stride 2*inter*hidden):

@@ -44,6 +44,7 @@ SIGNATURES = {
     "bq_moe_router_logits": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_moe_route_topk": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
+    "bq_moe_route_schedule": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "bq_head_prep": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_flash_sample_workspace_size": [_i, _i],
     "bq_flash_sample": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, C.c_int64, _vp, _sz,
@@ -301,6 +302,27 @@ def route_topk(logits: torch.Tensor, top_k: int, per_expert_scale: torch.Tensor 
     _check(_lib.bq_moe_route_topk(_p(logits), _p(per_expert_scale), t, e, top_k, _p(idx), _p(w),
                                   _stream()))
     return idx, w
+
+
+def route_schedule(logits: torch.Tensor, top_k: int, per_expert_scale: torch.Tensor | None = None,
+                   out=None):
+    """route_topk then build_schedule (expert_base 0) in one call:
+    f32 logits [T,E] -> (route_idx, route_w, expert_offset, routes)."""
+    _dev(logits, torch.float32)
+    if per_expert_scale is not None:
+        _dev(per_expert_scale, torch.bfloat16)
+    t, e = logits.shape
+    d = logits.device
+    if out is None:
+        idx = torch.empty((t, top_k), dtype=torch.int32, device=d)
+        w = torch.empty((t, top_k), dtype=torch.float32, device=d)
+        eo = torch.empty(e + 1, dtype=torch.int32, device=d)
+        routes = torch.zeros((t * top_k, 2), dtype=torch.int32, device=d)
+    else:
+        idx, w, eo, routes = out
+    _check(_lib.bq_moe_route_schedule(_p(logits), _p(per_expert_scale), t, e, top_k, _p(idx), _p(w),
+                                      _p(eo), _p(routes), _stream()))
+    return idx, w, eo, routes
 
 
 def build_schedule(route_idx: torch.Tensor, route_w: torch.Tensor, experts: int,

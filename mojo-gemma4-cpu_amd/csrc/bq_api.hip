@@ -302,6 +302,22 @@ int bq_moe_route_topk(const float* logits, const uint16_t* per_expert_scale, int
                    "route_topk");
 }
 
+int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale, int seq_len,
+                          int experts, int top_k, int32_t* route_idx, float* route_w,
+                          int32_t* expert_offset, bq_route* routes, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!logits || !route_idx || !route_w || !expert_offset || !routes)
+    return fail(BQ_ERR_INVALID, "bq_moe_route_schedule: null pointer");
+  if (experts <= 0 || top_k <= 0) return fail(BQ_ERR_SHAPE, "bq_moe_route_schedule: bad top_k/experts");
+  if (experts > 256 || top_k > 16)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_moe_route_schedule: experts %d > 256 or top_k %d > 16",
+                experts, top_k);
+  return check_hip(bq::launch_route_schedule(logits, per_expert_scale, seq_len, experts, top_k,
+                                             route_idx, route_w, expert_offset,
+                                             reinterpret_cast<bq::Route*>(routes), S(stream)),
+                   "route_schedule");
+}
+
 int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
                           int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
                           void* stream) {

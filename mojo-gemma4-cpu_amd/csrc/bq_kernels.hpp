@@ -120,6 +120,9 @@ int api_failv(int code, const char* fmt, va_list ap);  // sets bq_last_error()
 hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const uint16_t* rscale,
                                 float* logits, int T, int H, int E, float sqrt_n, float n_eps,
                                 hipStream_t st);
+hipError_t launch_route_schedule(const float* logits, const uint16_t* pes, int T, int E,
+                                 int top_k, int32_t* route_idx, float* route_w,
+                                 int32_t* expert_offset, Route* routes, hipStream_t st);
 hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,
                              int32_t* route_idx, float* route_w, hipStream_t st);
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,

@@ -16,10 +16,9 @@
 //   order, as the schedule (and the reference's) produces them.
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
+#include "bq_sched.hpp"
 
 namespace bq {
-
-constexpr int kMaxExperts = 256;
 
 // One workgroup per expert e.  The (expert, token, k) order puts route slot
 // s = t*top_k + kk of expert e at expert_offset[e] + (number of earlier slots
@@ -41,13 +40,21 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
   const int e = blockIdx.x, target = ebase + e, tid = threadIdx.x;
   const int lane = lane_id(), wave = tid >> 6;
   constexpr int kChunk = kRows * kSchedThreads;
-  // pass 1: slots routed to experts below e, and to e
+  // pass 1: slots routed to experts below e, and to e.  The first chunk's
+  // experts and weights stay in registers for pass 2 (with up to kChunk
+  // slots -- 2048 tokens x top-8 -- pass 2 then loads nothing).
   int below = 0, mine = 0;
+  int x0[kRows];
+  float w0[kRows];
   for (int c0 = 0; c0 < slots; c0 += kChunk) {
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
       const int s = c0 + j * kSchedThreads + tid;
       const int x = route_idx[min(s, slots - 1)];  // unmasked: loads stay batched
+      if (c0 == 0) {
+        x0[j] = x;
+        w0[j] = route_w[min(s, slots - 1)];
+      }
       below += (s < slots && x >= ebase && x < target) ? 1 : 0;
       mine += (s < slots && x == target) ? 1 : 0;
     }
@@ -75,8 +82,8 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
     for (int j = 0; j < kRows; ++j) {
       const int s = c0 + j * kSchedThreads + tid;
       const int sc = min(s, slots - 1);
-      const int x = route_idx[sc];
-      wts[j] = route_w[sc];
+      const int x = c0 == 0 ? x0[j] : route_idx[sc];
+      wts[j] = c0 == 0 ? w0[j] : route_w[sc];
       m[j] = __ballot(s < slots && x == target);
       if (lane == 0) cnt[j * kSchedWaves + wave] = __popcll(m[j]);
     }
@@ -113,64 +120,19 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
 }
 
 // Decode-sized schedules (at most 1024 slots): one workgroup, one thread per
-// slot.  A slot's record is its expert's offset plus the number of earlier
-// slots routed to the same expert -- the (expert, token, k) order of
-// k_build_schedule -- so one load, an LDS histogram, one scan and one
+// slot (schedule_small) -- one load, per-wave matching, two scans and one
 // scatter replace the per-expert passes over every slot.
-constexpr int kSchedSmallSlots = 1024;
-
 __global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
     const int32_t* __restrict__ route_idx, const float* __restrict__ route_w, int slots,
     int top_k, int ebase, int E, int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
-  __shared__ int s_e[kSchedSmallSlots];
+  __shared__ int s_wc[kSchedWavesSmall][kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
-  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int sc = min(tid, slots - 1);  // unmasked loads (slots >= 1)
   const int x = route_idx[sc];
   const float w = route_w[sc];
   const int e = (tid < slots && x >= ebase && x < ebase + E) ? x - ebase : -1;
-  s_e[tid] = e;
-  for (int i = tid; i < E; i += kSchedSmallSlots) s_cnt[i] = 0;
-  __syncthreads();
-  int rank = 0;
-  if (e >= 0) {
-    atomicAdd(&s_cnt[e], 1);
-#pragma unroll 8
-    for (int i = 0; i < tid; ++i) rank += s_e[i] == e ? 1 : 0;
-  }
-  __syncthreads();
-  if (wave == 0) {  // exclusive scan of the E <= 256 counts, 4 per lane
-    int v[4], sum = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ex = lane * 4 + j;
-      v[j] = ex < E ? s_cnt[ex] : 0;
-      sum += v[j];
-    }
-    int inc = sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += y;
-    }
-    int off = inc - sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ex = lane * 4 + j;
-      if (ex < E) {
-        s_cnt[ex] = off;
-        expert_offset[ex] = off;
-      }
-      off += v[j];
-    }
-    if (lane == 63) expert_offset[E] = inc;
-  }
-  __syncthreads();
-  if (e >= 0) {
-    const int pos = s_cnt[e] + rank;
-    routes[pos].token = tid / top_k;
-    routes[pos].weight = w;
-  }
+  schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
 }
 
 // Skinny (16-record m-tile) kernels for decode-sized batches.  Each wave owns

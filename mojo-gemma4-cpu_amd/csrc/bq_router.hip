@@ -17,6 +17,7 @@
 //   order, so the selected list is the reference's list entry for entry.
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
+#include "bq_sched.hpp"
 
 namespace bq {
 
@@ -176,6 +177,80 @@ __device__ inline uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// TPW tokens' top_k routes on one wave, their candidate chains interleaved:
+// lane k < top_k gets route k's expert and weight of token i in out_e[i],
+// out_w[i].  rows[i] points at token i's logits (all TPW rows are loaded
+// before any selection starts).
+template <int NE, int TPW>
+__device__ inline void topk_tokens(const float* const (&rows)[TPW],
+                                   const uint16_t* __restrict__ pes, int E, int top_k, int lane,
+                                   int (&out_e)[TPW], float (&out_w)[TPW]) {
+  uint64_t key[TPW][NE];
+  float lgv[TPW][NE];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+#pragma unroll
+    for (int q = 0; q < NE; ++q) lgv[i][q] = rows[i][min(lane + 64 * q, E - 1)];
+  uint64_t local[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+#pragma unroll
+    for (int q = 0; q < NE; ++q) {
+      const int e = lane + 64 * q;
+      key[i][q] = (e < E && lgv[i][q] > kRouterSentinel) ? cand_key(lgv[i][q], e) : 0ull;
+    }
+    local[i] = key[i][0];
+#pragma unroll
+    for (int q = 1; q < NE; ++q) local[i] = umax64(local[i], key[i][q]);
+  }
+  float mx[TPW], sum[TPW], my_ev[TPW];
+  int my_e[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    mx[i] = 0.0f;
+    sum[i] = 0.0f;
+    my_ev[i] = 0.0f;
+    my_e[i] = 0;
+  }
+  for (int k = 0; k < top_k; ++k) {
+    uint64_t best[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) best[i] = wave_max_u64(local[i]);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      float lg = kRouterSentinel;
+      int e = 0;
+      if (best[i] != 0ull) {
+        const uint32_t hi = (uint32_t)(best[i] >> 32), lo = (uint32_t)best[i];
+        e = 1023 - (int)(lo >> 1);
+        const uint32_t b = (hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi;
+        lg = __uint_as_float((lo & 1u) ? 0x80000000u : b);
+#pragma unroll
+        for (int q = 0; q < NE; ++q) key[i][q] = key[i][q] == best[i] ? 0ull : key[i][q];
+        local[i] = key[i][0];
+#pragma unroll
+        for (int q = 1; q < NE; ++q) local[i] = umax64(local[i], key[i][q]);
+      }
+      // RouterMergeKernel (:276-293): max = merged[0].logit, exp of the
+      // difference, sum in slot order
+      if (k == 0) mx[i] = lg;
+      const float ev = fast_exp_softmax_biased(lg - mx[i]);
+      sum[i] = sum[i] + ev;
+      if (lane == k) {
+        my_ev[i] = ev;
+        my_e[i] = e;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const float inv_sum = 1.0f / sum[i];
+    const float sc = (lane < top_k && pes) ? bf16_to_f32(pes[my_e[i]]) : 1.0f;
+    out_e[i] = my_e[i];
+    out_w[i] = my_ev[i] * inv_sum * sc;
+  }
+}
+
 template <int NE>
 __global__ __launch_bounds__(256) void k_route_topk(
     const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
@@ -183,51 +258,71 @@ __global__ __launch_bounds__(256) void k_route_topk(
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;  // whole waves; no block synchronization below
-  const float* row = logits + (size_t)t * E;
-  uint64_t key[NE];
-#pragma unroll
-  for (int q = 0; q < NE; ++q) {
-    const int e = lane + 64 * q;
-    const float lg = row[min(e, E - 1)];
-    key[q] = (e < E && lg > kRouterSentinel) ? cand_key(lg, e) : 0ull;
-  }
-  uint64_t local = key[0];
-#pragma unroll
-  for (int q = 1; q < NE; ++q) local = umax64(local, key[q]);
-
-  float mx = 0.0f, sum = 0.0f, my_ev = 0.0f;
-  int my_e = 0;
-  for (int k = 0; k < top_k; ++k) {
-    const uint64_t best = wave_max_u64(local);
-    float lg = kRouterSentinel;
-    int e = 0;
-    if (best != 0ull) {
-      const uint32_t hi = (uint32_t)(best >> 32), lo = (uint32_t)best;
-      e = 1023 - (int)(lo >> 1);
-      const uint32_t b = (hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi;
-      lg = __uint_as_float((lo & 1u) ? 0x80000000u : b);
-#pragma unroll
-      for (int q = 0; q < NE; ++q) key[q] = key[q] == best ? 0ull : key[q];
-      local = key[0];
-#pragma unroll
-      for (int q = 1; q < NE; ++q) local = umax64(local, key[q]);
-    }
-    // RouterMergeKernel (:276-293): max = merged[0].logit, exp of the
-    // difference, sum in slot order
-    if (k == 0) mx = lg;
-    const float ev = fast_exp_softmax_biased(lg - mx);
-    sum = sum + ev;
-    if (lane == k) {
-      my_ev = ev;
-      my_e = e;
-    }
-  }
-  const float inv_sum = 1.0f / sum;
+  const float* rows[1] = {logits + (size_t)t * E};
+  int e[1];
+  float w[1];
+  topk_tokens<NE, 1>(rows, pes, E, top_k, lane, e, w);
   if (lane < top_k) {
-    const float sc = pes ? bf16_to_f32(pes[my_e]) : 1.0f;
-    route_idx[(size_t)t * top_k + lane] = my_e;
-    route_w[(size_t)t * top_k + lane] = my_ev * inv_sum * sc;
+    route_idx[(size_t)t * top_k + lane] = e[0];
+    route_w[(size_t)t * top_k + lane] = w[0];
   }
+}
+
+// Route top-k + the CSR schedule in one workgroup (used up to 16 tokens;
+// seq_len * top_k <= kSchedSmallSlots, experts <= kMaxExperts): wave w takes tokens w, w + 16,
+// ... (TPW <= 8 at a time, their logits loaded at once and their selections
+// interleaved), writes route_idx / route_w and keeps each slot's expert and
+// weight in LDS, and the schedule is built from there (schedule_small) --
+// what k_route_topk followed by k_build_schedule_small write, in one launch.
+template <int NE, int TPW>
+__global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
+    const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
+    int32_t* __restrict__ route_idx, float* __restrict__ route_w,
+    int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
+  constexpr int NWV = kSchedSmallSlots / 64;
+  __shared__ int s_e[kSchedSmallSlots];
+  __shared__ float s_w[kSchedSmallSlots];
+  __shared__ int s_wc[kSchedWavesSmall][kMaxExperts];
+  __shared__ int s_cnt[kMaxExperts];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  for (int t0 = wave; t0 < T; t0 += NWV * TPW) {  // wave-uniform
+    const float* rows[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) rows[i] = logits + (size_t)min(t0 + NWV * i, T - 1) * E;
+    int e[TPW];
+    float w[TPW];
+    topk_tokens<NE, TPW>(rows, pes, E, top_k, lane, e, w);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int t = t0 + NWV * i;
+      if (t < T && lane < top_k) {
+        const int slot = t * top_k + lane;
+        route_idx[slot] = e[i];
+        route_w[slot] = w[i];
+        s_e[slot] = e[i];
+        s_w[slot] = w[i];
+      }
+    }
+  }
+  __syncthreads();
+  const bool live = tid < T * top_k;
+  const int e = live ? s_e[tid] : -1;
+  const float w = live ? s_w[tid] : 0.0f;
+  schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
+}
+
+template <int NE>
+static void launch_rss(int T, int E, int top_k, const float* logits, const uint16_t* pes,
+                       int32_t* route_idx, float* route_w, int32_t* eo, Route* routes,
+                       hipStream_t st) {
+  const dim3 g(1), b(kSchedSmallSlots);
+  const int tpw = (T + 15) / 16;  // tokens per wave (at most 8 at a time)
+#define BQ_RSS(N) hipLaunchKernelGGL((k_route_schedule_small<NE, N>), g, b, 0, st, logits, pes, T, E, top_k, route_idx, route_w, eo, routes)
+  if (tpw <= 1) BQ_RSS(1);
+  else if (tpw <= 2) BQ_RSS(2);
+  else if (tpw <= 4) BQ_RSS(4);
+  else BQ_RSS(8);
+#undef BQ_RSS
 }
 
 static int pick_port_unroll(int width, int cols) {
@@ -257,6 +352,25 @@ hipError_t launch_router_logits(const uint16_t* x, const uint16_t* proj, const u
                                 hipStream_t st) {
   if (T >= 256) return launch_logits_tile<8, 8>(x, proj, rscale, logits, T, H, E, sqrt_n, n_eps, st);
   return launch_logits_tile<2, 4>(x, proj, rscale, logits, T, H, E, sqrt_n, n_eps, st);
+}
+
+hipError_t launch_route_schedule(const float* logits, const uint16_t* pes, int T, int E,
+                                 int top_k, int32_t* route_idx, float* route_w,
+                                 int32_t* expert_offset, Route* routes, hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  if (E > kMaxExperts) return hipErrorInvalidValue;
+  // one workgroup for the whole call while every token has a wave of its
+  // own (16 tokens); beyond that the top-k spread over the chip and the
+  // schedule kernel are faster than one workgroup doing both
+  if (T > kSchedWavesSmall || T * top_k > kSchedSmallSlots) {
+    const hipError_t r = launch_route_topk(logits, pes, T, E, top_k, route_idx, route_w, st);
+    if (r != hipSuccess) return r;
+    return launch_build_schedule(route_idx, route_w, T, top_k, 0, E, expert_offset, routes, st);
+  }
+  if (E <= 64) launch_rss<1>(T, E, top_k, logits, pes, route_idx, route_w, expert_offset, routes, st);
+  else if (E <= 128) launch_rss<2>(T, E, top_k, logits, pes, route_idx, route_w, expert_offset, routes, st);
+  else launch_rss<4>(T, E, top_k, logits, pes, route_idx, route_w, expert_offset, routes, st);
+  return hipGetLastError();
 }
 
 hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,

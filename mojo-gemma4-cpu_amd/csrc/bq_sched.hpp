@@ -1,0 +1,90 @@
+// bq_sched.hpp -- the one-workgroup CSR expert schedule of up to
+// kSchedSmallSlots route slots (kernels/moe_router.mojo:60-106), shared by
+// bq_moe_build_schedule's decode-sized kernel and the fused route + schedule
+// kernel.
+#pragma once
+#include "bq_device.hpp"
+#include "bq_kernels.hpp"
+
+namespace bq {
+
+constexpr int kMaxExperts = 256;
+constexpr int kSchedSmallSlots = 1024;
+
+// Called by all kSchedSmallSlots threads of the workgroup; thread tid owns
+// route slot tid = token * top_k + k, with e its expert (0..E-1, or -1 for
+// no slot) and w its weight.  A slot's record is its expert's offset plus
+// the number of earlier slots routed to the same expert -- the (expert,
+// token, k) order.  Earlier slots of the same wave are counted by matching:
+// the wave takes one distinct expert at a time (its lowest unmatched lane's)
+// and ballots the lanes holding it; earlier waves' slots through an
+// exclusive prefix over the waves' per-expert counts (s_wc), and the experts'
+// offsets through a scan of their totals (s_cnt).
+constexpr int kSchedWavesSmall = kSchedSmallSlots / 64;
+
+__device__ inline void schedule_small(int e, float w, int top_k, int E,
+                                      int (*s_wc)[kMaxExperts], int* s_cnt,
+                                      int32_t* __restrict__ expert_offset,
+                                      Route* __restrict__ routes) {
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  for (int i = tid; i < kSchedWavesSmall * kMaxExperts; i += kSchedSmallSlots)
+    s_wc[i / kMaxExperts][i % kMaxExperts] = 0;
+  __syncthreads();
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int rank = 0;
+  unsigned long long active = __ballot(e >= 0);
+  while (active) {  // wave-uniform: one distinct expert per pass
+    const int leader = __ffsll((long long)active) - 1;
+    const int le = __builtin_amdgcn_readlane(e, leader);
+    const unsigned long long m = __ballot(e == le);
+    if (e == le) rank = __popcll(m & below);
+    if (lane == leader) s_wc[wave][le] = __popcll(m);
+    active &= ~m;
+  }
+  __syncthreads();
+  for (int x = tid; x < E; x += kSchedSmallSlots) {  // prefix over waves, per expert
+    int run = 0;
+#pragma unroll
+    for (int q = 0; q < kSchedWavesSmall; ++q) {
+      const int v = s_wc[q][x];
+      s_wc[q][x] = run;
+      run += v;
+    }
+    s_cnt[x] = run;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the E <= 256 totals, 4 per lane
+    int v[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane * 4 + j;
+      v[j] = ex < E ? s_cnt[ex] : 0;
+      sum += v[j];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += y;
+    }
+    int off = inc - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane * 4 + j;
+      if (ex < E) {
+        s_cnt[ex] = off;
+        expert_offset[ex] = off;
+      }
+      off += v[j];
+    }
+    if (lane == 63) expert_offset[E] = inc;
+  }
+  __syncthreads();
+  if (e >= 0) {
+    const int pos = s_cnt[e] + s_wc[wave][e] + rank;
+    routes[pos].token = tid / top_k;
+    routes[pos].weight = w;
+  }
+}
+
+}  // namespace bq

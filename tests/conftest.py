@@ -74,3 +74,8 @@ def moe_model(gpu, O):
     gp, gcs = O.pack_and_colsum(gq)
     dp, dcs = O.pack_and_colsum(dq, 64, False)
     return dict(E=E, H=H, I=I, gs=gs, ds=ds, gp=gp, gcs=gcs, dp=dp, dcs=dcs, Wgu=Wgu, Wd=Wd)
+
+# the CPU port's OpenMP team (oracle/cpu_baseline.c) sleeps between parallel
+# regions: spinning threads on a CPU share no larger than the team throttle
+# the process (read when the port's libgomp loads, after this module)
+os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")

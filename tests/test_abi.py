@@ -80,6 +80,11 @@ def test_validation_errors(L):
     assert L.bq_moe_route_topk(P, None, 4, 2048, 8, P, P, None) == 4
     assert L.bq_moe_route_topk(P, None, 4, 128, 0, P, P, None) == 2
     assert L.bq_moe_route_topk(None, None, 4, 128, 8, P, P, None) == 1
+    assert L.bq_moe_route_schedule(P, None, 4, 512, 8, P, P, P, P, None) == 4
+    assert L.bq_moe_route_schedule(P, None, 4, 128, 17, P, P, P, P, None) == 4
+    assert L.bq_moe_route_schedule(P, None, 4, 128, 0, P, P, P, P, None) == 2
+    assert L.bq_moe_route_schedule(P, None, 4, 128, 8, P, P, None, P, None) == 1
+    assert L.bq_moe_route_schedule(P, None, 0, 128, 8, None, None, None, None, None) == 0
     assert L.bq_moe_router_logits(P, P, P, P, 4, 2880 + 32, 128, C.c_float(1), C.c_float(1),
                                   None) == 2
     assert L.bq_moe_router_logits(P, C.c_void_p(18), P, P, 4, 2816, 128, C.c_float(1),

@@ -295,6 +295,33 @@ def test_build_schedule(gpu, O, T):
     np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
 
 
+@pytest.mark.parametrize("T,E,k,pes", [(1, 128, 8, False), (5, 128, 8, True), (16, 60, 8, False),
+                                      (16, 256, 16, True), (32, 128, 8, True),
+                                      (128, 128, 8, False), (129, 128, 8, True),
+                                      (2048, 128, 8, True), (40, 60, 2, False),
+                                      (64, 256, 16, True), (300, 8, 2, False),
+                                      (1000, 64, 1, False), (200, 128, 4, True)])
+def test_route_schedule(gpu, O, T, E, k, pes):
+    """the fused route top-k + schedule equals the two calls and the oracle:
+    one workgroup up to 16 tokens (E <= 64, <= 128, <= 256 instances), the
+    two kernels above"""
+    logits = O.synth_normal_f32(7 + T, 1.0, (T, E))
+    sc = O.f32_to_bf16(O.synth_normal_f32(8, 0.2, (E,)) + 1.0) if pes else None
+    idx, w, eo, routes = gpu.route_schedule(dev(logits), k, None if sc is None else dev(sc))
+    ridx, rw = O.route_topk_softmax(logits, k, sc)
+    np.testing.assert_array_equal(host(idx), ridx)
+    np.testing.assert_array_equal(host(w), rw)
+    reo, rroutes = O.build_schedule(ridx, rw, E)
+    np.testing.assert_array_equal(host(eo), reo)
+    r = host(routes)
+    np.testing.assert_array_equal(r[:, 0], rroutes["token"])
+    np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
+    i2, w2 = gpu.route_topk(dev(logits), k, None if sc is None else dev(sc))
+    eo2, routes2 = gpu.build_schedule(i2, w2, E)
+    np.testing.assert_array_equal(host(eo2), host(eo))
+    np.testing.assert_array_equal(host(routes2), r)
+
+
 def test_build_schedule_expert_range(gpu, O):
     # expert-parallel slice [32, 64) as a rank of degree 4 would build it
     idx, w = route_table(O, 40)
