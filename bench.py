@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration kernel)")
+    ap.add_argument("--samples", type=int, default=600,
+                    help="graph replays timed per workload (untimed warmup: min(30, samples)); "
+                         "profiler runs use a few")
     ap.add_argument("--launch-histogram", metavar="KERNEL_TRACE_CSV",
                     help="no GPU: summarize the per-launch durations of the GEMV and the "
                          "streaming read in a rocprofv3 --kernel-trace CSV of --workload gemv")
@@ -839,6 +842,9 @@ def launch_histogram(path, reps=64):
 
 def main():
     args = parse()
+    global SAMPLES, WARMUP
+    SAMPLES = max(1, args.samples)
+    WARMUP = min(WARMUP, SAMPLES)
     # the CPU legs' OpenMP team sleeps between parallel regions instead of
     # spinning: on a box whose CPU share equals the team size, spinning
     # threads exhaust the share and the process is throttled (the 32-token
@@ -940,7 +946,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(p["tops"], 1),
                          "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                          "frac": round(p["int8_frac"], 4),
-                         "traffic": _traffic("prefill_gemm_m512_k4096_n4096_traffic.txt"),
+                         "traffic": _traffic("prefill_gemm_m512_k4096_n4096_stats.txt"),
                          "measured_peak": mf,
                          "frac_of_measured": round(p["tops"] / mf, 4) if mf else None,
                          "basis": "2*M*N*K int8 ops / p50 launch time; peak = dense int8 MFMA"}}
@@ -955,7 +961,7 @@ def main():
                  "experts_touched": m["experts_touched"],
                  "weight_GBs": round(wgbs, 1), "hbm_frac_weights": round(wgbs / HBM_PEAK_GBS, 4),
                  "int8_tops": round(tops, 1), **m["s"].summary()}
-            traffic = _traffic(f"moe_layer_t{T}_traffic.txt")
+            traffic = _traffic(f"moe_layer_t{T}_stats.txt")
             if T >= 2048:
                 # the north star's bar for this layer: a fraction of the
                 # matching MFMA peak; the layer's weights are bf16 models
