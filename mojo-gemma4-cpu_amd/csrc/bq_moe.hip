@@ -400,12 +400,13 @@ __global__ __launch_bounds__(256) void k_combine(
     f4 v[kMaxTopK];
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j)
-      if (j < cnt) v[j] = *reinterpret_cast<const f4*>(y + (size_t)rr[j] * hidden + c);
+      if (j < cnt)  // each y row is read once: non-temporal
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(y + (size_t)rr[j] * hidden + c));
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j)
       if (j < cnt) acc = acc + v[j];
-    *reinterpret_cast<f4*>(accum + (size_t)t * hidden + c) = acc;
+    __builtin_nontemporal_store(acc, reinterpret_cast<f4*>(accum + (size_t)t * hidden + c));
     const uint32_t lo = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
     const uint32_t hi = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
