@@ -188,10 +188,15 @@ def bench_gemv(bq, torch, steps, warmup, reps=64):
     gl = graph_of(lambda i: (bq.norm_quant(x, gamma, 128, out=(xq, sa)),
                              bq.linear(xq, sa, replicas[i], out=out)), reps)
     s_lin = time_graph(gl, reps, 0, 0)
+    # the same in one launch (bq_norm_linear: every output tile quantizes the
+    # row itself while its weights stream in)
+    gf = graph_of(lambda i: bq.norm_linear(x, gamma, replicas[i], 128, out=out,
+                                           act_out=(xq, sa)), reps)
+    s_fused = time_graph(gf, reps, 0, 0)
     rd = bench_stream(torch, [r.data for r in replicas], N // 16, K // 64, steps, warmup)
     return dict(s=smp, alg_bytes=alg_bytes, gbs=alg_bytes / (smp.p50 * 1e-3) / 1e9,
                 gbs_min=alg_bytes / (smp.min * 1e-3) / 1e9, s_nq=s_nq, s_lin=s_lin,
-                rd=rd, codes=codes, scales=scales, xq=xq, sa=sa)
+                s_fused=s_fused, rd=rd, codes=codes, scales=scales, xq=xq, sa=sa)
 
 
 def bench_stream(torch, bufs, tiles, K64, steps, warmup):
@@ -921,7 +926,10 @@ def main():
                                "alg_bytes_per_launch": gv["alg_bytes"],
                                "best_GBs": round(gv["gbs_min"], 1), **smp.summary(),
                                "norm_quant": gv["s_nq"].summary(),
-                               "linear_with_prep": gv["s_lin"].summary()}
+                               "linear_with_prep": gv["s_lin"].summary(),
+                               "linear_with_prep_fused": {
+                                   "kernel": "k_norm_linear_skinny (bq_norm_linear)",
+                                   **gv["s_fused"].summary()}}
         rd = gv["rd"]
         line["stream_read_same_shape"] = {
             "kernel": "k_stream_read (256 workgroups x 8 waves, one-shot non-temporal 16-byte "

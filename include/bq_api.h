@@ -132,6 +132,26 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
            uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, int qn, int kvn, int seq_len,
            int hidden, void* stream);
 
+/* Fused decode prep: bq_norm_quant of src followed by bq_linear (resp.
+ * bq_qkv) on its output, with the same results: x_i8 / x_sa receive the
+ * norm-quant's codes and amax, out the linear's.  No single counterpart in
+ * the reference, whose decoder calls dispatch_bq_norm_quant and then
+ * dispatch_bq_linear / dispatch_bq_qkv on the activation it wrote
+ * (butterquant_kernels/linear.mojo:58-82, 119-149, 273-326).  For seq_len 1,
+ * hidden % 256 == 0 and hidden <= 4096 (the decode token) it is one launch,
+ * in which every output tile quantizes the row itself while its weights
+ * stream in; otherwise the two launches.  The checks of both calls apply
+ * (src and x_i8 16-byte aligned). */
+int bq_norm_linear(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                   const int8_t* w, const float* w_scale, uint16_t* out, float* out_f32,
+                   int n_rows, int seq_len, int hidden, int block, float sqrt_n, float n_eps,
+                   void* stream);
+int bq_norm_qkv(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                const int8_t* q_w, const float* q_scale, const int8_t* k_w, const float* k_scale,
+                const int8_t* v_w, const float* v_scale, uint16_t* q_out, uint16_t* k_out,
+                uint16_t* v_out, int qn, int kvn, int seq_len, int hidden, int block,
+                float sqrt_n, float n_eps, void* stream);
+
 /* ---- MoE ---------------------------------------------------------------- */
 
 /* RouterExpertKernel (kernels/moe_router.mojo:149-193, dispatch_router_expert
@@ -172,7 +192,7 @@ int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int se
  * its norm-quant (modeling/gemma_4_moe_bq.mojo:673-688) -- in one call:
  * route_idx / route_w exactly as bq_moe_route_topk writes them, and
  * expert_offset[experts+1] / routes[] exactly as bq_moe_build_schedule.
- * Up to 16 tokens (and seq_len * top_k <= 1024) one workgroup keeps the
+ * Up to 8 tokens (and seq_len * top_k <= 1024) one workgroup keeps the
  * routes in LDS and builds the schedule from there (one launch); larger
  * calls run the two kernels.  experts <= 256, top_k <= 16; routes holds
  * seq_len*top_k. */

@@ -41,6 +41,8 @@ SIGNATURES = {
     "bq_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "bq_block_linear": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "bq_qkv": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "bq_norm_linear": [_vp] * 8 + [_i, _i, _i, _i, _f, _f, _vp],
+    "bq_norm_qkv": [_vp] * 13 + [_i, _i, _i, _i, _i, _f, _f, _vp],
     "bq_moe_router_logits": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_moe_route_topk": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
@@ -264,6 +266,48 @@ def qkv(x_i8, x_sa, q: ButterquantWeight, k: ButterquantWeight, v: ButterquantWe
                        _p(v.data), _p(v.scale), _p(qo), _p(ko), _p(vo), q.n_rows, k.n_rows, m,
                        hidden, _stream()))
     return qo, ko, vo
+
+
+def norm_linear(x: torch.Tensor, gamma: torch.Tensor, w: ButterquantWeight, block: int = 128,
+                sqrt_n=None, n_eps=None, want_f32: bool = False, out=None, act_out=None):
+    """norm_quant(x) then linear on its codes, fused into one launch for one
+    token; returns out (and the f32 values) plus the activation (x_i8, x_sa)."""
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    m, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    xq, sa = act_out if act_out is not None else (
+        torch.empty((m, h), dtype=torch.int8, device=x.device),
+        torch.empty(m, dtype=torch.float32, device=x.device))
+    if out is None:
+        out = torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x.device)
+    of = torch.empty((m, w.n_rows), dtype=torch.float32, device=x.device) if want_f32 else None
+    _check(_lib.bq_norm_linear(_p(x), _p(gamma), _p(xq), _p(sa), _p(w.data), _p(w.scale),
+                               _p(out), _p(of), w.n_rows, m, h, block, sqrt_n, n_eps, _stream()))
+    return ((out, of) if want_f32 else out), (xq, sa)
+
+
+def norm_qkv(x: torch.Tensor, gamma: torch.Tensor, q: ButterquantWeight, k: ButterquantWeight,
+             v: ButterquantWeight, block: int = 128, sqrt_n=None, n_eps=None, outs=None,
+             act_out=None):
+    """norm_quant(x) then qkv on its codes, fused into one launch for one token."""
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    m, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    xq, sa = act_out if act_out is not None else (
+        torch.empty((m, h), dtype=torch.int8, device=x.device),
+        torch.empty(m, dtype=torch.float32, device=x.device))
+    if outs is None:
+        outs = tuple(torch.empty((m, wt.n_rows), dtype=torch.bfloat16, device=x.device)
+                     for wt in (q, k, v))
+    qo, ko, vo = outs
+    _check(_lib.bq_norm_qkv(_p(x), _p(gamma), _p(xq), _p(sa), _p(q.data), _p(q.scale),
+                            _p(k.data), _p(k.scale), _p(v.data), _p(v.scale), _p(qo), _p(ko),
+                            _p(vo), q.n_rows, k.n_rows, m, h, block, sqrt_n, n_eps, _stream()))
+    return (qo, ko, vo), (xq, sa)
 
 
 # --------------------------------------------------------------------------

@@ -326,21 +326,12 @@ static void launch_nq_wave(dim3 g, size_t lds, hipStream_t st, const uint16_t* s
                      hidden, block, pu, sqrt_n, n_eps, sc);
 }
 
-// Pair layout (hidden % 256 == 0, so the reference's sum of squares runs on
-// pu = 8 port-unrolled accumulators, i.e. 128 chains).  Lane L holds the
-// bf16 pair (128 q + 2 L, 128 q + 2 L + 1) of every 128-value segment q --
-// one coalesced 4-byte load per segment -- and with it exactly the pairs of
-// chains L (segments 0, 2, 4, ...) and L + 64 (segments 1, 3, 5, ...), in
-// chain order (rms_reduce_row: chain c takes pairs c, c + 128, c + 256, ...;
-// odd element first).  The FWHT of block B: stride 1 inside the pair,
-// strides 2 .. 64 across lanes (lane ^ s/2), strides 128 and 256 across
-// segments, ascending.
-//
-// A token takes WPT = ceil(nseg / SPW) waves: each loads the whole row and
-// computes the sum of squares (it is cheap, and it keeps the chain order),
-// then transforms and quantizes its own SPW segments; the row's amax is
-// exchanged through LDS (one barrier) when WPT > 1.  WPT = 1 runs four tokens
-// per workgroup without LDS or barriers.
+// Pair-layout norm-quant (nq_pair_* in bq_device.hpp).  A token takes
+// WPT = ceil(nseg / SPW) waves: each loads the whole row and computes the sum
+// of squares (it is cheap, and it keeps the chain order), then transforms and
+// quantizes its own SPW segments; the row's amax is exchanged through LDS
+// (one barrier) when WPT > 1.  WPT = 1 runs four tokens per workgroup without
+// LDS or barriers.
 template <int NSEG, int SPW>
 __global__ __launch_bounds__(512) void k_norm_quant_pair(
     const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
@@ -356,98 +347,30 @@ __global__ __launch_bounds__(512) void k_norm_quant_pair(
   if (t >= T) return;                      // (one: whole waves, nothing synchronizes)
   const uint32_t* xr = reinterpret_cast<const uint32_t*>(src + (size_t)t * hidden) + lane;
   const uint32_t* gr = reinterpret_cast<const uint32_t*>(gamma) + lane;
-  uint32_t xp[NSEG], gp[SPW];
+  // A wave of a token's several loads its own segments again, into x:
+  // cheaper than picking them out of xp by a run-time index.
+  // (loads return in issue order: the row first, which the sum of squares
+  // needs first)
+  uint32_t xp[NSEG], x[SPW], gp[SPW];
 #pragma unroll
   for (int q = 0; q < NSEG; ++q)
     if (q < nseg) xp[q] = xr[64 * q];
+  // (segments past nseg are loaded nowhere and read nowhere)
 #pragma unroll
-  for (int i = 0; i < SPW; ++i)
-    if (q0 + i < nseg) gp[i] = gr[64 * (q0 + i)];
-  // chains L (even segments) and L + 64 (odd segments)
-  float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-  for (int q = 0; q < NSEG; q += 2) {
-    if (q >= nseg) break;
-    const float o0 = __uint_as_float(xp[q] & 0xFFFF0000u), e0 = __uint_as_float(xp[q] << 16);
-    const float o1 = __uint_as_float(xp[q + 1] & 0xFFFF0000u), e1 = __uint_as_float(xp[q + 1] << 16);
-    a0 = fmaf(o0, o0, a0);
-    a0 = fmaf(e0, e0, a0);
-    a1 = fmaf(o1, o1, a1);
-    a1 = fmaf(e1, e1, a1);
+  for (int i = 0; i < SPW; ++i) {
+    if (q0 + i < nseg) {
+      if constexpr (SPW < NSEG) x[i] = xr[64 * (q0 + i)];
+      gp[i] = gr[64 * (q0 + i)];
+    }
   }
-  // s_j = sum over p of chain p*16 + j in p order, then the 16-lane halving tree
-  float sum = 0.0f;
+  if constexpr (SPW >= NSEG) {  // one wave per token: q0 = 0, x is xp
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int c = p * 16 + (lane & 15);
-    const float v0 = __shfl(a0, c & 63, kWave);
-    const float v1 = __shfl(a1, c & 63, kWave);
-    sum = sum + (c < 64 ? v0 : v1);
+    for (int i = 0; i < SPW; ++i) x[i] = xp[i];
   }
-#pragma unroll
-  for (int h = 8; h >= 1; h >>= 1) sum = sum + __shfl_down(sum, h, 16);
-  const float total = __shfl(sum, 0, kWave);
+  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
   const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
-
   float v[SPW][2];
-#pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    const int q = q0 + i;
-    uint32_t x = 0u;
-#pragma unroll
-    for (int k = 0; k < NSEG; ++k)  // static register index of segment q
-      if (k == q) x = xp[k];
-    if (q < nseg) {
-      const float e = __uint_as_float(x << 16), o = __uint_as_float(x & 0xFFFF0000u);
-      const float ge = __uint_as_float(gp[i] << 16), go = __uint_as_float(gp[i] & 0xFFFF0000u);
-      v[i][0] = e * inv_rms * ge;
-      v[i][1] = o * inv_rms * go;
-    } else {
-      v[i][0] = v[i][1] = 0.0f;
-    }
-  }
-  // stride 1 inside the pair
-#pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    const float x0 = v[i][0], x1 = v[i][1];
-    v[i][0] = x0 + x1;
-    v[i][1] = x0 - x1;
-  }
-  // strides 2 .. min(B/2, 64) across lanes: element bit k is lane bit k - 1
-  auto lanes = [&](auto st) {
-    constexpr int ST = decltype(st)::value;
-    if (block > 2 * ST) {
-#pragma unroll
-      for (int i = 0; i < SPW; ++i)
-#pragma unroll
-        for (int r = 0; r < 2; ++r) v[i][r] = xlane_bfly<ST>(v[i][r]);
-    }
-  };
-  lanes(Stride<1>{}); lanes(Stride<2>{}); lanes(Stride<4>{});
-  lanes(Stride<8>{}); lanes(Stride<16>{}); lanes(Stride<32>{});
-  // strides 128 and 256 across segments (SPW and q0 are multiples of B/128)
-#pragma unroll
-  for (int ss = 1; ss <= 2; ss <<= 1) {
-    if (block <= 128 * ss) break;
-#pragma unroll
-    for (int i = 0; i < SPW; ++i) {
-      if ((i & ss) || i + ss >= SPW) continue;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float x0 = v[i][r], x1 = v[i + ss][r];
-        v[i][r] = x0 + x1;
-        v[i + ss][r] = x0 - x1;
-      }
-    }
-  }
-  float m = 0.0f;
-#pragma unroll
-  for (int i = 0; i < SPW; ++i)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      v[i][r] = v[i][r] * fwht_scale;
-      m = fmaxf(m, fabsf(v[i][r]));
-    }
+  const float m = nq_pair_transform<SPW>(x, gp, inv_rms, q0, nseg, block, fwht_scale, v);
   float amax = wave_max(m);
   if (!one) {
     if (lane == 0) s_max[wave] = amax;
@@ -459,13 +382,11 @@ __global__ __launch_bounds__(512) void k_norm_quant_pair(
   uint16_t* qrow = reinterpret_cast<uint16_t*>(xq + (size_t)t * hidden) + lane;
 #pragma unroll
   for (int i = 0; i < SPW; ++i)
-    if (q0 + i < nseg)
-      qrow[64 * (q0 + i)] = (uint16_t)((uint8_t)quantize_i8(v[i][0], inv) |
-                                       ((uint16_t)(uint8_t)quantize_i8(v[i][1], inv) << 8));
+    if (q0 + i < nseg) qrow[64 * (q0 + i)] = nq_pair_code(v[i], inv);
   if (lane == 0 && wave == (one ? wave : 0)) sa[t] = amax;
 }
 
-// smallest instance holding nseg segments of R*64 values (hidden <= 4096)// smallest instance holding nseg segments of R*64 values (hidden <= 4096)
+// smallest instance holding nseg segments of R*64 values (hidden <= 4096)
 static bool launch_norm_quant_wave(int R, int nseg, const uint16_t* src, const uint16_t* gamma,
                                    int8_t* xq, float* sa, int T, int hidden, int block, int pu,
                                    float sqrt_n, float n_eps, float sc, hipStream_t st) {

@@ -273,6 +273,66 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
   return check_hip(bq::launch_linear(a, 0, S(stream)), "qkv");
 }
 
+// shared checks of the fused norm-quant + linear entries (those of
+// bq_norm_quant and of the linear on its output)
+static int norm_linear_args(const char* who, const uint16_t* src, const uint16_t* gamma,
+                            int8_t* x_i8, float* x_sa, int hidden, int block, float sqrt_n,
+                            float n_eps, bq::NormArgs& nq) {
+  if (!src || !gamma || !x_i8 || !x_sa) return fail(BQ_ERR_INVALID, "%s: null pointer", who);
+  if (!fwht_block_ok(block)) return fail(BQ_ERR_SHAPE, "%s: unsupported FWHT block %d", who, block);
+  if (hidden <= 0 || hidden % 64 || hidden % block)
+    return fail(BQ_ERR_SHAPE, "%s: hidden %d must be a multiple of 64 and of block %d", who, hidden, block);
+  if (hidden > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "%s: hidden %d > %d", who, hidden, kMaxRowLds);
+  if (!a16(src) || !a16(x_i8)) return fail(BQ_ERR_INVALID, "%s: src and x_i8 must be 16-byte aligned", who);
+  nq = bq::NormArgs{src, gamma, x_i8, x_sa, block, sqrt_n, n_eps, 0.0f};
+  return BQ_OK;
+}
+
+int bq_norm_linear(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                   const int8_t* w, const float* w_scale, uint16_t* out, float* out_f32,
+                   int n_rows, int seq_len, int hidden, int block, float sqrt_n, float n_eps,
+                   void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  bq::NormArgs nq{};
+  const int r = norm_linear_args("bq_norm_linear", src, gamma, x_i8, x_sa, hidden, block, sqrt_n,
+                                 n_eps, nq);
+  if (r != BQ_OK) return r;
+  if (!w || !w_scale || !out) return fail(BQ_ERR_INVALID, "bq_norm_linear: null pointer");
+  if (n_rows <= 0 || n_rows % 16)
+    return fail(BQ_ERR_SHAPE, "bq_norm_linear: need n_rows %% 16 == 0 (got %d)", n_rows);
+  if (!a16(w)) return fail(BQ_ERR_INVALID, "bq_norm_linear: int8 operands must be 16-byte aligned");
+  bq::LinArgs a{};
+  a.seg[0] = {w, w_scale, out, out_f32, n_rows, 0};
+  a.nseg = 1;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_norm_linear(a, nq, S(stream)), "norm_linear");
+}
+
+int bq_norm_qkv(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                const int8_t* q_w, const float* q_scale, const int8_t* k_w, const float* k_scale,
+                const int8_t* v_w, const float* v_scale, uint16_t* q_out, uint16_t* k_out,
+                uint16_t* v_out, int qn, int kvn, int seq_len, int hidden, int block,
+                float sqrt_n, float n_eps, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  bq::NormArgs nq{};
+  const int r = norm_linear_args("bq_norm_qkv", src, gamma, x_i8, x_sa, hidden, block, sqrt_n,
+                                 n_eps, nq);
+  if (r != BQ_OK) return r;
+  if (!q_w || !q_scale || !k_w || !k_scale || !v_w || !v_scale || !q_out || !k_out || !v_out)
+    return fail(BQ_ERR_INVALID, "bq_norm_qkv: null pointer");
+  if (qn <= 0 || kvn <= 0 || qn % 16 || kvn % 16)
+    return fail(BQ_ERR_SHAPE, "bq_norm_qkv: need qn, kvn %% 16 == 0");
+  if (!a16(q_w) || !a16(k_w) || !a16(v_w))
+    return fail(BQ_ERR_INVALID, "bq_norm_qkv: int8 operands must be 16-byte aligned");
+  bq::LinArgs a{};
+  a.seg[0] = {q_w, q_scale, q_out, nullptr, qn, 0};
+  a.seg[1] = {k_w, k_scale, k_out, nullptr, kvn, qn / 16};
+  a.seg[2] = {v_w, v_scale, v_out, nullptr, kvn, qn / 16 + kvn / 16};
+  a.nseg = 3;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_norm_linear(a, nq, S(stream)), "norm_qkv");
+}
+
 int bq_moe_router_logits(const uint16_t* x, const uint16_t* router_proj,
                          const uint16_t* router_scale, float* logits, int seq_len, int hidden,
                          int experts, float sqrt_n, float n_eps, void* stream) {

@@ -188,9 +188,17 @@ __device__ inline float gumbel_noise(uint64_t seed, int64_t row, int64_t idx) {
 // ---------------------------------------------------------------------------
 __device__ inline int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// (after the cross-lane partner helpers below)
+template <int ST>
+__device__ inline float xlane_partner(float v);
+
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  v = fmaxf(v, xlane_partner<32>(v));
+  v = fmaxf(v, xlane_partner<16>(v));
+  v = fmaxf(v, xlane_partner<8>(v));
+  v = fmaxf(v, xlane_partner<4>(v));
+  v = fmaxf(v, xlane_partner<2>(v));
+  v = fmaxf(v, xlane_partner<1>(v));
   return v;
 }
 
@@ -200,11 +208,13 @@ __device__ inline float group_max(float v, int width) {
   return v;
 }
 
-// The value that lane (lane ^ ST) of the wave holds.  Strides 1 and 2 are one
-// DPP quad permutation, stride 8 one DPP row rotation by 8 (within a row of
-// 16 lanes that is lane ^ 8), stride 4 two DPP row shifts (lane + 4 for
-// lanes with bit 2 clear, lane - 4 otherwise) and a select; strides 16 and
-// 32 cross rows and go through ds_bpermute.
+// The value that lane (lane ^ ST) of the wave holds, all on the VALU.  Strides
+// 1 and 2 are one DPP quad permutation, stride 8 one DPP row rotation by 8
+// (within a row of 16 lanes that is lane ^ 8), stride 4 two DPP row shifts
+// (lane + 4 for lanes with bit 2 clear, lane - 4 otherwise) and a select.
+// Strides 16 and 32 cross rows: v_permlane16_swap(v, v) leaves row r's
+// partner row (r ^ 1) in the second result for even rows and in the first
+// for odd rows; v_permlane32_swap(v, v) likewise for the two 32-lane halves.
 template <int ST>
 __device__ inline float xlane_partner(float v) {
   static_assert(ST >= 1 && ST <= 32 && (ST & (ST - 1)) == 0, "stride");
@@ -219,9 +229,39 @@ __device__ inline float xlane_partner(float v) {
     return __int_as_float((threadIdx.x & 4) ? dn : up);
   } else if constexpr (ST == 8) {
     return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false));  // row_ror:8
+  } else if constexpr (ST == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return __int_as_float((int)((threadIdx.x & 16) ? r[0] : r[1]));
   } else {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(((int)(threadIdx.x & 63) ^ ST) << 2, x));
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __int_as_float((int)((threadIdx.x & 32) ? r[0] : r[1]));
   }
+}
+
+// The value that lane (lane & 15) + 16 * R of the wave holds, for lanes 0..15
+// (row 0; the other lanes get values of no use): row R's lane j brought to
+// row 0 by the row swaps of xlane_partner<16> / <32>.
+template <int R>
+__device__ inline float row_to_row0(float v) {
+  static_assert(R >= 0 && R < 4, "row");
+  const unsigned x = (unsigned)__float_as_int(v);
+  if constexpr (R == 0) {
+    return v;
+  } else if constexpr (R == 1) {
+    return __int_as_float((int)__builtin_amdgcn_permlane16_swap(x, x, false, false)[1]);
+  } else if constexpr (R == 2) {
+    return __int_as_float((int)__builtin_amdgcn_permlane32_swap(x, x, false, false)[1]);
+  } else {
+    const unsigned hi = __builtin_amdgcn_permlane32_swap(x, x, false, false)[1];  // row 1: row 3
+    return __int_as_float((int)__builtin_amdgcn_permlane16_swap(hi, hi, false, false)[1]);
+  }
+}
+
+// lane i of row 0 receives lane i + H of the same row (DPP row_shl:H)
+template <int H>
+__device__ inline float row_shl(float v) {
+  const int x = __float_as_int(v);
+  return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x100 + H, 0xF, 0xF, false));
 }
 
 // One element of a cross-lane FWHT stage of stride ST: the lane with bit ST
@@ -409,6 +449,119 @@ __device__ inline bool find_mtile(const int32_t* __restrict__ eo, int E, int BM,
     carry += __shfl(inc, 63, kWave);
   }
   return false;
+}
+
+// ---------------------------------------------------------------------------
+// Norm-quant in the pair layout (hidden % 256 == 0, so the reference's sum of
+// squares runs on pu = 8 port-unrolled accumulators, i.e. 128 chains).  Lane
+// L holds the bf16 pair (128 q + 2 L, 128 q + 2 L + 1) of every 128-value
+// segment q -- one coalesced 4-byte load per segment -- and with it exactly
+// the pairs of chains L (segments 0, 2, 4, ...) and L + 64 (segments 1, 3,
+// 5, ...), in chain order (rms_reduce_row, butterquant/runtime.mojo:11-37:
+// chain c takes pairs c, c + 128, c + 256, ...; odd element first).  The
+// FWHT of block B: stride 1 inside the pair, strides 2 .. 64 across lanes
+// (lane ^ s/2), strides 128 and 256 across segments, ascending.  Shared by
+// k_norm_quant_pair and the fused norm-quant + linear kernel.
+
+// sum of squares of the row whose pairs xp holds (every segment < nseg), in
+// the reference's order: the 128 chains, then s_j = sum over p of chain
+// p*16 + j in p order, then the 16-lane halving tree; all 64 lanes active
+template <int NSEG>
+__device__ inline float nq_pair_sumsq(const uint32_t (&xp)[NSEG], int nseg) {
+  float a0 = 0.0f, a1 = 0.0f;  // chains L (even segments) and L + 64 (odd)
+#pragma unroll
+  for (int q = 0; q < NSEG; q += 2) {
+    if (q >= nseg) break;
+    const float o0 = __uint_as_float(xp[q] & 0xFFFF0000u), e0 = __uint_as_float(xp[q] << 16);
+    const float o1 = __uint_as_float(xp[q + 1] & 0xFFFF0000u), e1 = __uint_as_float(xp[q + 1] << 16);
+    a0 = fmaf(o0, o0, a0);
+    a0 = fmaf(e0, e0, a0);
+    a1 = fmaf(o1, o1, a1);
+    a1 = fmaf(e1, e1, a1);
+  }
+  // lanes 0..15 (row 0) take chains p*16 + j: rows 0..3 of a0, then of a1
+  float sum = 0.0f;
+  sum = sum + row_to_row0<0>(a0);
+  sum = sum + row_to_row0<1>(a0);
+  sum = sum + row_to_row0<2>(a0);
+  sum = sum + row_to_row0<3>(a0);
+  sum = sum + row_to_row0<0>(a1);
+  sum = sum + row_to_row0<1>(a1);
+  sum = sum + row_to_row0<2>(a1);
+  sum = sum + row_to_row0<3>(a1);
+  sum = sum + row_shl<8>(sum);
+  sum = sum + row_shl<4>(sum);
+  sum = sum + row_shl<2>(sum);
+  sum = sum + row_shl<1>(sum);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sum)));  // lane 0
+}
+
+// x * inv_rms * gamma of this wave's SPW segments q0 .. q0 + SPW - 1 (pairs
+// x[i], gains g[i]; segments >= nseg give 0), the FWHT of block B, times
+// fwht_scale, into v; returns the wave-local max |v|
+template <int SPW>
+__device__ inline float nq_pair_transform(const uint32_t (&x)[SPW], const uint32_t (&g)[SPW],
+                                          float inv_rms, int q0, int nseg, int block,
+                                          float fwht_scale, float (&v)[SPW][2]) {
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    if (q0 + i < nseg) {
+      const float e = __uint_as_float(x[i] << 16), o = __uint_as_float(x[i] & 0xFFFF0000u);
+      const float ge = __uint_as_float(g[i] << 16), go = __uint_as_float(g[i] & 0xFFFF0000u);
+      v[i][0] = e * inv_rms * ge;
+      v[i][1] = o * inv_rms * go;
+    } else {
+      v[i][0] = v[i][1] = 0.0f;
+    }
+  }
+  // stride 1 inside the pair
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const float x0 = v[i][0], x1 = v[i][1];
+    v[i][0] = x0 + x1;
+    v[i][1] = x0 - x1;
+  }
+  // strides 2 .. min(B/2, 64) across lanes: element bit k is lane bit k - 1
+  auto lanes = [&](auto st) {
+    constexpr int ST = decltype(st)::value;
+    if (block > 2 * ST) {
+#pragma unroll
+      for (int i = 0; i < SPW; ++i)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) v[i][r] = xlane_bfly<ST>(v[i][r]);
+    }
+  };
+  lanes(Stride<1>{}); lanes(Stride<2>{}); lanes(Stride<4>{});
+  lanes(Stride<8>{}); lanes(Stride<16>{}); lanes(Stride<32>{});
+  // strides 128 and 256 across segments (SPW and q0 are multiples of B/128)
+#pragma unroll
+  for (int ss = 1; ss <= 2; ss <<= 1) {
+    if (block <= 128 * ss) break;
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      if ((i & ss) || i + ss >= SPW) continue;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float x0 = v[i][r], x1 = v[i + ss][r];
+        v[i][r] = x0 + x1;
+        v[i + ss][r] = x0 - x1;
+      }
+    }
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      v[i][r] = v[i][r] * fwht_scale;
+      m = fmaxf(m, fabsf(v[i][r]));
+    }
+  return m;
+}
+
+// the int8 code pair of v[i] (low byte: the even element)
+__device__ inline uint16_t nq_pair_code(const float (&vi)[2], float inv) {
+  return (uint16_t)((uint8_t)quantize_i8(vi[0], inv) | ((uint16_t)(uint8_t)quantize_i8(vi[1], inv) << 8));
 }
 
 }  // namespace bq

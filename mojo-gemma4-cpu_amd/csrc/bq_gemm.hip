@@ -229,4 +229,140 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
   return launch_linear_tiled(a, per_block, bm, st);
 }
 
+// ---------------------------------------------------------------------------
+// norm-quant + per-row linear of one token (decode) in one launch
+// ---------------------------------------------------------------------------
+// What bq_norm_quant followed by bq_linear / bq_qkv on its output computes,
+// for seq_len 1.  Each workgroup of 8 waves loads the token's row, requests
+// its weight fragments (k_linear_skinny<8, false, 8>'s one-shot slices,
+// K <= 4096) and quantizes the row itself while they are in flight: every
+// wave takes the sum of squares over the whole row (nq_pair_sumsq's chain
+// order) and transforms its SPW segments (nq_pair_transform), the amax is
+// exchanged through LDS, and the int8 codes land in LDS, where the A operand
+// is read from.  Every workgroup
+// computes the same codes and scale; workgroup 0 also writes them to
+// x_i8 / x_sa.  Two launches become one, and the norm-quant's memory round
+// trips overlap the weight stream instead of preceding it.
+template <int NSEG, int SPW>
+__global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormArgs nq) {
+  constexpr int WAVES = 8, U = 8;
+  __shared__ __attribute__((aligned(16))) int8_t s_x[64 * WAVES * U];  // the row's codes
+  __shared__ int lds[WAVES * 256];
+  __shared__ float s_f[WAVES];  // per-wave amax
+  int nt;
+  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
+  const int K = args.K, K64 = K >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int per = (K64 + WAVES - 1) / WAVES;
+  const int kt0 = min(K64, wave * per), kt1 = min(K64, kt0 + per);
+  // The row's loads go out before the weights: loads return in issue order,
+  // so the norm-quant's operands must not queue behind the weight stream.
+  // Every wave loads the whole row and takes its sum of squares (as
+  // k_norm_quant_pair does: no barrier before the transform).
+  const int nseg = K >> 7, q0 = wave * SPW, wpt = (nseg + SPW - 1) / SPW;
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(nq.src) + lane;
+  const uint32_t* gr = reinterpret_cast<const uint32_t*>(nq.gamma) + lane;
+  // (the wave's own segments are loaded again, into x: cheaper than picking
+  // them out of xp by a run-time index)
+  uint32_t xp[NSEG], x[SPW], g[SPW];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)  // first: the sum of squares needs it first
+    if (q < nseg) xp[q] = xr[64 * q];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const bool in = q0 + i < nseg;
+    x[i] = in ? xr[64 * (q0 + i)] : 0u;
+    g[i] = in ? gr[64 * (q0 + i)] : 0u;
+  }
+  // epilogue: thread t < 16 owns row 0's column t (accumulator element v = 0
+  // of lanes 0..15); its weight scale is fetched now
+  const int t = threadIdx.x;
+  const float ews = seg.ws[nt * 16 + (t & 15)];
+  asm volatile("" ::: "memory");  // keep the weight loads after these
+  const int8_t* wb = seg.w + (size_t)nt * K64 * 1024 + lane * 16;
+  v4i bf[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    bf[u] = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(wb + (size_t)min(kt0 + u, max(kt1 - 1, 0)) * 1024));
+
+  // ---- the row's norm-quant ------------------------------------------------
+  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
+  const float inv_rms = nq.sqrt_n / __builtin_sqrtf(total + nq.n_eps);
+  float v[SPW][2];
+  const float m = nq_pair_transform<SPW>(x, g, inv_rms, q0, nseg, nq.block, nq.fwht_scale, v);
+  const float wmax = wave_max(m);
+  if (lane == 0) s_f[wave] = wmax;
+  __syncthreads();
+  float amax = s_f[0];
+  for (int w = 1; w < wpt; ++w) amax = fmaxf(amax, s_f[w]);
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  uint16_t* sx = reinterpret_cast<uint16_t*>(s_x) + lane;
+  uint16_t* gx = reinterpret_cast<uint16_t*>(nq.xq) + lane;
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    if (q0 + i < nseg) {
+      const uint16_t c = nq_pair_code(v[i], inv);
+      sx[64 * (q0 + i)] = c;
+      if (blockIdx.x == 0) gx[64 * (q0 + i)] = c;
+    }
+  }
+  if (blockIdx.x == 0 && t == 0) nq.sa[0] = amax;
+  __syncthreads();
+
+  // ---- the product (k_linear_skinny's per-row one-shot path, M = 1) ---------
+  const v4i zero = {0, 0, 0, 0};
+  v4i c = zero, c1 = zero;  // two independent chains of exact int32 sums
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (kt0 + u < kt1) {
+      const v4i af = *reinterpret_cast<const v4i*>(&s_x[(kt0 + u) * 64 + (lane >> 4) * 16]);
+      if (u & 1) c1 = mfma16x16x64(af, bf[u], c1);
+      else c = mfma16x16x64(af, bf[u], c);
+    }
+  }
+  c += c1;
+  lds[wave * 256 + lane] = c.x;  // element v = 0: row 0 for lanes 0..15
+  __syncthreads();
+  if (t >= 16) return;
+  int acc = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) acc += lds[w * 256 + t];
+  const float y = (float)acc * (amax * kInv127) * ews;
+  const int n = nt * 16 + t;
+  seg.out[n] = f32_to_bf16(y);
+  if (seg.out_f32) seg.out_f32[n] = y;
+}
+
+// the fused kernel's shapes: one token, the pair-layout norm-quant's shapes
+// (hidden % 256 == 0, hidden <= 4096), per-row weights
+static bool launch_norm_linear_fused(const LinArgs& a, const NormArgs& nq, hipStream_t st) {
+  if (a.M != 1 || a.K % 256 || a.K > 4096 || !tune().nq_pair ||
+      (reinterpret_cast<uintptr_t>(nq.xq) & 1u))
+    return false;
+  int tiles = 0;
+  for (int q = 0; q < a.nseg; ++q) tiles += a.seg[q].n / 16;
+  const int ns = a.K >> 7;
+  const int unit = nq.block > 128 ? nq.block / 128 : 1;
+  int spw = (ns + 7) / 8;
+  spw = (spw + unit - 1) / unit * unit;
+  const dim3 g(tiles), b(512);
+#define BQ_NL(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_linear_skinny<N, S>), g, b, 0, st, a, nq); return true; }
+  BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
+  BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
+#undef BQ_NL
+  return false;
+}
+
+hipError_t launch_norm_linear(const LinArgs& a, const NormArgs& nq_in, hipStream_t st) {
+  if (a.M <= 0) return hipSuccess;
+  NormArgs nq = nq_in;
+  nq.fwht_scale = fwht_scale_host(nq.block);
+  if (launch_norm_linear_fused(a, nq, st)) return hipGetLastError();
+  const hipError_t e = launch_norm_quant(nq.src, nq.gamma, nq.xq, nq.sa, a.M, a.K, nq.block,
+                                         nq.sqrt_n, nq.n_eps, st);
+  if (e != hipSuccess) return e;
+  return launch_linear(a, 0, st);
+}
+
 }  // namespace bq

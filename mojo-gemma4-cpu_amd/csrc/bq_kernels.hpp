@@ -72,6 +72,18 @@ hipError_t launch_block_quant(const uint16_t* src, int8_t* xq, float* sa, int ro
 // per_block = 0: y = f32(acc) * (sa[m]/127) * ws[n]
 // per_block = 1: y = ws[n] * sum_b fma-chain f32(acc_b) * (sa[m,b]/127)
 hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st);
+// bq_norm_quant of a.act's source rows followed by the per-row linear a
+// (a.act / a.sa are nq.xq / nq.sa): one fused launch for one token, else the
+// two launches
+struct NormArgs {
+  const uint16_t* src;    // bf16 [M, K]
+  const uint16_t* gamma;  // bf16 [K]
+  int8_t* xq;             // int8 [M, K] codes (written)
+  float* sa;              // [M] amax (written)
+  int block;              // FWHT block
+  float sqrt_n, n_eps, fwht_scale;  // fwht_scale: set by the launcher
+};
+hipError_t launch_norm_linear(const LinArgs& a, const NormArgs& nq, hipStream_t st);
 
 struct Route { int32_t token; float weight; };
 

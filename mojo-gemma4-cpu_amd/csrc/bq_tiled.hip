@@ -76,6 +76,31 @@ __device__ inline uint32_t lds_addr(const int8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
 }
 
+// The (m-tile, n-tile) item of this workgroup in the grouped MoE launches
+// (grid from moe_grid); false past the last item.  XCD-aware orders: the
+// hardware places workgroup b on XCD b % 8.  Order 1: XCD x takes the
+// contiguous work range [x*G/8, (x+1)*G/8) of (m-tile major, n-tile minor)
+// items, so the n-tiles sharing one gathered activation tile, and the
+// consecutive m-tiles of one expert sharing its weight tiles, meet in the
+// same L2.  Order 2: an m-tile's n-tiles on one XCD, consecutive m-tiles on
+// different XCDs.  Order 0: workgroup order.
+__device__ inline bool moe_item(const TiledArgs& args, int& mt, int& nt) {
+  const int total = args.gm * args.gn, per_xcd = (int)gridDim.x >> 3;
+  if (args.order == 1) {
+    const int work = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    mt = work / args.gn; nt = work % args.gn;
+    return work < total;
+  }
+  if (args.order == 2) {
+    const int xcd = (int)(blockIdx.x & 7), k = (int)(blockIdx.x >> 3);
+    mt = xcd + 8 * (k / args.gn); nt = k % args.gn;
+    return mt < args.gm;
+  }
+  const int work = (int)blockIdx.x;
+  mt = work / args.gn; nt = work % args.gn;
+  return work < total;
+}
+
 // A stage covers 128 bytes of K (two MFMA k-steps of 64).
 //   A: BM/8 DMAs, each 8 rows x 128 B, so every DMA reads whole 128-byte
 //      lines (a DMA of 16 rows x 64 B -- the raw MFMA fragment -- moves a
@@ -158,27 +183,8 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
     n0 = nt_in * BN;
     wbase = seg->w;
   } else {
-    // XCD-aware order: hardware places workgroup b on XCD b % 8, so XCD x
-    // takes the contiguous work range [x*G/8, (x+1)*G/8) of (m-tile major,
-    // n-tile minor) items.  The n-tiles sharing one gathered activation tile,
-    // and the consecutive m-tiles of one expert sharing its weight tiles, then
-    // meet in the same L2.
-    const int total = args.gm * args.gn, per_xcd = (int)gridDim.x >> 3;
     int mt, nt;
-    if (args.order == 1) {
-      const int work = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
-      if (work >= total) return;
-      mt = work / args.gn; nt = work % args.gn;
-    } else if (args.order == 2) {
-      // m-tile's n-tiles on one XCD, consecutive m-tiles on different XCDs
-      const int xcd = (int)(blockIdx.x & 7), k = (int)(blockIdx.x >> 3);
-      mt = xcd + 8 * (k / args.gn); nt = k % args.gn;
-      if (mt >= args.gm) return;
-    } else {
-      const int work = (int)blockIdx.x;
-      if (work >= total) return;
-      mt = work / args.gn; nt = work % args.gn;
-    }
+    if (!moe_item(args, mt, nt)) return;
     if (!find_mtile(args.eo, args.E, BM, mt, args.max_routes, e, r0, r1)) return;
     K = args.K;
     n0 = nt * (MODE == MODE_GATE_UP ? BN / 2 : BN);
@@ -934,6 +940,8 @@ hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const
   t.E = experts; t.max_routes = max_routes; t.N = 2 * inter; t.K = hidden;
   t.inter = inter; t.block = hidden;
   const int bmv = bm >= 256 ? 256 : bm >= 192 ? 192 : bm >= 128 ? 128 : 64;
+  t.gm = mtile_bound(max_routes, experts, bmv);
+  t.order = tune().moe_order;
   // weight rows per tile: bn/2 gate + bn/2 up.  256-record tiles pair with
   // 256 weight rows; 192-record tiles (2048 tokens x top-8 over 128 experts)
   // with 128, whose 80 KB ring leaves room for two workgroups per CU
@@ -941,8 +949,6 @@ hipError_t launch_moe_gate_up_tiled(const int8_t* x_i8, const float* x_sa, const
   const int bn = tile_bn(or_default(tune().tile_bn, bmv == 256 ? 256 : 128));
   const int nbuf = or_default(tune().ring, 2);
   t.gn = (inter + bn / 2 - 1) / (bn / 2);
-  t.gm = mtile_bound(max_routes, experts, bmv);
-  t.order = tune().moe_order;
   const dim3 g(moe_grid(t));
   launch_bm<MODE_GATE_UP, false>(bmv, bn, nbuf, g, 0, st, t);
   return hipGetLastError();

@@ -93,6 +93,16 @@ def test_validation_errors(L):
                                 C.c_void_p(256), 0, None) == 2
     assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
                                 C.c_void_p(100), 1 << 30, None) == 1
+    f1 = C.c_float(1)
+    nl = lambda *a: L.bq_norm_linear(*a, f1, f1, None)
+    assert nl(P, P, P, P, P, P, P, None, 256, 1, 2816, 48) == 2        # FWHT block
+    assert nl(P, P, P, P, P, P, P, None, 250, 1, 2816, 128) == 2       # n_rows % 16
+    assert nl(P, P, P, P, P, P, P, None, 256, 1, 2880, 128) == 2       # hidden % block
+    assert nl(P, P, None, P, P, P, P, None, 256, 1, 2816, 128) == 1    # x_i8
+    assert nl(P, P, P, P, None, P, P, None, 256, 1, 2816, 128) == 1    # weights
+    assert nl(P, P, C.c_void_p(264), P, P, P, P, None, 256, 1, 2816, 128) == 1  # alignment
+    assert L.bq_norm_qkv(*([P] * 13), 4096, 2050, 1, 2816, 128, f1, f1, None) == 2
+    assert L.bq_norm_qkv(*([P] * 12), None, 4096, 2048, 1, 2816, 128, f1, f1, None) == 1
 
 
 
@@ -140,6 +150,10 @@ def test_empty_batches_are_noops(L):
     assert L.bq_sliding_attention(*([None] * 9), 0, None, 1, None, 16, 8, 256, 1024, 10, 1023, 1,
                                   1, 0, None) == 0
     assert L.bq_qkv(*([None] * 11), 256, 128, 0, 2816, None) == 0
+    assert L.bq_norm_linear(*([None] * 8), 256, 0, 2816, 128, C.c_float(1), C.c_float(1),
+                            None) == 0
+    assert L.bq_norm_qkv(*([None] * 13), 256, 128, 0, 2816, 128, C.c_float(1), C.c_float(1),
+                         None) == 0
     assert L.bq_moe_build_schedule(None, None, 0, 8, 0, 128, None, None, None) == 0
     assert L.bq_moe_phase1_gate_up(*([None] * 7), 128, 0, 8, 2816, 704, None) == 0
     assert L.bq_head_prep(None, None, None, None, 0, 2816, 128, C.c_float(1), C.c_float(1),

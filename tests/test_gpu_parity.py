@@ -255,6 +255,57 @@ def test_qkv_matches_three_linears(gpu, O, M):
         np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
 
 
+@pytest.mark.parametrize("M,K,N,B", [(1, 2816, 256, 128), (1, 4096, 512, 128), (1, 2816, 128, 256),
+                                     (1, 4096, 256, 512), (1, 512, 256, 64), (1, 1024, 128, 512),
+                                     (1, 2304, 256, 256), (1, 768, 128, 16), (3, 2816, 256, 128),
+                                     (1, 8192, 128, 256), (1, 2112, 128, 64)])
+def test_norm_linear(gpu, O, M, K, N, B):
+    """The fused norm-quant + linear (one launch for one token of hidden % 256
+    == 0 up to 4096, else the two launches) against the oracle's norm-quant and
+    linear: codes, amax and both outputs bit-exact."""
+    q, s, W = weight(gpu, O, N, K, 128 if K % 128 == 0 else 64, seed=3)
+    p, cs = O.pack_and_colsum(q)
+    x = O.synth_normal_bf16(7, 1.0, (M, K))
+    g = O.f32_to_bf16(O.synth_normal_f32(9, 0.3, (K,)) + 1.0)
+    (ob, of), (xq, sa) = gpu.norm_linear(dev(x), dev(g), W, B, want_f32=True)
+    rq, rsa = O.norm_quant(x, g, B)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(xq), rq)
+    rb, rf = O.linear(rq, rsa, p, s, cs, N)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
+def test_norm_linear_zero_row(gpu, O):
+    """An all-zero token: amax 0, codes 0, outputs 0, as the two calls give."""
+    K, N = 2816, 128
+    W = weight(gpu, O, N, K, 128, seed=3)[2]
+    x = np.zeros((1, K), np.uint16)
+    g = np.full(K, ONE, np.uint16)
+    ob, (xq, sa) = gpu.norm_linear(dev(x), dev(g), W, 128)
+    rq, rsa = O.norm_quant(x, g, 128)
+    np.testing.assert_array_equal(host(sa), rsa)
+    np.testing.assert_array_equal(host(xq), rq)
+    xq2, sa2 = gpu.norm_quant(dev(x), dev(g), 128)
+    np.testing.assert_array_equal(host(ob), host(gpu.linear(xq2, sa2, W)))
+
+
+@pytest.mark.parametrize("M,K,qn,kvn", [(1, 2816, 4096, 2048), (1, 512, 256, 128),
+                                        (2, 2816, 256, 128)])
+def test_norm_qkv(gpu, O, M, K, qn, kvn):
+    """Fused norm-quant + q|k|v (the decoder's attention input at hidden 2816,
+    q 4096 / k, v 2048) against bq_norm_quant then bq_qkv: bit-exact."""
+    Ws = [weight(gpu, O, n, K, 128, seed=sd)[2] for n, sd in ((qn, 1), (kvn, 2), (kvn, 3))]
+    x = O.synth_normal_bf16(8, 1.0, (M, K))
+    g = O.f32_to_bf16(O.synth_normal_f32(4, 0.3, (K,)) + 1.0)
+    outs, (xq, sa) = gpu.norm_qkv(dev(x), dev(g), *Ws, block=128)
+    xq2, sa2 = gpu.norm_quant(dev(x), dev(g), 128)
+    np.testing.assert_array_equal(host(xq), host(xq2))
+    np.testing.assert_array_equal(host(sa), host(sa2))
+    for o, o2 in zip(outs, gpu.qkv(xq2, sa2, *Ws)):
+        np.testing.assert_array_equal(host(o), host(o2))
+
+
 @pytest.mark.parametrize("M", [1, 512])
 def test_linear_full_size(gpu, O, M):
     """Config sizes K = N = 4096: all rows against an exact f64 integer matmul
@@ -296,14 +347,15 @@ def test_build_schedule(gpu, O, T):
 
 
 @pytest.mark.parametrize("T,E,k,pes", [(1, 128, 8, False), (5, 128, 8, True), (16, 60, 8, False),
-                                      (16, 256, 16, True), (32, 128, 8, True),
+                                      (16, 256, 16, True), (32, 128, 8, True), (8, 60, 8, True),
+                                      (8, 256, 16, False), (9, 128, 8, False),
                                       (128, 128, 8, False), (129, 128, 8, True),
                                       (2048, 128, 8, True), (40, 60, 2, False),
                                       (64, 256, 16, True), (300, 8, 2, False),
                                       (1000, 64, 1, False), (200, 128, 4, True)])
 def test_route_schedule(gpu, O, T, E, k, pes):
     """the fused route top-k + schedule equals the two calls and the oracle:
-    one workgroup up to 16 tokens (E <= 64, <= 128, <= 256 instances), the
+    one workgroup up to 8 tokens (E <= 64, <= 128, <= 256 instances), the
     two kernels above"""
     logits = O.synth_normal_f32(7 + T, 1.0, (T, E))
     sc = O.f32_to_bf16(O.synth_normal_f32(8, 0.2, (E,)) + 1.0) if pes else None
