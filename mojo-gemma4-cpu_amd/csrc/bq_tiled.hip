@@ -572,14 +572,21 @@ __global__ __launch_bounds__(64 * WM * WN * KSP) void k_tiled(TiledArgs args) {
 // layout of k_tiled, one 128-byte stage after another -- is DMA'd into LDS
 // when the item's m-tile changes, with its per-block scales and route
 // weights.  Weights: each of the 8 waves owns NI 16-column strips of the
-// item's n-tile and holds all K of them in VGPRs; as soon as a k-step's
-// fragments have been multiplied they are reloaded with the next item's, so
-// the weight stream runs without a break and the bytes in flight per CU are
+// item's n-tile and holds all K of them in VGPRs; they are reloaded with the
+// next item's during the item's last m-subtile pair, each k-step's registers
+// as soon as that pair has multiplied them, so the bytes in flight per CU are
 // bounded by the register file (8 waves x NI x K/64 KiB), not by LDS.
 //
-// Every k-step is one drain block: its int32 product (an MFMA from zero) is
-// added to the f32 accumulator as fmaf(f32(dot), a_scale/127, acc), k-steps
-// in ascending order -- the per-block order of k_tiled's DOWN mode.
+// m-subtile pairs are the outer loop: a pair runs its k-steps in order, then
+// stores its records, so only two subtiles' accumulators are live (no
+// spills).  Every k-step is one drain block: its int32 product (an MFMA from
+// zero) is added to the f32 accumulator as fmaf(f32(dot), a_scale/127, acc),
+// k-steps in ascending order -- the per-block order of k_tiled's DOWN mode.
+// The product is taken transposed, D = W x A^T (the weight strip as the
+// MFMA's A operand, 16 records as its B): lane L holds columns 4 (L/16) ..
+// +3 of the strip for record L % 16, so a drain needs one activation scale
+// per lane (a 4-byte LDS read, not 16) and a record's four y values are one
+// 16-byte store.  The integer dot of each (record, column) is the same.
 constexpr int kBregMaxExperts = 256;
 
 template <int MI, int NI, int KMAX>
@@ -658,16 +665,19 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
       for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb, ns0, j, ks);
   }
 
-  // per-column weight scales of an item's strips
-  auto load_ep = [&](int item, float (&ep)[NI]) {
+  // per-column weight scales of an item's strips: lane L's columns
+  // 4 (L/16) .. +3 of each strip (the transposed product's layout)
+  float ep4[NI][4];
+  auto load_ep4 = [&](int item) {
     const int mt = item / args.gn, nt = item - mt * args.gn;
     const int e = expert_of(mt), ns0 = nt * (BN / 16) + wave * NI;
 #pragma unroll
     for (int j = 0; j < NI; ++j)
-      ep[j] = args.ws[(size_t)e * N + min((ns0 + j) * 16 + (lane & 15), N - 1)];
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ep4[j][v] = args.ws[(size_t)e * N + min((ns0 + j) * 16 + 4 * (lane >> 4) + v, N - 1)];
   };
-  float ep_col[NI];
-  load_ep(first, ep_col);
+  load_ep4(first);
 
   int cur_mt = -1, lds_mt = -1, r0 = 0, r1 = 0, nmi = 0;
   const uint32_t a_lds = lds_addr(abuf);
@@ -726,6 +736,8 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
         }
       }
       if (tid < BM) s_rw[tid] = rwv;
+      // k-steps K/64 .. KMAX-1 (multiplied without a branch) scale by 0
+      for (int i = nsc + tid; i < BM * KMAX; i += 64 * NW) sa[i] = 0.0f;
       asm volatile("" :: "v"(sv[0]));  // the first scale (and so every DMA) has landed
       lds_barrier();
     }
@@ -734,73 +746,83 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
     int ns0_n;
     strips(item + 1 < last ? item + 1 : item, wb_n, ns0_n);
 
-    // ---- multiply: k-steps in order, m-subtiles in pairs ------------------
-    float facc[MI][NI][4];
+    // ---- multiply: m-subtile pairs, each with its k-steps in order; the
+    // last pair (or, for an m-tile with no record, a pair that multiplies
+    // nothing) reloads each k-step's weight registers with the next item's
+    // once it has multiplied them: straight-line, unconditional loads
+    auto pair = [&](int mp, auto last_tag) {
+      constexpr bool LAST = decltype(last_tag)::value;
+      const bool active = mp < nmi;
+      float facc[2][NI][4];
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
+        for (int j = 0; j < NI; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) facc[mi][j][v] = 0.0f;
+          for (int v = 0; v < 4; ++v) facc[h][j][v] = 0.0f;
+      // one branch per pair, none per k-step: k-steps past K/64 multiply
+      // stale LDS rows by a zero scale, which leaves facc bit for bit
+      // (facc is never -0)
+      if (active) {  // wave-uniform
 #pragma unroll
-    for (int ks = 0; ks < KMAX; ++ks) {
-      const int st = ks >> 1, c = (ks & 1) * 4 + (lane >> 4);
-#pragma unroll
-      for (int mp = 0; mp < MI; mp += 2) {
-        // a pair past the tile's last record is skipped; the odd one out of
-        // a partial pair multiplies rows whose scales are 0
-        if (ks < K64 && mp < nmi) {  // wave-uniform
+        for (int ks = 0; ks < KMAX; ++ks) {
+          const int st = ks >> 1, c = (ks & 1) * 4 + (lane >> 4);
           v4i a[2];
-          float4 adv[2];
+          float adv[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int m = (mp + h) * 16 + (lane & 15), bb = m >> 3, r = m & 7;
             a[h] = *reinterpret_cast<const v4i*>(
                 &abuf[(st * FA + bb) * 1024 + r * 128 + ((c ^ r ^ (bb & 1)) * 16)]);
-            adv[h] = *reinterpret_cast<const float4*>(
-                &sa[ks * BM + (mp + h) * 16 + 4 * (lane >> 4)]);
+            adv[h] = sa[ks * BM + m];
           }
           v4i t[2][NI];
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int j = 0; j < NI; ++j) t[h][j] = mfma16x16x64(a[h], bw[ks][j], zero);
+            for (int j = 0; j < NI; ++j) t[h][j] = mfma16x16x64(bw[ks][j], a[h], zero);
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int j = 0; j < NI; ++j) {
-              float* f = facc[mp + h][j];
-              f[0] = fmaf((float)t[h][j][0], adv[h].x, f[0]);
-              f[1] = fmaf((float)t[h][j][1], adv[h].y, f[1]);
-              f[2] = fmaf((float)t[h][j][2], adv[h].z, f[2]);
-              f[3] = fmaf((float)t[h][j][3], adv[h].w, f[3]);
-            }
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                facc[h][j][v] = fmaf((float)t[h][j][v], adv[h], facc[h][j][v]);
+          if constexpr (LAST) {
+#pragma unroll
+            for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb_n, ns0_n, j, ks);
+          }
         }
+      } else if constexpr (LAST) {
+#pragma unroll
+        for (int ks = 0; ks < KMAX; ++ks)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb_n, ns0_n, j, ks);
       }
+      // y[rec, n] = (facc * ws[n]) * route_w of the pair's records
 #pragma unroll
-      for (int j = 0; j < NI; ++j) bw[ks][j] = load_strip(wb_n, ns0_n, j, ks);
-    }
-
-    // ---- epilogue: y[rec, n] = (facc * ws[n]) * route_w -------------------
-    // (the column scales are waited for once here, not before every store:
-    // a wait inside the guarded stores would also wait for the stores)
-    asm volatile("" :: "v"(ep_col[0]), "v"(ep_col[NI - 1]));
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = r0 + mi * 16 + 4 * (lane >> 4) + v;
-        if (mi < nmi && row < r1) {
+      for (int h = 0; h < 2; ++h) {
+        const int row = r0 + (mp + h) * 16 + (lane & 15);
+        if (mp + h < nmi && row < r1) {
           const float rw = s_rw[row - r0];
 #pragma unroll
           for (int j = 0; j < NI; ++j) {
-            const int col = (ns0 + j) * 16 + (lane & 15);
-            if (col < N) args.y[(size_t)row * N + col] = facc[mi][j][v] * ep_col[j] * rw;
+            const int col = (ns0 + j) * 16 + 4 * (lane >> 4);
+            if (col < N)
+              *reinterpret_cast<float4*>(&args.y[(size_t)row * N + col]) =
+                  float4{facc[h][j][0] * ep4[j][0] * rw, facc[h][j][1] * ep4[j][1] * rw,
+                         facc[h][j][2] * ep4[j][2] * rw, facc[h][j][3] * ep4[j][3] * rw};
           }
         }
       }
-    }
-    if (item + 1 < last) load_ep(item + 1, ep_col);
+    };
+    const int npair = (nmi + 1) >> 1;
+    // (the column scales are waited for once here, before any pair's
+    // stores: a wait inside the guarded stores would also wait for them)
+    asm volatile("" :: "v"(ep4[0][0]), "v"(ep4[NI - 1][3]));
+    for (int p = 0; p + 1 < npair; ++p) pair(2 * p, std::false_type{});
+    pair(2 * max(npair - 1, 0), std::true_type{});
+    if (item + 1 < last) load_ep4(item + 1);
   }
 }
 
@@ -964,8 +986,10 @@ hipError_t launch_moe_down_tiled(const int8_t* b_i8, const float* b_sa, const in
   t.block = block;
   // block-64 scales and K up to 704 (the model's inter): weights in registers,
   // 192-record m-tiles x 256 columns
+  // (hidden % 16 == 0 and a 16-byte aligned y: its lanes store four
+  // consecutive columns at once)
   if (block == 64 && inter % 64 == 0 && inter / 64 <= 11 && experts <= kBregMaxExperts &&
-      tune().down_breg) {
+      hidden % 16 == 0 && !(reinterpret_cast<uintptr_t>(y) & 15u) && tune().down_breg) {
     constexpr int MI = 12, NI = 2;
     t.gn = (hidden + 8 * NI * 16 - 1) / (8 * NI * 16);
     hipLaunchKernelGGL((k_down_breg<MI, NI, 11>), dim3(tune().cus), dim3(512), 0, st, t);
