@@ -279,7 +279,34 @@ def bench_prefill(bq, torch, steps, warmup, reps=32):
     tops = ops / (smp.p50 * 1e-3) / 1e12
     return dict(s=smp, ops=ops, tops=tops, int8_frac=tops / INT8_PEAK_TOPS,
                 bf16_frac=tops / BF16_PEAK_TFLOPS,
-                alg_bytes=N * K + N * 4 + M * K + M * 4 + M * N * 2)
+                alg_bytes=N * K + N * 4 + M * K + M * 4 + M * N * 2,
+                vendor=vendor_gemm(torch, M, N, K, reps))
+
+
+def vendor_gemm(torch, M, N, K, reps):
+    """The same product through the vendor library (hipBLASLt behind torch),
+    timed the same way over the same number of weight replicas: int8 x int8
+    -> int32 (torch._int_mm, the weight as a transposed [K, N] view, its
+    fastest layout here) and bf16 x bf16 -> bf16 (torch.mm).  Neither applies
+    the butterquant scales: a reference point for the product alone."""
+    g0 = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.randint(-127, 128, (M, K), generator=g0, dtype=torch.int8, device="cuda")
+    ws = [torch.randint(-127, 128, (N, K), generator=g0, dtype=torch.int8, device="cuda")
+          for _ in range(reps)]
+    res = {}
+    try:
+        o = torch.empty(M, N, dtype=torch.int32, device="cuda")
+        s = time_graph(graph_of(lambda i: torch._int_mm(a, ws[i].t(), out=o), reps), reps, 0, 0)
+        res["int8_int_mm_p50_us"] = round(s.p50 * 1e3, 2)
+    except Exception as e:  # an unsupported shape or build: report it, time the rest
+        res["int8_int_mm_error"] = str(e)[:200]
+    ab = a.to(torch.bfloat16)
+    wb = [w.to(torch.bfloat16) for w in ws]
+    ob = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    s = time_graph(graph_of(lambda i: torch.mm(ab, wb[i].t(), out=ob), reps), reps, 0, 0)
+    res["bf16_mm_p50_us"] = round(s.p50 * 1e3, 2)
+    res["library"] = "hipBLASLt via torch " + torch.__version__
+    return res
 
 
 class MoeLayer:
@@ -957,7 +984,8 @@ def main():
                          "traffic": _traffic("prefill_gemm_m512_k4096_n4096_stats.txt"),
                          "measured_peak": mf,
                          "frac_of_measured": round(p["tops"] / mf, 4) if mf else None,
-                         "basis": "2*M*N*K int8 ops / p50 launch time; peak = dense int8 MFMA"}}
+                         "basis": "2*M*N*K int8 ops / p50 launch time; peak = dense int8 MFMA"},
+            "vendor_same_shape": p["vendor"]}
     for key in ("moe32", "moe2048"):
         if key in res:
             m = res[key]

@@ -241,7 +241,11 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 // scales (16 records x K/block <= 64) are staged in LDS up front.  A wave
 // owns NS 16-row strips of the output: the records' activation fragments
 // are loaded once per k-step for all of them, and NS weight fragments per
-// k-step are in flight.
+// k-step are in flight.  The product is taken transposed, D = W x A^T (the
+// weight strip as the MFMA's A operand, the 16 records as its B): lane L
+// holds columns 4 (L/16) .. +3 of a strip for record L % 16, so a drain
+// reads one activation scale per lane and a record's four y values are one
+// 16-byte store; the integer dot of each (record, column) is the same.
 template <int U, int NS>
 __global__ __launch_bounds__(256) void k_moe_down_skinny(
     const int8_t* __restrict__ b_i8, const float* __restrict__ b_sa,
@@ -262,21 +266,19 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
   const int nstrips = hidden / 16;
   if (nsub0 >= nstrips) return;
   const int8_t* wb[NS];
-  float wsc[NS];
+  float wsc[NS][4];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int ns = min(nsub0 + j, nstrips - 1);  // a strip past the end is never stored
     wb[j] = w_d + (size_t)e * hidden * K + (size_t)ns * K64 * 1024 + lane * 16;
-    wsc[j] = d_scale[(size_t)e * hidden + ns * 16 + (lane & 15)];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      wsc[j][v] = d_scale[(size_t)e * hidden + ns * 16 + 4 * (lane >> 4) + v];
   }
+  // this lane's record: its activation fragment row and its result row
   const int arow = r0 + (lane & 15);
   const int8_t* ab = b_i8 + (size_t)(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
-  float rw[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int rec = r0 + 4 * (lane >> 4) + v;
-    rw[v] = routes[rec < r1 ? rec : r0].weight;
-  }
+  const float rw = routes[arow < r1 ? arow : r0].weight;
   const v4i zero = {0, 0, 0, 0};
   float facc[NS][4];
   v4i c[NS];
@@ -303,15 +305,15 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
       const int kt = ch * U + u;
       if (kt < K64) {
 #pragma unroll
-        for (int j = 0; j < NS; ++j) c[j] = mfma16x16x64(af[s][u], bf[s][j][u], c[j]);
+        for (int j = 0; j < NS; ++j) c[j] = mfma16x16x64(bf[s][j][u], af[s][u], c[j]);
         if (((kt + 1) & (fpb - 1)) == 0) {
           const int b = kt / fpb;
+          const float sc = s_sa[(lane & 15) * nb + b];
 #pragma unroll
           for (int j = 0; j < NS; ++j) {
             const int cc[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              facc[j][v] = fmaf((float)cc[v], s_sa[(4 * (lane >> 4) + v) * nb + b], facc[j][v]);
+            for (int v = 0; v < 4; ++v) facc[j][v] = fmaf((float)cc[v], sc, facc[j][v]);
             c[j] = zero;
           }
         }
@@ -327,16 +329,14 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
     if (ch + 2 < nch) load(0, ch + 2);
     mul(1, ch + 1);
   }
+  if (arow >= r1) return;
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     if (nsub0 + j >= nstrips) continue;
-    const int col = (nsub0 + j) * 16 + (lane & 15);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int rec = r0 + 4 * (lane >> 4) + v;
-      if (rec >= r1) continue;
-      y[(size_t)rec * hidden + col] = facc[j][v] * wsc[j] * rw[v];
-    }
+    const int col = (nsub0 + j) * 16 + 4 * (lane >> 4);
+    *reinterpret_cast<float4*>(&y[(size_t)arow * hidden + col]) =
+        float4{facc[j][0] * wsc[j][0] * rw, facc[j][1] * wsc[j][1] * rw,
+               facc[j][2] * wsc[j][2] * rw, facc[j][3] * wsc[j][3] * rw};
   }
 }
 
