@@ -342,14 +342,18 @@ class MoeLayer:
         self.out = torch.empty(T, H, dtype=torch.bfloat16, device=d)
         self.side = torch.cuda.Stream()  # default priority
 
-    def __call__(self, _i=0, fused=True, overlap=1):
-        # overlap 1: bq_moe_route_schedule (one launch up to 16 tokens) then
-        # the norm-quant; 2: the norm-quant on a second stream beside it
+    def __call__(self, _i=0, fused=True, overlap=3):
+        # overlap 3: bq_moe_prep (top-k, schedule and norm-quant in one launch
+        # up to 1024 route slots); 1: bq_moe_route_schedule then the
+        # norm-quant; 2: the norm-quant on a second stream beside the routing
         # (measured slower: the graph's cross-stream joins cost more than the
         # overlap saves); 0: the reference's three calls
         import torch
         bq, T = self.bq, self.T
-        if overlap == 2:
+        if overlap == 3:
+            bq.moe_prep(self.logits, self.x, self.gamma, TOPK, self.pes, 128,
+                        out=(self.idx, self.w, self.eo, self.routes, self.xq, self.xsa))
+        elif overlap == 2:
             main = torch.cuda.current_stream()
             self.side.wait_stream(main)
             with torch.cuda.stream(self.side):

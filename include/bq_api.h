@@ -200,6 +200,26 @@ int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale,
                           int experts, int top_k, int32_t* route_idx, float* route_w,
                           int32_t* expert_offset, bq_route* routes, void* stream);
 
+/* The three calls the reference's MoE block makes between its router and
+ * phase 1 -- dispatch_merge_router_candidates, dispatch_bq_norm_quant of the
+ * block input and dispatch_build_expert_schedules
+ * (modeling/gemma_4_moe_bq.mojo:673-688; kernels/moe_router.mojo:333-389,
+ * butterquant_kernels/linear.mojo:58-82, kernels/moe_router.mojo:60-145) --
+ * in one call, with bq_moe_route_schedule's and bq_norm_quant's results:
+ * route_idx / route_w / expert_offset / routes from logits, x_i8 / x_sa from
+ * x and gamma.  For seq_len * top_k <= 1024 slots and the pair-layout
+ * norm-quant's shapes (hidden % 256 == 0, hidden <= 4096) it is one launch,
+ * in which workgroups quantize the rows while others take the top-k, and
+ * the last top-k workgroup to finish builds the schedule (a device-scope
+ * counter of the library's, reset by that workgroup: calls on one device
+ * must not overlap in time, as stream order gives); otherwise the separate
+ * launches.  The checks of both calls apply. */
+int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,
+                const uint16_t* gamma, int seq_len, int experts, int top_k, int hidden, int block,
+                float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
+                int32_t* expert_offset, bq_route* routes, int8_t* x_i8, float* x_sa,
+                void* stream);
+
 /* dispatch_bq_phase1_gate_up[hidden, gate_up, inter] (moe.mojo:132-164):
  * for every route record rec of expert e (rows of w_gate_up: gate
  * [0,inter), up [inter, 2*inter) of expert e, expert stride 2*inter*hidden):

@@ -95,6 +95,7 @@ void tune_init(int device) {
   t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 2;
   t.down_breg = getenv("BQ_DOWN_BREG") ? env_int("BQ_DOWN_BREG") : 1;
   t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
+  t.moe_prep = getenv("BQ_MOE_PREP") ? env_int("BQ_MOE_PREP") : 1;
   // 16x16x64 by default: these LDS-ring kernels wait on their operand
   // stream, not on the MFMA rate (gate/up at 2048 tokens: 142 us with
   // 16x16x64 on 8-wave workgroups, 158 us with 32x32x32 on 4-wave ones)
@@ -376,6 +377,32 @@ int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale,
                                              route_idx, route_w, expert_offset,
                                              reinterpret_cast<bq::Route*>(routes), S(stream)),
                    "route_schedule");
+}
+
+int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,
+                const uint16_t* gamma, int seq_len, int experts, int top_k, int hidden, int block,
+                float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
+                int32_t* expert_offset, bq_route* routes, int8_t* x_i8, float* x_sa,
+                void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!logits || !x || !gamma || !route_idx || !route_w || !expert_offset || !routes || !x_i8 ||
+      !x_sa)
+    return fail(BQ_ERR_INVALID, "bq_moe_prep: null pointer");
+  if (experts <= 0 || top_k <= 0) return fail(BQ_ERR_SHAPE, "bq_moe_prep: bad top_k/experts");
+  if (experts > 256 || top_k > 16)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_moe_prep: experts %d > 256 or top_k %d > 16", experts,
+                top_k);
+  // the norm-quant's contract (bq_norm_quant)
+  if (!fwht_block_ok(block)) return fail(BQ_ERR_SHAPE, "bq_moe_prep: unsupported FWHT block %d", block);
+  if (hidden <= 0 || hidden % 64 || hidden % block)
+    return fail(BQ_ERR_SHAPE, "bq_moe_prep: hidden %d must be a multiple of 64 and of block %d", hidden, block);
+  if (hidden > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_prep: hidden %d > %d", hidden, kMaxRowLds);
+  if (!a16(x)) return fail(BQ_ERR_INVALID, "bq_moe_prep: x must be 16-byte aligned");
+  return check_hip(bq::launch_moe_prep(logits, per_expert_scale, x, gamma, seq_len, experts,
+                                       top_k, hidden, block, sqrt_n, n_eps, route_idx, route_w,
+                                       expert_offset, reinterpret_cast<bq::Route*>(routes), x_i8,
+                                       x_sa, S(stream)),
+                   "moe_prep");
 }
 
 int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,

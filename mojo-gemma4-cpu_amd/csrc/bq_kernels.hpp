@@ -23,6 +23,7 @@ struct Tune {
   int moe_order;    // BQ_MOE_ORDER: MoE work order of the LDS-ring kernels (0, 1, 2)
   int down_breg;    // BQ_DOWN_BREG: 0 disables the register-streamed down kernel
   int nq_pair;      // BQ_NQ_PAIR: 0 disables the pair-layout norm-quant
+  int moe_prep;     // BQ_MOE_PREP: 0 runs bq_moe_prep as separate launches
   int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
   int cus;          // compute units of the device
 };
@@ -137,6 +138,11 @@ hipError_t launch_route_schedule(const float* logits, const uint16_t* pes, int T
                                  int32_t* expert_offset, Route* routes, hipStream_t st);
 hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,
                              int32_t* route_idx, float* route_w, hipStream_t st);
+hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint16_t* src,
+                           const uint16_t* gamma, int T, int E, int top_k, int hidden, int block,
+                           float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
+                           int32_t* expert_offset, Route* routes, int8_t* xq, float* sa,
+                           hipStream_t st);
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);

@@ -15,6 +15,8 @@
 //   among logits above the sentinel -1e30, padding with {expert 0, -1e30}.
 //   The wave takes k successive maxima of a 64-bit key that encodes that
 //   order, so the selected list is the reference's list entry for entry.
+#include <mutex>
+
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
 #include "bq_sched.hpp"
@@ -311,6 +313,112 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
   schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
 }
 
+// The MoE block's prep for a decode-sized batch in one launch: the route
+// top-k + softmax merge, the norm-quant of the hidden states and the CSR
+// schedule -- the reference's dispatch_merge_router_candidates,
+// dispatch_bq_norm_quant and dispatch_build_expert_schedules
+// (modeling/gemma_4_moe_bq.mojo:673-688) -- with the same results.
+// Workgroups [0, nq_blocks) norm-quantize two tokens each (the pair layout of
+// k_norm_quant_pair: a token over WPT <= 8 waves of SPW segments, the row's
+// amax through LDS); the others take 16 tokens' top-k each, one wave per
+// token.  The last top-k workgroup to finish builds the schedule from every
+// workgroup's routes (schedule_small, one thread per slot): each top-k
+// workgroup fences its route stores at device scope before it counts itself
+// done on *done, and the last one fences again before it reads them.  That
+// one resets *done for the next launch, so launches on one device must not
+// overlap (stream order gives that).
+constexpr int kPrepThreads = kSchedSmallSlots;   // 16 waves
+constexpr int kPrepTopkTokens = kPrepThreads / 64;
+__device__ unsigned g_prep_done = 0;
+
+template <int NE, int NSEG, int SPW>
+__global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
+    const float* __restrict__ logits, const uint16_t* __restrict__ pes,
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int32_t* __restrict__ route_idx,
+    float* __restrict__ route_w, int32_t* __restrict__ expert_offset, Route* __restrict__ routes,
+    int T, int E, int top_k, int hidden, int block, float sqrt_n, float n_eps, float fwht_scale,
+    int nq_blocks, unsigned* done) {
+  __shared__ float s_max[kPrepThreads / 64];
+  __shared__ int s_wc[kSchedWavesSmall][kMaxExperts];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if ((int)blockIdx.x < nq_blocks) {
+    // ---- norm-quant: token 2 b + g on waves 8 g .. 8 g + WPT - 1
+    const int nseg = hidden >> 7, wpt = (nseg + SPW - 1) / SPW;
+    const int g = wave >> 3, wv = wave & 7;
+    const int t = (int)blockIdx.x * 2 + g, q0 = wv * SPW;
+    const bool live = t < T && wv < wpt;  // wave-uniform
+    float v[SPW][2];
+    if (live) {
+      const uint32_t* xr = reinterpret_cast<const uint32_t*>(src + (size_t)t * hidden) + lane;
+      const uint32_t* gr = reinterpret_cast<const uint32_t*>(gamma) + lane;
+      // (loads return in issue order: the row first, which the sum of
+      // squares needs first; the wave's own segments again, into x)
+      uint32_t xp[NSEG], x[SPW], gp[SPW];
+#pragma unroll
+      for (int q = 0; q < NSEG; ++q)
+        if (q < nseg) xp[q] = xr[64 * q];
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        if (q0 + i < nseg) {
+          x[i] = xr[64 * (q0 + i)];
+          gp[i] = gr[64 * (q0 + i)];
+        }
+      }
+      const float total = nq_pair_sumsq<NSEG>(xp, nseg);
+      const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+      const float m = nq_pair_transform<SPW>(x, gp, inv_rms, q0, nseg, block, fwht_scale, v);
+      const float am = wave_max(m);
+      if (lane == 0) s_max[wave] = am;
+    }
+    __syncthreads();
+    if (!live) return;
+    float amax = s_max[8 * g];
+    for (int w = 1; w < wpt; ++w) amax = fmaxf(amax, s_max[8 * g + w]);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    uint16_t* qrow = reinterpret_cast<uint16_t*>(xq + (size_t)t * hidden) + lane;
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+      if (q0 + i < nseg) qrow[64 * (q0 + i)] = nq_pair_code(v[i], inv);
+    if (lane == 0 && wv == 0) sa[t] = amax;
+    return;
+  }
+  // ---- top-k + softmax merge: token 16 b' + wave
+  const int t = ((int)blockIdx.x - nq_blocks) * kPrepTopkTokens + wave;
+  if (t < T) {  // wave-uniform
+    const float* rows[1] = {logits + (size_t)t * E};
+    int e[1];
+    float w[1];
+    topk_tokens<NE, 1>(rows, pes, E, top_k, lane, e, w);
+    if (lane < top_k) {
+      route_idx[(size_t)t * top_k + lane] = e[0];
+      route_w[(size_t)t * top_k + lane] = w[0];
+    }
+  }
+  // ---- the last top-k workgroup builds the schedule.  Every wave waits
+  // for its route stores to reach L2; after the barrier one thread makes
+  // them visible device-wide (a device-scope fence writes the XCD's L2 back)
+  // and counts the workgroup done.  The last one invalidates its caches
+  // (the fence again, one thread) before any of its waves reads the routes.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    s_last = atomicAdd(done, 1u) == gridDim.x - (unsigned)nq_blocks - 1u;
+    if (s_last) __threadfence();
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int slots = T * top_k, sc = min(tid, slots - 1);
+  const int ex = route_idx[sc];
+  const float wx = route_w[sc];
+  schedule_small(tid < slots ? ex : -1, wx, top_k, E, s_wc, s_cnt, expert_offset, routes);
+  if (tid == 0) *done = 0u;  // for the next launch
+}
+
 template <int NE>
 static void launch_rss(int T, int E, int top_k, const float* logits, const uint16_t* pes,
                        int32_t* route_idx, float* route_w, int32_t* eo, Route* routes,
@@ -370,6 +478,73 @@ hipError_t launch_route_schedule(const float* logits, const uint16_t* pes, int T
   else if (E <= 128) launch_rss<2>(T, E, top_k, logits, pes, route_idx, route_w, expert_offset, routes, st);
   else launch_rss<4>(T, E, top_k, logits, pes, route_idx, route_w, expert_offset, routes, st);
   return hipGetLastError();
+}
+
+// g_prep_done's address on the current device, looked up once per device
+static hipError_t prep_counter(unsigned** out) {
+  constexpr int kDevices = 64;
+  static unsigned* addr[kDevices] = {};
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_prep_done));
+    if (e != hipSuccess) return e;
+    addr[dev] = static_cast<unsigned*>(p);
+  }
+  *out = addr[dev];
+  return hipSuccess;
+}
+
+// The prep in one launch (k_moe_prep) for T * top_k <= 1024 slots, E <= 256
+// and the pair-layout norm-quant's shapes (hidden % 256 == 0, <= 4096, FWHT
+// block <= 512, 2-byte aligned codes); otherwise the route top-k + schedule
+// and the norm-quant as separate launches.  Same results either way.
+hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint16_t* src,
+                           const uint16_t* gamma, int T, int E, int top_k, int hidden, int block,
+                           float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
+                           int32_t* expert_offset, Route* routes, int8_t* xq, float* sa,
+                           hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  if (E > kMaxExperts) return hipErrorInvalidValue;
+  const int ns = hidden >> 7;
+  const int unit = block > 128 ? block / 128 : 1;
+  int spw = (ns + 7) / 8;
+  spw = (spw + unit - 1) / unit * unit;
+  const bool fused = T * top_k <= kSchedSmallSlots && hidden % 256 == 0 && hidden <= 4096 &&
+                     tune().nq_pair && tune().moe_prep && !(reinterpret_cast<uintptr_t>(xq) & 1u) &&
+                     (ns + spw - 1) / spw <= 8;
+  if (!fused) {
+    const hipError_t r = launch_route_schedule(logits, pes, T, E, top_k, route_idx, route_w,
+                                               expert_offset, routes, st);
+    if (r != hipSuccess) return r;
+    return launch_norm_quant(src, gamma, xq, sa, T, hidden, block, sqrt_n, n_eps, st);
+  }
+  unsigned* done = nullptr;
+  const hipError_t ra = prep_counter(&done);
+  if (ra != hipSuccess) return ra;
+  const int nq_blocks = (T + 1) / 2;
+  const dim3 g(nq_blocks + (T + kPrepTopkTokens - 1) / kPrepTopkTokens), b(kPrepThreads);
+  const float sc = fwht_scale_host(block);
+  const int ne = (E + 63) / 64;
+#define BQ_PREP(NEV, N, S)                                                                        \
+  if (ne <= NEV && ns <= N && spw == S) {                                                        \
+    hipLaunchKernelGGL((k_moe_prep<NEV, N, S>), g, b, 0, st, logits, pes, src, gamma, xq, sa,     \
+                       route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,    \
+                       sqrt_n, n_eps, sc, nq_blocks, done);                                       \
+    return hipGetLastError();                                                                     \
+  }
+#define BQ_PREP_NQ(NEV) \
+  BQ_PREP(NEV, 8, 1) BQ_PREP(NEV, 8, 2) BQ_PREP(NEV, 8, 4) BQ_PREP(NEV, 16, 2) BQ_PREP(NEV, 16, 4) \
+  BQ_PREP(NEV, 24, 3) BQ_PREP(NEV, 24, 4) BQ_PREP(NEV, 32, 4)
+  BQ_PREP_NQ(1) BQ_PREP_NQ(2) BQ_PREP_NQ(4)
+#undef BQ_PREP_NQ
+#undef BQ_PREP
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_route_topk(const float* logits, const uint16_t* pes, int T, int E, int top_k,

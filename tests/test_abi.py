@@ -85,6 +85,15 @@ def test_validation_errors(L):
     assert L.bq_moe_route_schedule(P, None, 4, 128, 0, P, P, P, P, None) == 2
     assert L.bq_moe_route_schedule(P, None, 4, 128, 8, P, P, None, P, None) == 1
     assert L.bq_moe_route_schedule(P, None, 0, 128, 8, None, None, None, None, None) == 0
+    f1 = C.c_float(1)
+    prep = lambda T, E, k, H, B, *ptrs: L.bq_moe_prep(P, None, P, P, T, E, k, H, B, f1, f1,
+                                                      *ptrs, None)
+    assert prep(0, 128, 8, 2816, 128, *([None] * 6)) == 0                 # empty batch
+    assert prep(4, 128, 8, 2816, 128, P, P, None, P, P, P) == 1          # null expert_offset
+    assert prep(4, 512, 8, 2816, 128, P, P, P, P, P, P) == 4             # experts > 256
+    assert prep(4, 128, 0, 2816, 128, P, P, P, P, P, P) == 2             # top_k
+    assert prep(4, 128, 8, 2816, 48, P, P, P, P, P, P) == 2              # FWHT block
+    assert prep(4, 128, 8, 2880, 128, P, P, P, P, P, P) == 2             # hidden % block
     assert L.bq_moe_router_logits(P, P, P, P, 4, 2880 + 32, 128, C.c_float(1), C.c_float(1),
                                   None) == 2
     assert L.bq_moe_router_logits(P, C.c_void_p(18), P, P, 4, 2816, 128, C.c_float(1),

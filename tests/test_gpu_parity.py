@@ -374,6 +374,53 @@ def test_route_schedule(gpu, O, T, E, k, pes):
     np.testing.assert_array_equal(host(routes2), r)
 
 
+@pytest.mark.parametrize("T,E,k,H,B,pes", [(1, 128, 8, 2816, 128, True), (7, 128, 8, 2816, 128, False),
+                                           (16, 128, 8, 2816, 128, True), (32, 128, 8, 2816, 128, True),
+                                           (33, 128, 8, 2816, 128, False), (128, 128, 8, 2816, 128, True),
+                                           (129, 128, 8, 2816, 128, False), (20, 60, 2, 512, 64, False),
+                                           (9, 256, 16, 4096, 256, True), (40, 64, 4, 1024, 512, False),
+                                           (3, 200, 3, 2304, 256, True)])
+def test_moe_prep(gpu, O, T, E, k, H, B, pes):
+    """route top-k + softmax, the CSR schedule and the norm-quant of the MoE
+    input in one call (one launch up to 1024 slots, the separate launches at
+    T = 129) against the oracle, bit-exact; three calls in a row (the
+    launch's completion counter is reset by the workgroup that builds the
+    schedule)"""
+    logits = O.synth_normal_f32(70 + T, 1.0, (T, E))
+    sc = O.f32_to_bf16(O.synth_normal_f32(71, 0.2, (E,)) + 1.0) if pes else None
+    x = O.synth_normal_bf16(72 + T, 1.0, (T, H))
+    g = O.f32_to_bf16(O.synth_normal_f32(73, 0.3, (H,)) + 1.0)
+    ridx, rw = O.route_topk_softmax(logits, k, sc)
+    reo, rroutes = O.build_schedule(ridx, rw, E)
+    rq, rsa = O.norm_quant(x, g, B)
+    for _ in range(3):
+        idx, w, eo, routes, xq, sa = gpu.moe_prep(dev(logits), dev(x), dev(g), k,
+                                                  None if sc is None else dev(sc), block=B)
+        np.testing.assert_array_equal(host(idx), ridx)
+        np.testing.assert_array_equal(host(w), rw)
+        np.testing.assert_array_equal(host(eo), reo)
+        r = host(routes)
+        np.testing.assert_array_equal(r[:, 0], rroutes["token"])
+        np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
+        np.testing.assert_array_equal(host(xq), rq)
+        np.testing.assert_array_equal(host(sa), rsa)
+
+
+def test_moe_prep_batches_in_a_row(gpu, O):
+    """calls of different batch sizes after each other (grids of different
+    workgroup counts share the completion counter) match the separate calls"""
+    E, k, H = 128, 8, 2816
+    g = O.f32_to_bf16(O.synth_normal_f32(75, 0.3, (H,)) + 1.0)
+    for T in (32, 5, 64, 1, 32):
+        logits = dev(O.synth_normal_f32(76 + T, 1.0, (T, E)))
+        x = dev(O.synth_normal_bf16(77 + T, 1.0, (T, H)))
+        idx, w, eo, routes, xq, sa = gpu.moe_prep(logits, x, dev(g), k)
+        i2, w2, eo2, r2 = gpu.route_schedule(logits, k)
+        xq2, sa2 = gpu.norm_quant(x, dev(g), 128)
+        for a, b in ((idx, i2), (w, w2), (eo, eo2), (routes, r2), (xq, xq2), (sa, sa2)):
+            np.testing.assert_array_equal(host(a), host(b))
+
+
 def test_build_schedule_expert_range(gpu, O):
     # expert-parallel slice [32, 64) as a rank of degree 4 would build it
     idx, w = route_table(O, 40)
