@@ -219,16 +219,17 @@ template <int ST>
 __device__ inline float xlane_partner(float v) {
   static_assert(ST >= 1 && ST <= 32 && (ST & (ST - 1)) == 0, "stride");
   const int x = __float_as_int(v);
+  // (mov_dpp where every lane is written: no old value to keep, so no copy)
   if constexpr (ST == 1) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
   } else if constexpr (ST == 2) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
   } else if constexpr (ST == 4) {
     const int up = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0xF, false);  // row_shl:4
     const int dn = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false);  // row_shr:4
     return __int_as_float((threadIdx.x & 4) ? dn : up);
   } else if constexpr (ST == 8) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false));  // row_ror:8
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));  // row_ror:8
   } else if constexpr (ST == 16) {
     const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
     return __int_as_float((int)((threadIdx.x & 16) ? r[0] : r[1]));
