@@ -394,14 +394,6 @@ __global__ __launch_bounds__(512) void k_norm_quant_pair(
 // stages in its order, with no cross-row swaps.  The sum of squares reads
 // the row a second time in the pair layout (nq_pair_sumsq: the reference's
 // 128 chains in order).  The codes of a lane are one 8-byte store.
-__device__ inline float xlane_partner4_banks(float v) {
-  // lane ^ 4 inside rows of 16: row_shl:4 written into banks 0 and 2 (lanes
-  // 0-3, 8-11), row_shr:4 into banks 1 and 3
-  const int x = __float_as_int(v);
-  const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);
-  return __int_as_float(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false));
-}
-
 template <int NSEG>
 __global__ __launch_bounds__(256) void k_norm_quant_v8(
     const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
@@ -431,49 +423,12 @@ __global__ __launch_bounds__(256) void k_norm_quant_v8(
   }
   const float total = nq_pair_sumsq<NSEG>(xp, nseg);
   const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
-  const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f;
-  const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
-  const float sc_lane = (__builtin_popcount(lane & 15) & 1) ? -fwht_scale : fwht_scale;
   float v[NR][8];
   float m = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    const int r = i;
-    float xf[8], gf[8];
-    bf16x8_to_f32(xv[i], xf);
-    bf16x8_to_f32(gv[i], gf);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = xf[j] * inv_rms * gf[j];
-#pragma unroll
-    for (int st = 1; st < 8; st <<= 1)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j & st) continue;
-        const float a = v[i][j], b = v[i][j + st];
-        v[i][j] = a + b;
-        v[i][j + st] = a - b;
-      }
-    // across lanes: each lane computes own + s * partner, s = -1 on the
-    // upper lane of a pair, so the upper lane holds b - a = -(a - b).  Before
-    // every such stage both lanes of a pair carry the same sign (the parity
-    // of their lane bits already crossed), so each stage is exactly the
-    // reference's a + b / a - b up to that sign (negation commutes with
-    // round-to-nearest), and after the four stages a lane's values carry
-    // (-1)^parity(lane & 15), folded into the final scale multiply.
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = fmaf(xlane_partner<1>(v[i][j]), s1, v[i][j]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = fmaf(xlane_partner<2>(v[i][j]), s2, v[i][j]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = fmaf(xlane_partner4_banks(v[i][j]), s4, v[i][j]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = fmaf(xlane_partner<8>(v[i][j]), s8, v[i][j]);
-    const bool live = 512 * r + 8 * lane < hidden;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      v[i][j] = v[i][j] * sc_lane;
-      if (live) m = fmaxf(m, fabsf(v[i][j]));
-    }
+  for (int r = 0; r < NR; ++r) {
+    const float mr = nq_v8_transform(xv[r], gv[r], inv_rms, fwht_scale, v[r]);
+    if (512 * r + 8 * lane < hidden) m = fmaxf(m, mr);
   }
   const float amax = wave_max(m);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
@@ -482,14 +437,53 @@ __global__ __launch_bounds__(256) void k_norm_quant_v8(
   for (int i = 0; i < NR; ++i) {
     const int r = i;
     if (512 * r + 8 * lane >= hidden) continue;
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      w[j >> 2] |= (uint32_t)(uint8_t)quantize_i8(v[i][j], inv) << (8 * (j & 3));
+    uint32_t w[2];
+    nq_v8_codes(v[i], inv, w);
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
     *reinterpret_cast<u2*>(qrow + 512 * r + 8 * lane) = u2{w[0], w[1]};
   }
   if (lane == 0) sa[t] = amax;
+}
+
+// The same for a few tokens: one workgroup per token, wave w transforming
+// round w (values 512 w .. + 511); every wave takes the whole row's sum of
+// squares (the chain order forbids splitting it) and the row's amax meets
+// in LDS (one barrier).
+template <int NSEG>
+__global__ __launch_bounds__(512) void k_norm_quant_v8_row(
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int hidden, float sqrt_n, float n_eps,
+    float fwht_scale) {
+  __shared__ float s_max[8];
+  const int lane = lane_id(), wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int t = blockIdx.x, nseg = hidden >> 7;
+  const uint16_t* row = src + (size_t)t * hidden;
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(row) + lane;
+  uint32_t xp[NSEG];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+    if (q < nseg) xp[q] = xr[64 * q];
+  const int e0 = 512 * wave + 8 * lane;
+  const int ec = min(e0, hidden - 8);  // runs past the row are read, never stored
+  const v4i xv = *reinterpret_cast<const v4i*>(row + ec);
+  const v4i gv = *reinterpret_cast<const v4i*>(gamma + ec);
+  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
+  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+  float v[8];
+  float m = nq_v8_transform(xv, gv, inv_rms, fwht_scale, v);
+  if (e0 >= hidden) m = 0.0f;
+  m = wave_max(m);
+  if (lane == 0) s_max[wave] = m;
+  __syncthreads();
+  float amax = s_max[0];
+  for (int w = 1; w < nw; ++w) amax = fmaxf(amax, s_max[w]);
+  if (e0 < hidden) {
+    uint32_t w[2];
+    nq_v8_codes(v, amax > 0.0f ? 127.0f / amax : 0.0f, w);
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(xq + (size_t)t * hidden + e0) = u2{w[0], w[1]};
+  }
+  if (threadIdx.x == 0) sa[t] = amax;
 }
 
 // smallest instance holding nseg segments of R*64 values (hidden <= 4096)
@@ -556,10 +550,17 @@ hipError_t launch_norm_quant(const uint16_t* src, const uint16_t* gamma, int8_t*
     const int ns = hidden >> 7;
     // many tokens: one wave each (4 per workgroup); few: a token over up to
     // 8 waves of SPW segments (a multiple of B/128 segments: whole blocks)
-    // FWHT block 128 over many tokens: 8 values per lane for the transform
-    // (16-byte aligned gain, 8-byte aligned codes)
-    if (seq_len >= 256 && block == 128 && tune().nq_v8 &&
-        !(reinterpret_cast<uintptr_t>(gamma) & 15u) && !(reinterpret_cast<uintptr_t>(xq) & 7u)) {
+    // FWHT block 128: 8 values per lane for the transform (16-byte aligned
+    // gain, 8-byte aligned codes); a workgroup per token below 256 tokens
+    const bool v8 = block == 128 && tune().nq_v8 && !(reinterpret_cast<uintptr_t>(gamma) & 15u) &&
+                    !(reinterpret_cast<uintptr_t>(xq) & 7u);
+    if (v8 && seq_len < 256) {
+      const dim3 g(seq_len), b(64 * ((hidden + 511) / 512));
+#define BQ_NQ8R(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_quant_v8_row<N>), g, b, 0, st, src, gamma, xq, sa, hidden, sqrt_n, n_eps, sc); return hipGetLastError(); }
+      BQ_NQ8R(8) BQ_NQ8R(16) BQ_NQ8R(22) BQ_NQ8R(24) BQ_NQ8R(32)
+#undef BQ_NQ8R
+    }
+    if (v8 && seq_len >= 256) {
       const dim3 g((seq_len + 3) / 4), b(256);
 #define BQ_NQ8(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_quant_v8<N>), g, b, 0, st, src, gamma, xq, sa, seq_len, hidden, sqrt_n, n_eps, sc); return hipGetLastError(); }
       BQ_NQ8(8) BQ_NQ8(16) BQ_NQ8(22) BQ_NQ8(24) BQ_NQ8(32)

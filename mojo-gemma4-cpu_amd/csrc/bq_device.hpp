@@ -560,6 +560,72 @@ __device__ inline float nq_pair_transform(const uint32_t (&x)[SPW], const uint32
   return m;
 }
 
+// ---------------------------------------------------------------------------
+// Norm-quant transform with FWHT block 128 on 8 consecutive values per lane
+// (lane L of a 512-value round holds values 8L .. 8L+7, so a 128-value block
+// is one row of 16 lanes): x * inv_rms * gain, the FWHT's strides 1, 2, 4
+// inside the lane and strides 8, 16, 32, 64 across lanes 1, 2, 4, 8 apart,
+// times fwht_scale -- the reference's stages in its order.  Each cross-lane
+// stage computes own + s * partner, s = -1 on the upper lane of a pair, so
+// the upper lane holds b - a = -(a - b); before every such stage both lanes
+// of a pair carry the same sign (the parity of the lane bits already
+// crossed), so each stage is exactly a + b / a - b up to that sign
+// (negation commutes with round-to-nearest), and the final sign,
+// (-1)^parity(lane & 15), is folded into the scale multiply.  Returns the
+// lane's max |v|.
+__device__ inline float xlane_partner4_banks(float v) {
+  // lane ^ 4 inside rows of 16: row_shl:4 written into banks 0 and 2 (lanes
+  // 0-3, 8-11), row_shr:4 into banks 1 and 3
+  const int x = __float_as_int(v);
+  const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);
+  return __int_as_float(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false));
+}
+
+__device__ inline float nq_v8_transform(v4i xv, v4i gv, float inv_rms, float fwht_scale,
+                                        float (&v)[8]) {
+  const int lane = lane_id();
+  const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f;
+  const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
+  const float sc_lane = (__builtin_popcount(lane & 15) & 1) ? -fwht_scale : fwht_scale;
+  float xf[8], gf[8];
+  bf16x8_to_f32(xv, xf);
+  bf16x8_to_f32(gv, gf);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = xf[j] * inv_rms * gf[j];
+#pragma unroll
+  for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j & st) continue;
+      const float a = v[j], b = v[j + st];
+      v[j] = a + b;
+      v[j + st] = a - b;
+    }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = fmaf(xlane_partner<1>(v[j]), s1, v[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = fmaf(xlane_partner<2>(v[j]), s2, v[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = fmaf(xlane_partner4_banks(v[j]), s4, v[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = fmaf(xlane_partner<8>(v[j]), s8, v[j]);
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = v[j] * sc_lane;
+    m = fmaxf(m, fabsf(v[j]));
+  }
+  return m;
+}
+
+// the 8 int8 codes of v, little-endian in two words
+__device__ inline void nq_v8_codes(const float (&v)[8], float inv, uint32_t (&w)[2]) {
+  w[0] = w[1] = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    w[j >> 2] |= (uint32_t)(uint8_t)quantize_i8(v[j], inv) << (8 * (j & 3));
+}
+
 // the int8 code pair of v[i] (low byte: the even element)
 __device__ inline uint16_t nq_pair_code(const float (&vi)[2], float inv) {
   return (uint16_t)((uint8_t)quantize_i8(vi[0], inv) | ((uint16_t)(uint8_t)quantize_i8(vi[1], inv) << 8));

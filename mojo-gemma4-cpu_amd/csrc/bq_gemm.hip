@@ -243,7 +243,10 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
 // computes the same codes and scale; workgroup 0 also writes them to
 // x_i8 / x_sa.  Two launches become one, and the norm-quant's memory round
 // trips overlap the weight stream instead of preceding it.
-template <int NSEG, int SPW>
+// V8 (FWHT block 128): wave w transforms values 512 w .. 512 w + 511 with 8
+// consecutive values per lane (nq_v8_transform), the codes one 8-byte store
+// per lane; otherwise the pair layout's SPW segments per wave.
+template <int NSEG, int SPW, bool V8 = false>
 __global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormArgs nq) {
   constexpr int WAVES = 8, U = 8;
   __shared__ __attribute__((aligned(16))) int8_t s_x[64 * WAVES * U];  // the row's codes
@@ -265,14 +268,22 @@ __global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormAr
   // (the wave's own segments are loaded again, into x: cheaper than picking
   // them out of xp by a run-time index)
   uint32_t xp[NSEG], x[SPW], g[SPW];
+  v4i xv, gv;
 #pragma unroll
   for (int q = 0; q < NSEG; ++q)  // first: the sum of squares needs it first
     if (q < nseg) xp[q] = xr[64 * q];
+  const int e0 = 512 * wave + 8 * lane;  // V8: this lane's run
+  if constexpr (V8) {
+    const int ec = min(e0, K - 8);  // runs past the row are read, never used
+    xv = *reinterpret_cast<const v4i*>(nq.src + ec);
+    gv = *reinterpret_cast<const v4i*>(nq.gamma + ec);
+  } else {
 #pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    const bool in = q0 + i < nseg;
-    x[i] = in ? xr[64 * (q0 + i)] : 0u;
-    g[i] = in ? gr[64 * (q0 + i)] : 0u;
+    for (int i = 0; i < SPW; ++i) {
+      const bool in = q0 + i < nseg;
+      x[i] = in ? xr[64 * (q0 + i)] : 0u;
+      g[i] = in ? gr[64 * (q0 + i)] : 0u;
+    }
   }
   // epilogue: thread t < 16 owns row 0's column t (accumulator element v = 0
   // of lanes 0..15); its weight scale is fetched now
@@ -289,22 +300,38 @@ __global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormAr
   // ---- the row's norm-quant ------------------------------------------------
   const float total = nq_pair_sumsq<NSEG>(xp, nseg);
   const float inv_rms = nq.sqrt_n / __builtin_sqrtf(total + nq.n_eps);
-  float v[SPW][2];
-  const float m = nq_pair_transform<SPW>(x, g, inv_rms, q0, nseg, nq.block, nq.fwht_scale, v);
+  float v[SPW][2], v8[8];
+  float m;
+  if constexpr (V8) {
+    m = nq_v8_transform(xv, gv, inv_rms, nq.fwht_scale, v8);
+    if (e0 >= K) m = 0.0f;
+  } else {
+    m = nq_pair_transform<SPW>(x, g, inv_rms, q0, nseg, nq.block, nq.fwht_scale, v);
+  }
   const float wmax = wave_max(m);
   if (lane == 0) s_f[wave] = wmax;
   __syncthreads();
   float amax = s_f[0];
-  for (int w = 1; w < wpt; ++w) amax = fmaxf(amax, s_f[w]);
+  for (int w = 1; w < (V8 ? WAVES : wpt); ++w) amax = fmaxf(amax, s_f[w]);
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-  uint16_t* sx = reinterpret_cast<uint16_t*>(s_x) + lane;
-  uint16_t* gx = reinterpret_cast<uint16_t*>(nq.xq) + lane;
+  if constexpr (V8) {
+    if (e0 < K) {
+      uint32_t w[2];
+      nq_v8_codes(v8, inv, w);
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u2*>(&s_x[e0]) = u2{w[0], w[1]};
+      if (blockIdx.x == 0) *reinterpret_cast<u2*>(nq.xq + e0) = u2{w[0], w[1]};
+    }
+  } else {
+    uint16_t* sx = reinterpret_cast<uint16_t*>(s_x) + lane;
+    uint16_t* gx = reinterpret_cast<uint16_t*>(nq.xq) + lane;
 #pragma unroll
-  for (int i = 0; i < SPW; ++i) {
-    if (q0 + i < nseg) {
-      const uint16_t c = nq_pair_code(v[i], inv);
-      sx[64 * (q0 + i)] = c;
-      if (blockIdx.x == 0) gx[64 * (q0 + i)] = c;
+    for (int i = 0; i < SPW; ++i) {
+      if (q0 + i < nseg) {
+        const uint16_t c = nq_pair_code(v[i], inv);
+        sx[64 * (q0 + i)] = c;
+        if (blockIdx.x == 0) gx[64 * (q0 + i)] = c;
+      }
     }
   }
   if (blockIdx.x == 0 && t == 0) nq.sa[0] = amax;
@@ -347,6 +374,14 @@ static bool launch_norm_linear_fused(const LinArgs& a, const NormArgs& nq, hipSt
   int spw = (ns + 7) / 8;
   spw = (spw + unit - 1) / unit * unit;
   const dim3 g(tiles), b(512);
+  // FWHT block 128 (the model's): 8 values per lane for the transform
+  // (16-byte aligned gain, 8-byte aligned codes)
+  if (nq.block == 128 && tune().nq_v8 && !(reinterpret_cast<uintptr_t>(nq.gamma) & 15u) &&
+      !(reinterpret_cast<uintptr_t>(nq.xq) & 7u)) {
+#define BQ_NL8(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_linear_skinny<N, 1, true>), g, b, 0, st, a, nq); return true; }
+    BQ_NL8(8) BQ_NL8(16) BQ_NL8(22) BQ_NL8(24) BQ_NL8(32)
+#undef BQ_NL8
+  }
 #define BQ_NL(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_linear_skinny<N, S>), g, b, 0, st, a, nq); return true; }
   BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
   BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
