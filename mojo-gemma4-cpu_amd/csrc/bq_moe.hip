@@ -495,8 +495,10 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
+      // two k-steps per register slot (83 VGPRs, five waves per SIMD): 32-token
+      // layer 131.4 -> 130.2 us against four (131 VGPRs, three waves)
       dim3 g((hidden / 16 + 7) / 8, mtile_bound(max_routes, experts, 16)), b(256);
-      hipLaunchKernelGGL((k_moe_down_skinny<4, 2>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
+      hipLaunchKernelGGL((k_moe_down_skinny<2, 2>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
                          w_down, down_scale, y, experts, hidden, inter, block, max_routes);
     }
   }
