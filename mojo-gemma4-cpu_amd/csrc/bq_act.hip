@@ -386,63 +386,20 @@ __global__ __launch_bounds__(512) void k_norm_quant_pair(
   if (lane == 0 && wave == (one ? wave : 0)) sa[t] = amax;
 }
 
-// Norm-quant with FWHT block 128, one wave per token, the transform on 8
-// consecutive values per lane: in round r lane L holds values 512 r + 8 L ..
-// + 7, so a 128-value block is one row of 16 lanes and the FWHT's strides 1,
-// 2, 4 run inside the lane and strides 8, 16, 32, 64 across lanes 1, 2, 4, 8
-// apart (one DPP row move each, two for lanes 4 apart) -- the reference's
-// stages in its order, with no cross-row swaps.  The sum of squares reads
-// the row a second time in the pair layout (nq_pair_sumsq: the reference's
-// 128 chains in order).  The codes of a lane are one 8-byte store.
+// Norm-quant with FWHT block 128, one wave per token (nq_v8_token): the
+// transform on 8 consecutive values per lane, so a 128-value block is one
+// row of 16 lanes and the FWHT's strides 1, 2, 4 run inside the lane and
+// strides 8, 16, 32, 64 across lanes 1, 2, 4, 8 apart (one DPP row move
+// each, two for lanes 4 apart) -- the reference's stages in its order, with
+// no cross-row swaps.
 template <int NSEG>
 __global__ __launch_bounds__(256) void k_norm_quant_v8(
     const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
     int8_t* __restrict__ xq, float* __restrict__ sa, int T, int hidden, float sqrt_n,
     float n_eps, float fwht_scale) {
-  constexpr int NR = (NSEG + 3) / 4;  // rounds of 512 values
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // whole waves; nothing synchronizes
-  const int nseg = hidden >> 7;
-  const uint16_t* row = src + (size_t)t * hidden;
-  // the pair layout for the sum of squares, then this lane's 8-value runs
-  // (loads return in issue order: the sum of squares' first)
-  const uint32_t* xr = reinterpret_cast<const uint32_t*>(row) + lane;
-  uint32_t xp[NSEG];
-#pragma unroll
-  for (int q = 0; q < NSEG; ++q)
-    if (q < nseg) xp[q] = xr[64 * q];
-  v4i xv[NR], gv[NR];
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    const int r = i;
-    // runs past the row are read, never stored
-    const int e0 = min(512 * r + 8 * lane, hidden - 8);
-    xv[i] = *reinterpret_cast<const v4i*>(row + e0);
-    gv[i] = *reinterpret_cast<const v4i*>(gamma + e0);
-  }
-  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
-  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
-  float v[NR][8];
-  float m = 0.0f;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const float mr = nq_v8_transform(xv[r], gv[r], inv_rms, fwht_scale, v[r]);
-    if (512 * r + 8 * lane < hidden) m = fmaxf(m, mr);
-  }
-  const float amax = wave_max(m);
-  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-  int8_t* qrow = xq + (size_t)t * hidden;
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    const int r = i;
-    if (512 * r + 8 * lane >= hidden) continue;
-    uint32_t w[2];
-    nq_v8_codes(v[i], inv, w);
-    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-    *reinterpret_cast<u2*>(qrow + 512 * r + 8 * lane) = u2{w[0], w[1]};
-  }
-  if (lane == 0) sa[t] = amax;
+  nq_v8_token<NSEG>(src, gamma, xq, sa, t, hidden, sqrt_n, n_eps, fwht_scale);
 }
 
 // The same for a few tokens: one workgroup per token, wave w transforming

@@ -631,4 +631,57 @@ __device__ inline uint16_t nq_pair_code(const float (&vi)[2], float inv) {
   return (uint16_t)((uint8_t)quantize_i8(vi[0], inv) | ((uint16_t)(uint8_t)quantize_i8(vi[1], inv) << 8));
 }
 
+// Norm-quant of token t with FWHT block 128 by one wave (hidden % 256 == 0,
+// hidden <= 128 * NSEG, 16-byte aligned gain, 8-byte aligned codes): the
+// transform on 8 consecutive values per lane (nq_v8_transform, round r of
+// 512 values: lane L holds 512 r + 8 L .. + 7), the sum of squares from a
+// second read of the row in the pair layout (nq_pair_sumsq: the reference's
+// 128 chains in order), the codes of a lane one 8-byte store.
+template <int NSEG>
+__device__ __attribute__((always_inline)) inline void nq_v8_token(const uint16_t* __restrict__ src,
+                                   const uint16_t* __restrict__ gamma, int8_t* __restrict__ xq,
+                                   float* __restrict__ sa, int t, int hidden, float sqrt_n,
+                                   float n_eps, float fwht_scale) {
+  constexpr int NR = (NSEG + 3) / 4;  // rounds of 512 values
+  const int lane = lane_id();
+  const int nseg = hidden >> 7;
+  const uint16_t* row = src + (size_t)t * hidden;
+  // the pair layout for the sum of squares, then this lane's 8-value runs
+  // (loads return in issue order: the sum of squares' first)
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(row) + lane;
+  uint32_t xp[NSEG];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+    if (q < nseg) xp[q] = xr[64 * q];
+  v4i xv[NR], gv[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    // runs past the row are read, never stored
+    const int e0 = min(512 * r + 8 * lane, hidden - 8);
+    xv[r] = *reinterpret_cast<const v4i*>(row + e0);
+    gv[r] = *reinterpret_cast<const v4i*>(gamma + e0);
+  }
+  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
+  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+  float v[NR][8];
+  float m = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float mr = nq_v8_transform(xv[r], gv[r], inv_rms, fwht_scale, v[r]);
+    if (512 * r + 8 * lane < hidden) m = fmaxf(m, mr);
+  }
+  const float amax = wave_max(m);
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int8_t* qrow = xq + (size_t)t * hidden;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (512 * r + 8 * lane >= hidden) continue;
+    uint32_t w[2];
+    nq_v8_codes(v[r], inv, w);
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(qrow + 512 * r + 8 * lane) = u2{w[0], w[1]};
+  }
+  if (lane == 0) sa[t] = amax;
+}
+
 }  // namespace bq

@@ -500,6 +500,37 @@ static hipError_t prep_counter(unsigned** out) {
   return hipSuccess;
 }
 
+// The prep's route top-k and norm-quant for larger batches in one launch
+// (the schedule follows as its own launch): workgroups [0, tk_blocks) take
+// four tokens' top-k + softmax merge (one wave per token, as k_route_topk),
+// the others four tokens' norm-quant with FWHT block 128 (one wave per token,
+// nq_v8_token, as k_norm_quant_v8).  The two are independent, so the
+// norm-quant's waves fill the issue slots the top-k's leave.
+template <int NE, int NSEG>
+__global__ __launch_bounds__(256) void k_topk_norm_quant(
+    const float* __restrict__ logits, const uint16_t* __restrict__ pes,
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int32_t* __restrict__ route_idx,
+    float* __restrict__ route_w, int T, int E, int top_k, int hidden, float sqrt_n, float n_eps,
+    float fwht_scale, int tk_blocks) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const bool tk = (int)blockIdx.x < tk_blocks;
+  const int t = ((int)blockIdx.x - (tk ? 0 : tk_blocks)) * 4 + wave;
+  if (t >= T) return;  // whole waves; no block synchronization below
+  if (!tk) {
+    nq_v8_token<NSEG>(src, gamma, xq, sa, t, hidden, sqrt_n, n_eps, fwht_scale);
+    return;
+  }
+  const float* rows[1] = {logits + (size_t)t * E};
+  int e[1];
+  float w[1];
+  topk_tokens<NE, 1>(rows, pes, E, top_k, lane, e, w);
+  if (lane < top_k) {
+    route_idx[(size_t)t * top_k + lane] = e[0];
+    route_w[(size_t)t * top_k + lane] = w[0];
+  }
+}
+
 // The prep in one launch (k_moe_prep) for T * top_k <= 1024 slots, E <= 256
 // and the pair-layout norm-quant's shapes (hidden % 256 == 0, <= 4096, FWHT
 // block <= 512, 2-byte aligned codes); otherwise the route top-k + schedule
@@ -518,6 +549,33 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
   const bool fused = T * top_k <= kSchedSmallSlots && hidden % 256 == 0 && hidden <= 4096 &&
                      tune().nq_pair && tune().moe_prep && !(reinterpret_cast<uintptr_t>(xq) & 1u) &&
                      (ns + spw - 1) / spw <= 8;
+  // larger batches with FWHT block 128: top-k and norm-quant in one launch,
+  // then the schedule (the conditions of launch_norm_quant's v8 path)
+  const bool wide = !fused && T * top_k > kSchedSmallSlots && block == 128 && hidden % 256 == 0 &&
+                    hidden <= 4096 && tune().nq_pair && tune().nq_v8 && tune().moe_prep &&
+                    !(reinterpret_cast<uintptr_t>(gamma) & 15u) &&
+                    !(reinterpret_cast<uintptr_t>(xq) & 7u);
+  if (wide) {
+    const int tk_blocks = (T + 3) / 4;
+    const dim3 g(2 * tk_blocks), b(256);
+    const float sc = fwht_scale_host(block);
+    const int ne = (E + 63) / 64;
+    bool launched = false;
+#define BQ_TNQ(NEV, N)                                                                           \
+  if (!launched && ne <= NEV && ns <= N) {                                                       \
+    hipLaunchKernelGGL((k_topk_norm_quant<NEV, N>), g, b, 0, st, logits, pes, src, gamma, xq, sa, \
+                       route_idx, route_w, T, E, top_k, hidden, sqrt_n, n_eps, sc, tk_blocks);   \
+    launched = true;                                                                             \
+  }
+#define BQ_TNQ_NS(NEV) BQ_TNQ(NEV, 8) BQ_TNQ(NEV, 16) BQ_TNQ(NEV, 22) BQ_TNQ(NEV, 24) BQ_TNQ(NEV, 32)
+    BQ_TNQ_NS(1) BQ_TNQ_NS(2) BQ_TNQ_NS(4)
+#undef BQ_TNQ_NS
+#undef BQ_TNQ
+    if (!launched) return hipErrorInvalidValue;
+    const hipError_t r = hipGetLastError();
+    if (r != hipSuccess) return r;
+    return launch_build_schedule(route_idx, route_w, T, top_k, 0, E, expert_offset, routes, st);
+  }
   if (!fused) {
     const hipError_t r = launch_route_schedule(logits, pes, T, E, top_k, route_idx, route_w,
                                                expert_offset, routes, st);

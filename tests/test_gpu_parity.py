@@ -379,13 +379,17 @@ def test_route_schedule(gpu, O, T, E, k, pes):
                                            (33, 128, 8, 2816, 128, False), (128, 128, 8, 2816, 128, True),
                                            (129, 128, 8, 2816, 128, False), (20, 60, 2, 512, 64, False),
                                            (9, 256, 16, 4096, 256, True), (40, 64, 4, 1024, 512, False),
-                                           (3, 200, 3, 2304, 256, True)])
+                                           (3, 200, 3, 2304, 256, True), (257, 64, 4, 4096, 128, False),
+                                           (600, 200, 2, 1024, 128, True), (301, 128, 8, 2816, 256, True),
+                                           (2048, 128, 8, 2816, 128, True)])
 def test_moe_prep(gpu, O, T, E, k, H, B, pes):
     """route top-k + softmax, the CSR schedule and the norm-quant of the MoE
-    input in one call (one launch up to 1024 slots, the separate launches at
-    T = 129) against the oracle, bit-exact; three calls in a row (the
-    launch's completion counter is reset by the workgroup that builds the
-    schedule)"""
+    input in one call against the oracle, bit-exact: one launch up to 1024
+    slots; above, with FWHT block 128, the top-k and the norm-quant in one
+    launch and the schedule in a second (T = 129, 257, 600, 2048), else the
+    separate launches (T = 301 at block 256).  Three calls in a row (the
+    small launch's completion counter is reset by the workgroup that builds
+    the schedule)"""
     logits = O.synth_normal_f32(70 + T, 1.0, (T, E))
     sc = O.f32_to_bf16(O.synth_normal_f32(71, 0.2, (E,)) + 1.0) if pes else None
     x = O.synth_normal_bf16(72 + T, 1.0, (T, H))
