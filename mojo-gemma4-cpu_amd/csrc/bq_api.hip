@@ -97,6 +97,8 @@ void tune_init(int device) {
   t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
   t.moe_prep = getenv("BQ_MOE_PREP") ? env_int("BQ_MOE_PREP") : 1;
   t.nq_v8 = getenv("BQ_NQ_V8") ? env_int("BQ_NQ_V8") : 1;
+  t.down_skinny = getenv("BQ_DOWN_SKINNY") ? env_int("BQ_DOWN_SKINNY") : 12;
+  t.gu_skinny = getenv("BQ_GU_SKINNY") ? env_int("BQ_GU_SKINNY") : 4;
   // 16x16x64 by default: these LDS-ring kernels wait on their operand
   // stream, not on the MFMA rate (gate/up at 2048 tokens: 142 us with
   // 16x16x64 on 8-wave workgroups, 158 us with 32x32x32 on 4-wave ones)

@@ -347,12 +347,14 @@ __global__ __launch_bounds__(256) void k_moe_down_skinny(
 // a token that lists an expert twice (the router's padding repeats expert 0)
 // has a run of two, added in record order as the reference adds its routes.
 // A scan over experts lists the runs in ascending expert order.  At most
-// kMaxTopK records.
+// kMaxTopK records.  Workgroup (t, c) takes columns [c * chunk, + chunk) of
+// token t (a small batch spreads over more CUs; each repeats the scan).
 constexpr int kMaxTopK = 16;
 
 __global__ __launch_bounds__(256) void k_combine(
     const float* __restrict__ y, const int32_t* __restrict__ eo, const Route* __restrict__ routes,
-    int E, int max_routes, int hidden, float* __restrict__ accum, uint16_t* __restrict__ out) {
+    int E, int max_routes, int hidden, int chunk, float* __restrict__ accum,
+    uint16_t* __restrict__ out) {
   __shared__ int recs[kMaxTopK];
   __shared__ int wsum[4];
   const int t = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
@@ -396,7 +398,8 @@ __global__ __launch_bounds__(256) void k_combine(
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j) rr[j] = j < cnt ? recs[j] : 0;
   typedef float f4 __attribute__((ext_vector_type(4)));
-  for (int c = tid * 4; c < hidden; c += 1024) {
+  const int c1 = min(hidden, ((int)blockIdx.y + 1) * chunk);
+  for (int c = (int)blockIdx.y * chunk + tid * 4; c < c1; c += 1024) {
     f4 v[kMaxTopK];
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j)
@@ -466,9 +469,17 @@ hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_
     return launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket, bi8, bsa,
                                     experts, max_routes, hidden, inter, bm, st);
   dim3 g((inter / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
-  hipLaunchKernelGGL(k_moe_gate_up_skinny<4>, g, b, 0, st, x_i8, x_sa, eo, routes, w_gu,
-                     gu_scale, bucket, bi8, bsa, fwht_scale_host(64), experts, hidden, inter,
-                     max_routes);
+#define BQ_GU(U)                                                                                  \
+  case U:                                                                                         \
+    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, x_i8, x_sa, eo, routes, w_gu,       \
+                       gu_scale, bucket, bi8, bsa, fwht_scale_host(64), experts, hidden, inter,  \
+                       max_routes);                                                               \
+    break;
+  switch (tune().gu_skinny) {
+    BQ_GU(2) BQ_GU(3) BQ_GU(6)
+    default: BQ_GU(4)
+  }
+#undef BQ_GU
   return hipGetLastError();
 }
 
@@ -495,15 +506,32 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
-      // two k-steps per register slot (83 VGPRs, five waves per SIMD): 32-token
-      // layer 131.4 -> 130.2 us against four (131 VGPRs, three waves)
-      dim3 g((hidden / 16 + 7) / 8, mtile_bound(max_routes, experts, 16)), b(256);
-      hipLaunchKernelGGL((k_moe_down_skinny<2, 2>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes,
-                         w_down, down_scale, y, experts, hidden, inter, block, max_routes);
+      // one k-step per register slot and two strips per wave (58 VGPRs, seven
+      // waves per SIMD; BQ_DOWN_SKINNY): the 32-token layer 127.6 us against
+      // 128.0-130.6 us for 1-4 k-steps x 1-4 strips
+      const int ut = tune().down_skinny;
+#define BQ_DS(U, NS)                                                                              \
+  case U * 10 + NS: {                                                                             \
+    dim3 g((hidden / 16 + 4 * NS - 1) / (4 * NS), mtile_bound(max_routes, experts, 16)), b(256); \
+    hipLaunchKernelGGL((k_moe_down_skinny<U, NS>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes, \
+                       w_down, down_scale, y, experts, hidden, inter, block, max_routes);         \
+    break;                                                                                        \
+  }
+      switch (ut) {
+        BQ_DS(3, 2) BQ_DS(1, 3) BQ_DS(2, 3) BQ_DS(1, 4) BQ_DS(2, 4) BQ_DS(2, 1)
+        BQ_DS(4, 1) BQ_DS(4, 2)
+        BQ_DS(2, 2)
+        default: BQ_DS(1, 2)
+      }
+#undef BQ_DS
     }
   }
-  hipLaunchKernelGGL(k_combine, dim3(seq_len), dim3(256), 0, st, y, eo, routes, experts,
-                     max_routes, hidden, accum, out);
+  // below 256 tokens each workgroup takes 256 columns of its token (32
+  // tokens: 32 workgroups -> 352, the layer ~130 -> 128.7 us), else the
+  // whole row
+  const int chunk = seq_len < 256 ? 256 : (hidden + 3) / 4 * 4;
+  hipLaunchKernelGGL(k_combine, dim3(seq_len, (hidden + chunk - 1) / chunk), dim3(256), 0, st, y,
+                     eo, routes, experts, max_routes, hidden, chunk, accum, out);
   return hipGetLastError();
 }
 
