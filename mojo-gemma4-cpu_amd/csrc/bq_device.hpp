@@ -362,7 +362,7 @@ __device__ inline void bf16x8_to_f32(v4i raw, float (&v)[8]) {
   }
 }
 
-// Workgroup barrier for LDS producer/consumer hand-offs// Workgroup barrier for LDS producer/consumer hand-offs: waits for this
+// Workgroup barrier for LDS producer/consumer hand-offs: waits for this
 // wave's LDS operations only.  (__syncthreads() also carries a release fence,
 // which on gfx9 waits for every outstanding global load -- it would drain the
 // global-load prefetch pipeline at each stage.)  Global loads land in private
