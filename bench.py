@@ -1003,9 +1003,9 @@ def main():
                  "int8_tops": round(tops, 1), **m["s"].summary()}
             traffic = _traffic(f"moe_layer_t{T}_stats.txt")
             if T >= 2048:
-                # the north star's bar for this layer: a fraction of the
-                # matching MFMA peak; the layer's weights are bf16 models
-                # computed at int8, so dense bf16 is the declared matching peak
+                # this layer is judged as a fraction of the matching MFMA
+                # peak; its weights are bf16 models computed at int8, so
+                # dense bf16 is the declared matching peak
                 d["roofline"] = {
                     "bound": "mfma", "achieved": round(tops, 1), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TOP/s", "frac": round(tops / BF16_PEAK_TFLOPS, 4),

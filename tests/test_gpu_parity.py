@@ -6,7 +6,7 @@ Bar (tolerances are stated per assertion):
   * f32 outputs of the linears and the MoE: bit-exact with the oracle's
     signed-form restatement (which equals the reference's VNNI u8/colsum
     form whenever |sum (x+128)w| < 2^24, asserted where it matters); the
-    north-star tolerance (normwise rel 1e-3, cosine > 0.9999) is checked too.
+    floating-point tolerance (normwise rel 1e-3, cosine > 0.9999) is checked too.
 """
 import os
 
