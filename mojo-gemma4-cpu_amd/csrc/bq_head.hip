@@ -145,7 +145,7 @@ __device__ inline void samp_merge(float& s, int& i, float os, int oi) {
   }
 }
 
-template <int MI>
+template <int MI, int CH>
 __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
   constexpr int RP = 16 * MI;  // padded rows
   const int wave = threadIdx.x >> 6, lane = lane_id();
@@ -158,6 +158,38 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
   __shared__ uint64_t s_seed[RP];
   __shared__ int s_greedy[RP];
   __shared__ float s_red[kHeadWaves][4][RP];
+
+  // The wave's strips s0, s0 + stride, ... as a sequence of chunks of CH
+  // fragments (a strip's last chunk may be partial: its clamped loads are
+  // never multiplied), two register slots deep: chunk i + 1's fragments and
+  // block scales are in flight while chunk i multiplies.  Every block (fpb
+  // fragments; the launch picks CH with fpb dividing CH, and K64 is a
+  // multiple of fpb) lies inside one chunk; its int32 MFMA chain starts
+  // from zero and is drained into the f32 sum once.
+  const int stride = gridDim.x * kHeadWaves;
+  const int s0 = blockIdx.x * kHeadWaves + wave;
+  const int nch = (K64 + CH - 1) / CH;
+  const int nmine = s0 < a.nstrips ? (a.nstrips - 1 - s0) / stride + 1 : 0;
+  const int nsteps = nmine * nch;
+  const int bpc = CH / fpb;  // blocks per chunk
+  v4i wf[2][CH];
+  float wsc[2][CH];
+  auto load = [&](int slot, int step) {
+    const int si = step / nch, ch = step - si * nch;
+    const int s = s0 + si * stride;
+    const int8_t* wstrip = a.w + (size_t)s * K64 * 1024 + lane * 16;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      wf[slot][j] = *reinterpret_cast<const v4i*>(wstrip + (size_t)min(ch * CH + j, K64 - 1) * 1024);
+    }
+    const float* wsr = a.ws + (size_t)(s * 16 + (lane & 15)) * nb;
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
+      if (q < bpc) wsc[slot][q] = wsr[min(ch * bpc + q, nb - 1)];
+  };
+  // the first chunk's loads go out before the activation tile is staged,
+  // so their latency overlaps the staging's
+  if (nsteps > 0) load(0, 0);
 
   for (int i = threadIdx.x; i < RP * (H / 16); i += blockDim.x) {
     const int r = i / (H / 16), c = i % (H / 16);
@@ -177,7 +209,8 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
     s_seed[r] = p.seed;
     s_greedy[r] = p.greedy != 0;
   }
-  __syncthreads();
+  // (not __syncthreads: its fence would wait for the chunk loads in flight)
+  lds_barrier();
 
   // running partials per (mi, v) row slot: rows 16*mi + 4*(lane>>4) + v
   float best[MI][4], lmx[MI][4], lsum[MI][4];
@@ -192,63 +225,55 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
       lsum[mi][v] = 0.0f;
     }
 
-  const int stride = gridDim.x * kHeadWaves;
-  for (int s = blockIdx.x * kHeadWaves + wave; s < a.nstrips; s += stride) {
-    const int8_t* wstrip = a.w + (size_t)s * K64 * 1024 + lane * 16;
-    const int col = s * 16 + (lane & 15);  // this lane's vocabulary row
-    const float* wsr = a.ws + (size_t)col * nb;
-    float raw[MI][4];
+  float raw[MI][4];
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) raw[mi][v] = 0.0f;
-    // blocks in chunks of up to 8 fragments whose loads go out together
-    for (int f0 = 0; f0 < K64; f0 += 8) {
-      v4i wf[8];
+    for (int v = 0; v < 4; ++v) raw[mi][v] = 0.0f;
+  auto compute = [&](int slot, int step) {
+    const int si = step / nch, ch = step - si * nch;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) wf[j] = *reinterpret_cast<const v4i*>(wstrip + (size_t)min(f0 + j, K64 - 1) * 1024);
-      // every block (fpb fragments; fpb divides 8 for block <= 512, and K64
-      // is a multiple of fpb) lies inside one chunk; its int32 MFMA chain
-      // starts from zero and is drained into the f32 sum once
+    for (int j0 = 0; j0 < CH; ++j0) {
+      const int f = ch * CH + j0;
+      if (f >= K64 || (j0 % fpb) != 0) continue;
+      const int b = f / fpb;
+      const float wsb = wsc[slot][j0 / fpb];
+      v4i acc[MI];
 #pragma unroll
-      for (int j0 = 0; j0 < 8; j0 += 1) {
-        const int f = f0 + j0;
-        if (f >= K64 || (f % fpb) != 0) continue;
-        const int b = f / fpb;
-        const float wsb = wsr[b];
-        v4i acc[MI];
+      for (int mi = 0; mi < MI; ++mi) acc[mi] = {0, 0, 0, 0};
 #pragma unroll
-        for (int mi = 0; mi < MI; ++mi) acc[mi] = {0, 0, 0, 0};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (q >= fpb) break;
-          const int ff = f + q;
-#pragma unroll
-          for (int mi = 0; mi < MI; ++mi) {
-            const v4i xa = *reinterpret_cast<const v4i*>(
-                s_x + (size_t)(16 * mi + (lane & 15)) * xstride + ff * 64 + (lane >> 4) * 16);
-            acc[mi] = mfma16x16x64(xa, wf[(j0 + q) & 7], acc[mi]);
-          }
-        }
+      for (int q = 0; q < CH; ++q) {
+        if (q >= fpb) break;
+        const int ff = f + q;
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi) {
-          const float4 sv = *reinterpret_cast<const float4*>(s_sa + b * RP + 16 * mi + 4 * (lane >> 4));
-          raw[mi][0] = raw[mi][0] + (float)acc[mi][0] * sv.x * wsb;
-          raw[mi][1] = raw[mi][1] + (float)acc[mi][1] * sv.y * wsb;
-          raw[mi][2] = raw[mi][2] + (float)acc[mi][2] * sv.z * wsb;
-          raw[mi][3] = raw[mi][3] + (float)acc[mi][3] * sv.w * wsb;
+          const v4i xa = *reinterpret_cast<const v4i*>(
+              s_x + (size_t)(16 * mi + (lane & 15)) * xstride + ff * 64 + (lane >> 4) * 16);
+          acc[mi] = mfma16x16x64(xa, wf[slot][(j0 + q) % CH], acc[mi]);
         }
       }
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const float4 sv = *reinterpret_cast<const float4*>(s_sa + b * RP + 16 * mi + 4 * (lane >> 4));
+        raw[mi][0] = raw[mi][0] + (float)acc[mi][0] * sv.x * wsb;
+        raw[mi][1] = raw[mi][1] + (float)acc[mi][1] * sv.y * wsb;
+        raw[mi][2] = raw[mi][2] + (float)acc[mi][2] * sv.z * wsb;
+        raw[mi][3] = raw[mi][3] + (float)acc[mi][3] * sv.w * wsb;
+      }
     }
-    // epilogue: y = bf16(softcap(raw)), score = y/T + gumbel
+    if (ch != nch - 1) return;  // uniform
+    // the strip's epilogue: y = bf16(softcap(raw)), score = y/T + gumbel
+    const int col = (s0 + si * stride) * 16 + (lane & 15);  // this lane's vocabulary row
     const int64_t gidx = a.vbase + col;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 16 * mi + 4 * (lane >> 4) + v;
+        const float rv = raw[mi][v];
+        raw[mi][v] = 0.0f;
         if (r >= a.R) continue;
-        const uint16_t yb = f32_to_bf16(tanh_f32(raw[mi][v] / a.cap) * a.cap);
+        const uint16_t yb = f32_to_bf16(tanh_f32(rv / a.cap) * a.cap);
         a.y[(size_t)r * a.V + col] = yb;
         const float yt = bf16_to_f32(yb) * s_invt[r];
         const float g = s_greedy[r] ? 0.0f : gumbel_noise(s_seed[r], r, gidx);
@@ -256,6 +281,13 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
         // lse_push (flash_sample.mojo:77-85)
         lse_merge(lmx[mi][v], lsum[mi][v], yt, 1.0f);
       }
+  };
+  for (int st = 0; st < nsteps; st += 2) {
+    if (st + 1 < nsteps) load(1, st + 1);
+    compute(0, st);
+    if (st + 1 >= nsteps) break;
+    if (st + 2 < nsteps) load(0, st + 2);
+    compute(1, st + 1);
   }
 
   // fold the 16 lanes sharing each row (lane & 15 = vocabulary column) and
@@ -715,10 +747,15 @@ hipError_t launch_embed(const int32_t* tokens, const int8_t* w, const float* ws,
   return hipGetLastError();
 }
 
+// One workgroup of 8 waves per CU, each wave walking its strips: the
+// 262144 x 2816 head (761 MB) 1 row 190.5 -> 182.2 us, 16 rows 237.1 ->
+// 230.2 us against 1024 workgroups (two per CU in two rounds; 512: 188.2 /
+// 235.3 us).  BQ_HEAD_GRID overrides it.
 int head_grid(int vocab) {
   const int strips = vocab / 16;
   const int g = (strips + kHeadWaves - 1) / kHeadWaves;
-  return g < 1024 ? g : 1024;
+  const int cap = tune().head_grid ? tune().head_grid : tune().cus;
+  return g < cap ? g : cap;
 }
 
 struct HeadWs {
@@ -760,10 +797,17 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
   const int grid = head_grid(V);
   const int RP = R <= 16 ? 16 : 32;
   const size_t lds = (size_t)RP * (H + 16) + (size_t)(H / block) * RP * sizeof(float);
-  if (R <= 16)
-    hipLaunchKernelGGL(k_head_logits<1>, dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+  // chunks of 4 fragments up to block 256 (104 VGPRs, two slots of 4 KiB
+  // per wave), else 8 (a block never spans two chunks)
+  const bool ch4 = block <= 256;
+  if (R <= 16 && ch4)
+    hipLaunchKernelGGL((k_head_logits<1, 4>), dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+  else if (R <= 16)
+    hipLaunchKernelGGL((k_head_logits<1, 8>), dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+  else if (ch4)
+    hipLaunchKernelGGL((k_head_logits<2, 4>), dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
   else
-    hipLaunchKernelGGL(k_head_logits<2>, dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
+    hipLaunchKernelGGL((k_head_logits<2, 8>), dim3(grid), dim3(64 * kHeadWaves), lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 

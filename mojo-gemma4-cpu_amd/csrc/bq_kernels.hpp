@@ -28,6 +28,7 @@ struct Tune {
   int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
   int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (12)
   int gu_skinny;    // BQ_GU_SKINNY: skinny MoE gate/up, k-steps per register slot (4)
+  int head_grid;    // BQ_HEAD_GRID: vocabulary-head workgroups (one per CU)
   int cus;          // compute units of the device
 };
 const Tune& tune();
