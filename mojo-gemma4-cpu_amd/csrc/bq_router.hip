@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void k_route_topk(
 // weight in LDS, and the schedule is built from there (schedule_small) --
 // what k_route_topk followed by k_build_schedule_small write, in one launch.
 template <int NE, int TPW>
-__global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
+__device__ inline void route_schedule_block(
     const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
     int32_t* __restrict__ route_idx, float* __restrict__ route_w,
     int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
@@ -313,6 +313,15 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
   schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
 }
 
+template <int NE, int TPW>
+__global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
+    const float* __restrict__ logits, const uint16_t* __restrict__ pes, int T, int E, int top_k,
+    int32_t* __restrict__ route_idx, float* __restrict__ route_w,
+    int32_t* __restrict__ expert_offset, Route* __restrict__ routes) {
+  route_schedule_block<NE, TPW>(logits, pes, T, E, top_k, route_idx, route_w, expert_offset,
+                                routes);
+}
+
 // The MoE block's prep for a decode-sized batch in one launch: the route
 // top-k + softmax merge, the norm-quant of the hidden states and the CSR
 // schedule -- the reference's dispatch_merge_router_candidates,
@@ -326,12 +335,14 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
 // workgroup fences its route stores at device scope before it counts itself
 // done on *done, and the last one fences again before it reads them.  That
 // one resets *done for the next launch, so launches on one device must not
-// overlap (stream order gives that).
+// overlap (stream order gives that).  With ONE > 0 (up to 16 tokens) a single
+// workgroup after the norm-quant ones takes every token's top-k and builds
+// the schedule from LDS (route_schedule_block), with no hand-off.
 constexpr int kPrepThreads = kSchedSmallSlots;   // 16 waves
 constexpr int kPrepTopkTokens = kPrepThreads / 64;
 __device__ unsigned g_prep_done = 0;
 
-template <int NE, int NSEG, int SPW>
+template <int NE, int NSEG, int SPW, int ONE = 0>  // ONE: tokens per wave of the one route workgroup
 __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
     const float* __restrict__ logits, const uint16_t* __restrict__ pes,
     const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
@@ -384,6 +395,13 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
     for (int i = 0; i < SPW; ++i)
       if (q0 + i < nseg) qrow[64 * (q0 + i)] = nq_pair_code(v[i], inv);
     if (lane == 0 && wv == 0) sa[t] = amax;
+    return;
+  }
+  if constexpr (ONE > 0) {
+    // one workgroup: every token's top-k (ONE per wave at a time) and the
+    // schedule from LDS, no cross-workgroup hand-off
+    route_schedule_block<NE, ONE>(logits, pes, T, E, top_k, route_idx, route_w, expert_offset,
+                                  routes);
     return;
   }
   // ---- top-k + softmax merge: token 16 b' + wave
@@ -586,14 +604,25 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
   const hipError_t ra = prep_counter(&done);
   if (ra != hipSuccess) return ra;
   const int nq_blocks = (T + 1) / 2;
-  const dim3 g(nq_blocks + (T + kPrepTopkTokens - 1) / kPrepTopkTokens), b(kPrepThreads);
+  // up to 16 tokens one workgroup takes every top-k (one token per wave) and
+  // builds the schedule from LDS, with no cross-workgroup hand-off: the
+  // batch-16 decoder layer's MoE 106.6 -> 105.1 us.  At 32 tokens (two per
+  // wave) the spread top-k with the last-workgroup schedule is faster
+  // (127.7 vs 129.9 us for the layer).  BQ_PREP_ONE=0 keeps the spread form.
+  const bool one = tune().prep_one && T <= kPrepTopkTokens;
+  const dim3 g(nq_blocks + (one ? 1 : (T + kPrepTopkTokens - 1) / kPrepTopkTokens)), b(kPrepThreads);
   const float sc = fwht_scale_host(block);
   const int ne = (E + 63) / 64;
 #define BQ_PREP(NEV, N, S)                                                                        \
   if (ne <= NEV && ns <= N && spw == S) {                                                        \
-    hipLaunchKernelGGL((k_moe_prep<NEV, N, S>), g, b, 0, st, logits, pes, src, gamma, xq, sa,     \
-                       route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,    \
-                       sqrt_n, n_eps, sc, nq_blocks, done);                                       \
+    if (one)                                                                                      \
+      hipLaunchKernelGGL((k_moe_prep<NEV, N, S, 1>), g, b, 0, st, logits, pes, src, gamma, xq, sa, \
+                         route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,  \
+                         sqrt_n, n_eps, sc, nq_blocks, done);                                     \
+    else                                                                                          \
+      hipLaunchKernelGGL((k_moe_prep<NEV, N, S>), g, b, 0, st, logits, pes, src, gamma, xq, sa,   \
+                         route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,  \
+                         sqrt_n, n_eps, sc, nq_blocks, done);                                     \
     return hipGetLastError();                                                                     \
   }
 #define BQ_PREP_NQ(NEV) \

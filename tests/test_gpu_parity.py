@@ -385,7 +385,9 @@ def test_route_schedule(gpu, O, T, E, k, pes):
 def test_moe_prep(gpu, O, T, E, k, H, B, pes):
     """route top-k + softmax, the CSR schedule and the norm-quant of the MoE
     input in one call against the oracle, bit-exact: one launch up to 1024
-    slots; above, with FWHT block 128, the top-k and the norm-quant in one
+    slots (up to 16 tokens one workgroup takes the whole top-k and schedule,
+    above that the last of the top-k workgroups builds the schedule); above,
+    with FWHT block 128, the top-k and the norm-quant in one
     launch and the schedule in a second (T = 129, 257, 600, 2048), else the
     separate launches (T = 301 at block 256).  Three calls in a row (the
     small launch's completion counter is reset by the workgroup that builds
@@ -415,7 +417,7 @@ def test_moe_prep_batches_in_a_row(gpu, O):
     workgroup counts share the completion counter) match the separate calls"""
     E, k, H = 128, 8, 2816
     g = O.f32_to_bf16(O.synth_normal_f32(75, 0.3, (H,)) + 1.0)
-    for T in (32, 5, 64, 1, 32):
+    for T in (32, 5, 64, 1, 16, 17, 32):
         logits = dev(O.synth_normal_f32(76 + T, 1.0, (T, E)))
         x = dev(O.synth_normal_bf16(77 + T, 1.0, (T, H)))
         idx, w, eo, routes, xq, sa = gpu.moe_prep(logits, x, dev(g), k)
