@@ -26,8 +26,8 @@ struct Tune {
   int nq_v8;        // BQ_NQ_V8: 0 disables the 8-values-per-lane norm-quant (block 128, many tokens)
   int moe_prep;     // BQ_MOE_PREP: 0 runs bq_moe_prep as separate launches
   int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
-  int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (12)
-  int gu_skinny;    // BQ_GU_SKINNY: skinny MoE gate/up, k-steps per register slot (4)
+  int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (12; 22, 14, 21)
+  int gu_skinny;    // BQ_GU_SKINNY: skinny MoE gate/up, k-steps per register slot (4; 2, 6)
   int head_grid;    // BQ_HEAD_GRID: vocabulary-head workgroups (one per CU)
   int prep_one;     // BQ_PREP_ONE: MoE prep's top-k + schedule in one workgroup (up to 16 tokens)
   int cus;          // compute units of the device

@@ -475,8 +475,8 @@ hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_
                        gu_scale, bucket, bi8, bsa, fwht_scale_host(64), experts, hidden, inter,  \
                        max_routes);                                                               \
     break;
-  switch (tune().gu_skinny) {
-    BQ_GU(2) BQ_GU(3) BQ_GU(6)
+  switch (tune().gu_skinny) {  // 2 or 6 k-steps per register slot; 4 measured best
+    BQ_GU(2) BQ_GU(6)
     default: BQ_GU(4)
   }
 #undef BQ_GU
@@ -518,9 +518,7 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     break;                                                                                        \
   }
       switch (ut) {
-        BQ_DS(3, 2) BQ_DS(1, 3) BQ_DS(2, 3) BQ_DS(1, 4) BQ_DS(2, 4) BQ_DS(2, 1)
-        BQ_DS(4, 1) BQ_DS(4, 2)
-        BQ_DS(2, 2)
+        BQ_DS(2, 2) BQ_DS(1, 4) BQ_DS(2, 1)
         default: BQ_DS(1, 2)
       }
 #undef BQ_DS
