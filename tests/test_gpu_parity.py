@@ -527,6 +527,31 @@ def test_moe_duplicate_experts(gpu, O):
     np.testing.assert_array_equal(host(out), rout)
 
 
+@pytest.mark.parametrize("T,H", [(5, 832), (3, 320), (300, 832)])
+def test_moe_combine_ragged_hidden(gpu, O, T, H):
+    """Phase 2 with hidden not a multiple of the combine's 256-column
+    chunks (a partial last chunk below 256 tokens, whole rows above)
+    against the oracle, bit-exact."""
+    E, I, k = 8, 128, 2
+    idx, w = O.route_topk_softmax(O.synth_normal_f32(T + 11, 1.0, (T, E)), k)
+    B = 128 if H % 128 == 0 else 64
+    gq, gs, Wgu = weight(gpu, O, E * 2 * I, H, B, seed=21)
+    dq, ds, Wd = weight(gpu, O, E * H, I, 64, seed=22)
+    gp, gcs = O.pack_and_colsum(gq)
+    dp, dcs = O.pack_and_colsum(dq, 64, False)
+    x = O.synth_normal_bf16(T + 12, 1.0, (T, H))
+    xq, xsa = O.norm_quant(x, np.full(H, ONE, np.uint16), B)
+    eo, routes, bucket, bi8, bsa, accum, out = gpu_moe(gpu, dev(xq), dev(xsa), idx, w, Wgu, Wd,
+                                                       E, H, I)
+    reo, rroutes = O.build_schedule(idx, w, E)
+    rb = O.moe_phase1(xq, xsa, reo, rroutes, gp, gs, gcs, I)
+    np.testing.assert_array_equal(host(bucket), rb)
+    rbq, rbsa = O.block_quant(rb, 64, True)
+    racc, rout = O.moe_phase2(rbq, rbsa, reo, rroutes, T, dp, ds, dcs, H)
+    np.testing.assert_array_equal(host(accum), racc)
+    np.testing.assert_array_equal(host(out), rout)
+
+
 def test_moe_model_shape_decode(gpu, O, moe_model):
     """Gemma-4-26B-A4B expert shapes (H=2816, I=704, 128 experts, top-8), T=8."""
     m = moe_model
