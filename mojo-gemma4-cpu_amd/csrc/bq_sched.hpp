@@ -15,32 +15,36 @@ constexpr int kSchedSmallSlots = 1024;
 // route slot tid = token * top_k + k, with e its expert (0..E-1, or -1 for
 // no slot) and w its weight.  A slot's record is its expert's offset plus
 // the number of earlier slots routed to the same expert -- the (expert,
-// token, k) order.  Earlier slots of the same wave are counted by matching:
-// the wave takes one distinct expert at a time (its lowest unmatched lane's)
-// and ballots the lanes holding it; earlier waves' slots through an
-// exclusive prefix over the waves' per-expert counts (s_wc), and the experts'
-// offsets through a scan of their totals (s_cnt).
+// token, k) order.  Earlier slots of the same wave are counted from the
+// wave's experts staged in LDS (each lane compares the lanes below it: no
+// serial pass per distinct expert); earlier waves' slots through an
+// exclusive prefix over the waves' per-expert counts (s_wc, LDS atomics),
+// and the experts' offsets through a scan of their totals (s_cnt).
 constexpr int kSchedWavesSmall = kSchedSmallSlots / 64;
 
 __device__ inline void schedule_small(int e, float w, int top_k, int E,
                                       int (*s_wc)[kMaxExperts], int* s_cnt,
                                       int32_t* __restrict__ expert_offset,
                                       Route* __restrict__ routes) {
+  __shared__ __attribute__((aligned(16))) int s_key[kSchedSmallSlots];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   for (int i = tid; i < kSchedWavesSmall * kMaxExperts; i += kSchedSmallSlots)
     s_wc[i / kMaxExperts][i % kMaxExperts] = 0;
+  s_key[tid] = e;
   __syncthreads();
-  const unsigned long long below = (1ull << lane) - 1ull;
+  // rank among the wave's earlier lanes with the same expert; four keys per
+  // 16-byte LDS read (every lane reads the same address: a broadcast)
   int rank = 0;
-  unsigned long long active = __ballot(e >= 0);
-  while (active) {  // wave-uniform: one distinct expert per pass
-    const int leader = __ffsll((long long)active) - 1;
-    const int le = __builtin_amdgcn_readlane(e, leader);
-    const unsigned long long m = __ballot(e == le);
-    if (e == le) rank = __popcll(m & below);
-    if (lane == leader) s_wc[wave][le] = __popcll(m);
-    active &= ~m;
+  const int* wk = &s_key[wave * 64];
+#pragma unroll
+  for (int j0 = 0; j0 < 64; j0 += 4) {
+    const int4 k4 = *reinterpret_cast<const int4*>(wk + j0);
+    rank += (j0 + 0 < lane && k4.x == e) ? 1 : 0;
+    rank += (j0 + 1 < lane && k4.y == e) ? 1 : 0;
+    rank += (j0 + 2 < lane && k4.z == e) ? 1 : 0;
+    rank += (j0 + 3 < lane && k4.w == e) ? 1 : 0;
   }
+  if (e >= 0) atomicAdd(&s_wc[wave][e], 1);
   __syncthreads();
   for (int x = tid; x < E; x += kSchedSmallSlots) {  // prefix over waves, per expert
     int run = 0;
