@@ -151,7 +151,7 @@ def calib_lib():
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built (python __graft_entry__.py)")
     L = C.CDLL(path)
-    L.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    L.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     L.bqc_mfma_i8.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     L.bqc_mfma_i8_ops.argtypes = [C.c_int, C.c_int, C.c_int]
     L.bqc_mfma_i8_ops.restype = C.c_double
@@ -199,10 +199,16 @@ def bench_gemv(bq, torch, steps, warmup, reps=64):
                 s_fused=s_fused, rd=rd, codes=codes, scales=scales, xq=xq, sa=sa)
 
 
+def gemv_waves():
+    """Waves per workgroup of the decode GEMV: the library's default (16) or
+    BQ_GEMV_WAVES when that selects 8."""
+    return 8 if os.environ.get("BQ_GEMV_WAVES") == "8" else 16
+
+
 def bench_stream(torch, bufs, tiles, K64, steps, warmup):
     """The streaming-read kernel (bqc_stream_read): the GEMV's launch shape
-    (`tiles` workgroups x 8 waves, one-shot non-temporal 16-byte loads of
-    each wave's K64/8 fragments) over the GEMV's own replicas -> the measured
+    (`tiles` workgroups x gemv_waves() waves, one-shot non-temporal 16-byte
+    loads of each wave's K64/waves fragments) over the GEMV's own replicas -> the measured
     per-launch ceiling; the same grid reading nothing -> the fixed cost of a
     launch in a graph; and 256 MiB per launch (4096 workgroups) rotated over
     four windows of a 1 GiB buffer -> the sustained streaming rate."""
@@ -211,7 +217,7 @@ def bench_stream(torch, bufs, tiles, K64, steps, warmup):
 
     def launcher(ptrs, t, k):
         def f(i):
-            rc = L.bqc_stream_read(ptrs[i], t, k, sink.data_ptr(), _stream(torch))
+            rc = L.bqc_stream_read(ptrs[i], t, k, gemv_waves(), sink.data_ptr(), _stream(torch))
             if rc != 0:
                 raise RuntimeError(f"bqc_stream_read: hipError {rc}")
         return f
@@ -953,7 +959,7 @@ def main():
                                        f"{len(smp.ms)} graph replays of 64 launches; "
                                        "measured_peak = the same-launch-shape streaming read "
                                        "of the same replicas (p50)"})
-        line["gemv_detail"] = {"kernel": "k_linear_skinny<8, false, 8>",
+        line["gemv_detail"] = {"kernel": f"k_linear_skinny<{gemv_waves()}, false, {64 // gemv_waves()}>",
                                "alg_bytes_per_launch": gv["alg_bytes"],
                                "best_GBs": round(gv["gbs_min"], 1), **smp.summary(),
                                "norm_quant": gv["s_nq"].summary(),
@@ -963,8 +969,9 @@ def main():
                                    **gv["s_fused"].summary()}}
         rd = gv["rd"]
         line["stream_read_same_shape"] = {
-            "kernel": "k_stream_read (256 workgroups x 8 waves, one-shot non-temporal 16-byte "
-                      "loads of each wave's 8 KiB slice; the GEMV's launch without arithmetic)",
+            "kernel": f"k_stream_read (256 workgroups x {gemv_waves()} waves, one-shot non-temporal 16-byte "
+                      f"loads of each wave's {64 // gemv_waves()} KiB slice; the GEMV's launch without "
+                      "arithmetic)",
             "bytes_per_launch": rd["bytes"], "p50_GBs": round(rd["gbs"], 1),
             "best_GBs": round(rd["gbs_best"], 1),
             "frac_of_datasheet": round(rd["gbs"] / HBM_PEAK_GBS, 4), **rd["same"].summary(),

@@ -3,12 +3,12 @@
 // libbq.so) and compute nothing a caller uses.
 //
 // bqc_stream_read: the decode GEMV's launch shape and read pattern with the
-//   arithmetic taken out.  One 512-thread workgroup per 16-row tile of a
-//   tile16x64 weight (tile t at byte t * K64 * 1024), 8 waves splitting the
+//   arithmetic taken out.  One workgroup per 16-row tile of a tile16x64
+//   weight (tile t at byte t * K64 * 1024), W = 8 or 16 waves splitting the
 //   K64 fragments of 1 KiB evenly, each lane loading its 16 bytes of every
 //   fragment of its slice, the whole slice requested at once with
-//   non-temporal loads (k_linear_skinny<8, false, 8> does exactly this for
-//   K <= 4096).  Each wave's bytes are XOR-folded into one 16-byte value per
+//   non-temporal loads (k_linear_skinny<16, false, 4> and <8, false, 8> do
+//   exactly this for K <= 4096).  Each wave's bytes are XOR-folded into one 16-byte value per
 //   lane, the waves' partial tiles reduced through LDS as the GEMV reduces its
 //   int32 tiles, and 16 uint16 written per workgroup, the GEMV's 16 bf16
 //   outputs.  Its per-launch time is the
@@ -24,8 +24,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int kWaves = 8, kU = 8;
-
+template <int kWaves, int kU>
 __global__ __launch_bounds__(kWaves * 64) void k_stream_read(const int8_t* __restrict__ w,
                                                              int K64, uint16_t* __restrict__ out) {
   __shared__ int part[kWaves * 256];
@@ -105,14 +104,20 @@ __global__ __launch_bounds__(256) void k_mfma_i8(int iters, int* __restrict__ ou
 
 extern "C" {
 
-// w: tiles * K64 * 1024 bytes (16-byte aligned); out: tiles * 16 uint16.
-// K64 <= 64 keeps the launch the GEMV's one-shot shape; K64 = 0 launches the
-// same grid reading nothing (the fixed cost of a launch).  Returns a hipError_t.
-int bqc_stream_read(const int8_t* w, int tiles, int K64, uint16_t* out, void* stream) {
-  if (!w || !out || tiles <= 0 || K64 < 0 || K64 > kWaves * kU) return (int)hipErrorInvalidValue;
+// w: tiles * K64 * 1024 bytes (16-byte aligned); out: tiles * 16 uint16;
+// waves 8 or 16 (the GEMV's workgroup).  K64 <= 64 keeps the launch the
+// GEMV's one-shot shape; K64 = 0 launches the same grid reading nothing (the
+// fixed cost of a launch).  Returns a hipError_t.
+int bqc_stream_read(const int8_t* w, int tiles, int K64, int waves, uint16_t* out, void* stream) {
+  if (!w || !out || tiles <= 0 || K64 < 0 || K64 > 64 || (waves != 8 && waves != 16))
+    return (int)hipErrorInvalidValue;
   if (reinterpret_cast<uintptr_t>(w) & 15u) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_stream_read, dim3(tiles), dim3(kWaves * 64), 0, (hipStream_t)stream, w,
-                     K64, out);
+  if (waves == 16)
+    hipLaunchKernelGGL((k_stream_read<16, 4>), dim3(tiles), dim3(16 * 64), 0, (hipStream_t)stream,
+                       w, K64, out);
+  else
+    hipLaunchKernelGGL((k_stream_read<8, 8>), dim3(tiles), dim3(8 * 64), 0, (hipStream_t)stream,
+                       w, K64, out);
   return (int)hipGetLastError();
 }
 

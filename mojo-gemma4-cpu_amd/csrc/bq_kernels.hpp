@@ -13,7 +13,7 @@ namespace bq {
 // and the device's compute-unit count, read once: at bq_init, or at the
 // first launch of a process that never called it.
 struct Tune {
-  int gemv_waves;   // BQ_GEMV_WAVES: waves per decode-GEMV workgroup (4, 8, 16)
+  int gemv_waves;   // BQ_GEMV_WAVES: waves per decode-GEMV workgroup (4, 8, 16; default 16)
   int tile_bm;      // BQ_TILE_BM: rows per tiled prefill tile (32, 64, 128)
   int tile_bn;      // BQ_TILE_BN: columns per tiled tile (128, 256)
   int ring;         // BQ_RING: LDS ring stages of the tiled kernels
