@@ -92,7 +92,10 @@ void tune_init(int device) {
   t.tile_ksp = env_int("BQ_TILE_KSP");
   t.moe_bm = env_int("BQ_MOE_BM");
   t.moe_bm_down = env_int("BQ_MOE_BM_DOWN");
-  t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 2;
+  // n-tile fastest over the whole grid: the 2048-token layer 310.9 -> 308.0
+  // us against an m-tile's n-tiles on one XCD (order 2, faster when the
+  // gate/up and down kernels took 142 / 128 us)
+  t.moe_order = getenv("BQ_MOE_ORDER") ? env_int("BQ_MOE_ORDER") : 0;
   t.down_breg = getenv("BQ_DOWN_BREG") ? env_int("BQ_DOWN_BREG") : 1;
   t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
   t.moe_prep = getenv("BQ_MOE_PREP") ? env_int("BQ_MOE_PREP") : 1;
