@@ -902,10 +902,12 @@ hipError_t launch_flash_attn(const AttnArgs& a, int head_dim, hipStream_t st) {
 }
 
 int attn_splits(int seq_len, int num_kv, int max_kv_len) {
-  // enough splits for ~2048 waves, each at least kAttnMinSplit positions
+  // enough splits for ~2048 waves (BQ_ATTN_WAVES), each at least
+  // kAttnMinSplit positions
   if (seq_len <= 0 || num_kv <= 0) return 1;
   const int64_t items = (int64_t)seq_len * num_kv;
-  int s = (int)((2048 + items - 1) / items);
+  const int64_t target = tune().attn_waves ? tune().attn_waves : 2048;
+  int s = (int)((target + items - 1) / items);
   const int cap = max_kv_len > 0 ? (max_kv_len + kAttnMinSplit - 1) / kAttnMinSplit : 1;
   if (s > cap) s = cap;
   return s < 1 ? 1 : s;
