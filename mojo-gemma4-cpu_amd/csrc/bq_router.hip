@@ -551,8 +551,10 @@ __global__ __launch_bounds__(256) void k_topk_norm_quant(
 
 // The prep in one launch (k_moe_prep) for T * top_k <= 1024 slots, E <= 256
 // and the pair-layout norm-quant's shapes (hidden % 256 == 0, <= 4096, FWHT
-// block <= 512, 2-byte aligned codes); otherwise the route top-k + schedule
-// and the norm-quant as separate launches.  Same results either way.
+// block <= 512, 2-byte aligned codes); above 1024 slots with FWHT block 128,
+// the top-k and the norm-quant in one launch (k_topk_norm_quant) and the
+// schedule in a second; otherwise the route top-k + schedule and the
+// norm-quant as separate launches.  Same results either way.
 hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint16_t* src,
                            const uint16_t* gamma, int T, int E, int top_k, int hidden, int block,
                            float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
