@@ -209,11 +209,13 @@ int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale,
  * route_idx / route_w / expert_offset / routes from logits, x_i8 / x_sa from
  * x and gamma.  For seq_len * top_k <= 1024 slots and the pair-layout
  * norm-quant's shapes (hidden % 256 == 0, hidden <= 4096) it is one launch,
- * in which workgroups quantize the rows while others take the top-k, and
- * the last top-k workgroup to finish builds the schedule (a device-scope
- * counter of the library's, reset by that workgroup: calls on one device
- * must not overlap in time, as stream order gives); otherwise the separate
- * launches.  The checks of both calls apply. */
+ * in which workgroups quantize the rows while others take the top-k: up to
+ * 16 tokens one workgroup takes every top-k and builds the schedule, above
+ * that the last top-k workgroup to finish builds it (a device-scope counter
+ * of the library's, reset by that workgroup: calls on one device must not
+ * overlap in time, as stream order gives).  Above 1024 slots with block 128
+ * the top-k and the norm-quant share one launch and the schedule follows;
+ * otherwise the separate launches.  The checks of both calls apply. */
 int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,
                 const uint16_t* gamma, int seq_len, int experts, int top_k, int hidden, int block,
                 float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
