@@ -104,6 +104,7 @@ void tune_init(int device) {
   t.gu_skinny = getenv("BQ_GU_SKINNY") ? env_int("BQ_GU_SKINNY") : 4;
   t.head_grid = env_int("BQ_HEAD_GRID");
   t.attn_waves = env_int("BQ_ATTN_WAVES");
+  t.sel_fused = getenv("BQ_SEL_FUSED") ? env_int("BQ_SEL_FUSED") : 1;
   t.prep_one = getenv("BQ_PREP_ONE") ? env_int("BQ_PREP_ONE") : 1;
   // 16x16x64 by default: these LDS-ring kernels wait on their operand
   // stream, not on the MFMA rate (gate/up at 2048 tokens: 142 us with

@@ -374,6 +374,7 @@ struct SelArgs {
   int* cnt;            // [R] candidates appended
   uint64_t* cand;      // [R, 256] (key << 32) | (0x7FFFFFFF - index)
   int V, nc;
+  int fused;           // 1: each chunk workgroup derives its row's thresholds itself
 };
 
 // this thread's 16 keys of chunk c (V % 16 == 0: all valid or none)
@@ -441,8 +442,11 @@ __device__ inline void pick_bin(int suffix, int total, int need, int base, int* 
   }
 }
 
-__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_hi(SelArgs a) {
-  const int r = blockIdx.x, tid = threadIdx.x;
+// Row r's high byte hb of the 256th largest key and the count of keys in
+// higher bins, from every chunk's high-byte histogram (all kChunkThreads
+// threads call it; every thread gets the results).
+__device__ inline void row_thr_hi(const SelArgs& a, int r, int& hb, int& above_hb) {
+  const int tid = threadIdx.x;
   __shared__ int tmp[4];
   __shared__ int s_bin, s_above;
   int total = 0;
@@ -454,9 +458,16 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_thr_hi(SelArgs a) {
   const int suf = suffix_sum256(total, tmp);
   pick_bin(suf, total, need, 0, &s_bin, &s_above);
   __syncthreads();
-  if (tid == 0) {
-    a.thr[r * 4 + 0] = s_bin;
-    a.thr[r * 4 + 1] = s_above;
+  hb = s_bin;
+  above_hb = s_above;
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_hi(SelArgs a) {
+  int hb, above;
+  row_thr_hi(a, blockIdx.x, hb, above);
+  if (threadIdx.x == 0) {
+    a.thr[blockIdx.x * 4 + 0] = hb;
+    a.thr[blockIdx.x * 4 + 1] = above;
   }
 }
 
@@ -464,8 +475,19 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_hist_lo(SelArgs a) {
   const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
   __shared__ uint32_t hist[256];
   hist[tid] = 0;
-  __syncthreads();
-  const uint32_t hb = (uint32_t)a.thr[r * 4 + 0];
+  uint32_t hb;
+  if (a.fused) {  // uniform
+    int b, above;
+    row_thr_hi(a, r, b, above);  // (its barriers also cover the zeroing above)
+    hb = (uint32_t)b;
+    if (c == 0 && tid == 0) {
+      a.thr[r * 4 + 0] = b;
+      a.thr[r * 4 + 1] = above;
+    }
+  } else {
+    __syncthreads();
+    hb = (uint32_t)a.thr[r * 4 + 0];
+  }
   uint32_t k[16];
   const bool ok = chunk_keys(a, r, c, k);
 #pragma unroll
@@ -474,10 +496,15 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_hist_lo(SelArgs a) {
   a.hist2[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];
 }
 
-__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_lo(SelArgs a) {
-  const int r = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+// Row r's threshold key t (its 256th largest), the ties (keys == t) the
+// selection needs, and the ties in the chunks before chunk `want` (every
+// chunk's with want < 0, written to eqpre), from every chunk's low-byte
+// histogram of the keys in bin hb.  All kChunkThreads threads call it.
+__device__ inline void row_thr_lo(const SelArgs& a, int r, int want, uint32_t& t_out,
+                                  int& ties_out, int& eqb_out) {
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   __shared__ int tmp[4];
-  __shared__ int s_bin, s_above;
+  __shared__ int s_bin, s_above, s_eqb;
   int total = 0;
 #pragma unroll 8
   for (int c = 0; c < a.nc; ++c) total += (int)a.hist2[((size_t)r * a.nc + c) * 256 + tid];
@@ -502,10 +529,21 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_thr_lo(SelArgs a) {
   __syncthreads();
   int before = 0;
   for (int w = 0; w < wave; ++w) before += tmp[w];
-  if (tid < a.nc) a.eqpre[(size_t)r * a.nc + tid] = before + incl - e;
-  if (tid == 0) {
-    a.thr[r * 4 + 2] = (hb << 8) | lb;
-    a.thr[r * 4 + 3] = need - s_above;  // ties needed
+  if (want < 0 && tid < a.nc) a.eqpre[(size_t)r * a.nc + tid] = before + incl - e;
+  if (tid == want) s_eqb = before + incl - e;
+  __syncthreads();
+  t_out = (uint32_t)((hb << 8) | lb);
+  ties_out = need - s_above;
+  eqb_out = want >= 0 ? s_eqb : 0;
+}
+
+__global__ __launch_bounds__(kChunkThreads) void k_sel_thr_lo(SelArgs a) {
+  uint32_t t;
+  int ties, eqb;
+  row_thr_lo(a, blockIdx.x, -1, t, ties, eqb);
+  if (threadIdx.x == 0) {
+    a.thr[blockIdx.x * 4 + 2] = (int)t;
+    a.thr[blockIdx.x * 4 + 3] = ties;  // ties needed
   }
 }
 
@@ -513,9 +551,15 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_collect(SelArgs a) {
   const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   __shared__ int tmp_e[4], tmp_s[4];
   __shared__ int s_base;
-  const uint32_t t = (uint32_t)a.thr[r * 4 + 2];
-  const int ties_needed = a.thr[r * 4 + 3];
-  const int eq_before = a.eqpre[(size_t)r * a.nc + c];
+  uint32_t t;
+  int ties_needed, eq_before;
+  if (a.fused) {  // uniform
+    row_thr_lo(a, r, c, t, ties_needed, eq_before);
+  } else {
+    t = (uint32_t)a.thr[r * 4 + 2];
+    ties_needed = a.thr[r * 4 + 3];
+    eq_before = a.eqpre[(size_t)r * a.nc + c];
+  }
   uint32_t k[16];
   const bool ok = chunk_keys(a, r, c, k);
   // ties before this thread's keys, in index order
@@ -822,10 +866,14 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
   s.V = V;
   s.nc = (V + kChunk - 1) / kChunk;
   const dim3 cg(s.nc, R), cb(kChunkThreads);
+  // each chunk workgroup of hist_lo and collect derives its row's thresholds
+  // from the histograms itself (the two one-workgroup-per-row threshold
+  // launches go; BQ_SEL_FUSED=0 keeps them)
+  s.fused = tune().sel_fused;
   hipLaunchKernelGGL(k_sel_hist_hi, cg, cb, 0, st, s);
-  hipLaunchKernelGGL(k_sel_thr_hi, dim3(R), cb, 0, st, s);
+  if (!s.fused) hipLaunchKernelGGL(k_sel_thr_hi, dim3(R), cb, 0, st, s);
   hipLaunchKernelGGL(k_sel_hist_lo, cg, cb, 0, st, s);
-  hipLaunchKernelGGL(k_sel_thr_lo, dim3(R), cb, 0, st, s);
+  if (!s.fused) hipLaunchKernelGGL(k_sel_thr_lo, dim3(R), cb, 0, st, s);
   hipLaunchKernelGGL(k_sel_collect, cg, cb, 0, st, s);
   hipLaunchKernelGGL(k_head_select, dim3(R), dim3(kSelThreads), 0, st, s.cand, a.part, grid, RP,
                      params, out, V, vbase);

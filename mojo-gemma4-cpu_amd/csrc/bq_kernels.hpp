@@ -29,6 +29,7 @@ struct Tune {
   int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (12; 22, 14, 21)
   int gu_skinny;    // BQ_GU_SKINNY: skinny MoE gate/up, k-steps per register slot (4; 2, 6)
   int head_grid;    // BQ_HEAD_GRID: vocabulary-head workgroups (one per CU)
+  int sel_fused;    // BQ_SEL_FUSED: 0 keeps the head selection's two threshold launches
   int attn_waves;   // BQ_ATTN_WAVES: waves the attention split plan aims for (2048)
   int prep_one;     // BQ_PREP_ONE: MoE prep's top-k + schedule in one workgroup (up to 16 tokens)
   int cus;          // compute units of the device
