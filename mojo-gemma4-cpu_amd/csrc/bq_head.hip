@@ -656,26 +656,35 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
   }
 
   // 2. the selected candidates, padded and sorted descending by
-  // (key, -index): bitonic over 256 entries
+  // (key, -index): bitonic over 256 entries, one per thread, in registers.
+  // A stride below 64 pairs lanes of one wave (cross-lane shuffles, no
+  // barrier); strides 64 and 128 (three of the 36 stages) pair waves through
+  // LDS, alternating two buffers so one barrier per stage suffices.
+  static_assert(kSampleNmax == kSelThreads, "one candidate per thread");
   const int need = V < kSampleNmax ? V : kSampleNmax;
-  if (tid < kSampleNmax) cand[tid] = tid < need ? cand_g[(size_t)r * kSampleNmax + tid] : 0ull;
-  __syncthreads();
+  uint64_t key = tid < need ? cand_g[(size_t)r * kSampleNmax + tid] : 0ull;
+  __shared__ uint64_t xch[2][kSampleNmax];
+  int xb = 0;
   for (int size = 2; size <= kSampleNmax; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (tid < kSampleNmax) {
-        const int j = tid ^ stride;
-        if (j > tid) {
-          const bool desc = (tid & size) == 0;
-          const uint64_t a0 = cand[tid], a1 = cand[j];
-          if (desc ? (a0 < a1) : (a0 > a1)) {
-            cand[tid] = a1;
-            cand[j] = a0;
-          }
-        }
+      uint64_t other;
+      if (stride < 64) {
+        const uint32_t lo = __shfl_xor((uint32_t)key, stride, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), stride, 64);
+        other = ((uint64_t)hi << 32) | lo;
+      } else {
+        xch[xb][tid] = key;
+        __syncthreads();
+        other = xch[xb][tid ^ stride];
+        xb ^= 1;
       }
-      __syncthreads();
+      // the lower entry of a pair takes the larger key in a descending run
+      const bool take_max = ((tid & stride) == 0) == ((tid & size) == 0);
+      key = take_max ? (other > key ? other : key) : (other < key ? other : key);
     }
   }
+  cand[tid] = key;
+  __syncthreads();
 
   // 3. finalize (flash_sample.mojo:232-265).  The min_p / top_k pick scans
   // the top list keeping the first strictly larger score among entries
