@@ -71,6 +71,46 @@ __global__ __launch_bounds__(256) void k_head_prep(
   }
 }
 
+// Head prep with FWHT block 128 (hidden % 256 == 0, hidden <= 128 * NSEG <=
+// 4096, 16-byte aligned gain, 8-byte aligned codes): a workgroup of
+// ceil(hidden / 512) waves per row, wave w holding values 512w .. 512w + 511
+// as 8 consecutive values per lane, so a 128-value block is one row of 16
+// lanes and its scale is the max over those lanes.  The same norm and
+// transform as the per-row norm-quant (nq_pair_sumsq's chains, x * inv_rms *
+// gain, nq_v8_transform), quantized per block (runtime.mojo:11-37 with a
+// per-block scale).
+template <int NSEG>
+__global__ __launch_bounds__(512) void k_head_prep_v8(
+    const uint16_t* __restrict__ src, const uint16_t* __restrict__ gamma,
+    int8_t* __restrict__ xq, float* __restrict__ sa, int hidden, float sqrt_n, float n_eps,
+    float fwht_scale) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int t = blockIdx.x, nseg = hidden >> 7;
+  const uint16_t* row = src + (size_t)t * hidden;
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(row) + lane;
+  uint32_t xp[NSEG];
+#pragma unroll
+  for (int q = 0; q < NSEG; ++q)
+    if (q < nseg) xp[q] = xr[64 * q];
+  const int e0 = 512 * wave + 8 * lane;
+  const int ec = min(e0, hidden - 8);  // runs past the row are read, never stored
+  const v4i xv = *reinterpret_cast<const v4i*>(row + ec);
+  const v4i gv = *reinterpret_cast<const v4i*>(gamma + ec);
+  const float total = nq_pair_sumsq<NSEG>(xp, nseg);
+  const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
+  float v[8];
+  float m = nq_v8_transform(xv, gv, inv_rms, fwht_scale, v);
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+  if (e0 < hidden) {  // a whole 16-lane block is in or out (hidden % 128 == 0)
+    uint32_t w[2];
+    nq_v8_codes(v, m > 0.0f ? 127.0f / m : 0.0f, w);
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2*>(xq + (size_t)t * hidden + e0) = u2{w[0], w[1]};
+    if ((lane & 15) == 0) sa[(size_t)t * nseg + (e0 >> 7)] = m;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // embedding lookup: one workgroup (4 waves) per token; wave w rotates blocks
 // w, w+4, ... of the row read from the tile16x64 layout.
@@ -774,6 +814,15 @@ hipError_t launch_head_prep(const uint16_t* src, const uint16_t* gamma, int8_t* 
                             hipStream_t st) {
   const float sc = fwht_scale_host(block);
   const int pu = pick_pu_bf16(hidden);
+  if (rows > 0 && hidden > 0 && block == 128 && pu == 8 && hidden <= 4096 && tune().nq_v8 &&
+      !(reinterpret_cast<uintptr_t>(gamma) & 15u) && !(reinterpret_cast<uintptr_t>(xq) & 7u)) {
+    // hidden 2816, one row: 7.4 us (k_head_prep<2>, min) -> 4.1 us
+    const int ns = hidden >> 7;
+    const dim3 g(rows), b(64 * ((hidden + 511) / 512));
+#define BQ_HP8(N) if (ns <= N) { hipLaunchKernelGGL((k_head_prep_v8<N>), g, b, 0, st, src, gamma, xq, sa, hidden, sqrt_n, n_eps, sc); return hipGetLastError(); }
+    BQ_HP8(8) BQ_HP8(16) BQ_HP8(22) BQ_HP8(24) BQ_HP8(32)
+#undef BQ_HP8
+  }
   const dim3 g(rows), b(256);
   switch (block) {
     case 64: hipLaunchKernelGGL(k_head_prep<1>, g, b, 0, st, src, gamma, xq, sa, hidden, pu, sqrt_n, n_eps, sc); break;

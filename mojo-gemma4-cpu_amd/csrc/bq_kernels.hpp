@@ -23,7 +23,7 @@ struct Tune {
   int moe_order;    // BQ_MOE_ORDER: MoE work order of the LDS-ring kernels (0, 1, 2)
   int down_breg;    // BQ_DOWN_BREG: 0 disables the register-streamed down kernel
   int nq_pair;      // BQ_NQ_PAIR: 0 disables the pair-layout norm-quant
-  int nq_v8;        // BQ_NQ_V8: 0 disables the 8-values-per-lane norm-quant (block 128, many tokens)
+  int nq_v8;        // BQ_NQ_V8: 0 disables the 8-values-per-lane norm-quant and head prep (block 128)
   int moe_prep;     // BQ_MOE_PREP: 0 runs bq_moe_prep as separate launches
   int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
   int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (12; 22, 14, 21)

@@ -40,9 +40,15 @@ def check_outcomes(got, ref):
 
 
 @pytest.mark.parametrize("R,H,B", [(1, 2816, 128), (5, 2816, 128), (32, 2816, 128),
-                                   (3, 512, 64), (3, 512, 256), (2, 1024, 512)])
+                                   (2, 4096, 128), (4, 256, 128), (3, 1280, 128),
+                                   (2, 640, 128), (3, 512, 64), (3, 512, 256), (2, 1024, 512)])
 def test_head_prep(gpu, O, R, H, B):
+    """FWHT block 128 with hidden % 256 == 0 takes the 8-values-per-lane form
+    (a block's scale is a max over 16 lanes); 640 and the other blocks take
+    the wave-per-block form. The last row's second block is all zeros: its
+    scale and codes are 0."""
     x = O.synth_normal_bf16(40 + R, 1.0, (R, H))
+    x[-1, B:2 * B] = 0
     g = O.f32_to_bf16(np.linspace(0.5, 1.5, H).astype(np.float32))
     q, sa = gpu.head_prep(dev(x), dev(g), B)
     rq, rsa = O.norm_quant(x, g, B, per_block=True)
