@@ -100,8 +100,10 @@ __global__ __launch_bounds__(512) void k_head_prep_v8(
   const float inv_rms = sqrt_n / __builtin_sqrtf(total + n_eps);
   float v[8];
   float m = nq_v8_transform(xv, gv, inv_rms, fwht_scale, v);
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+  m = fmaxf(m, xlane_partner<8>(m));  // the block's 16 lanes
+  m = fmaxf(m, xlane_partner<4>(m));
+  m = fmaxf(m, xlane_partner<2>(m));
+  m = fmaxf(m, xlane_partner<1>(m));
   if (e0 < hidden) {  // a whole 16-lane block is in or out (hidden % 128 == 0)
     uint32_t w[2];
     nq_v8_codes(v, m > 0.0f ? 127.0f / m : 0.0f, w);
@@ -659,6 +661,19 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
   __shared__ float r_bs[kSelWaves], r_mx[kSelWaves], r_sm[kSelWaves], r_ps[kSelWaves];
   __shared__ int r_bi[kSelWaves], r_pk[kSelWaves];
   const SamplingParams p = params[r];
+  // lane ^ stride's value (stride < 64) by the DPP / permlane moves of
+  // xlane_partner: bit moves, no LDS
+  auto partner = [](uint32_t x, int stride) -> uint32_t {
+    const float f = __uint_as_float(x);
+    switch (stride) {
+      case 1: return __float_as_uint(xlane_partner<1>(f));
+      case 2: return __float_as_uint(xlane_partner<2>(f));
+      case 4: return __float_as_uint(xlane_partner<4>(f));
+      case 8: return __float_as_uint(xlane_partner<8>(f));
+      case 16: return __float_as_uint(xlane_partner<16>(f));
+      default: return __float_as_uint(xlane_partner<32>(f));
+    }
+  };
 
   // 1. merge the per-workgroup partials in order
   float bs = kNegInf, mx = kNegInf, sm = 0.0f;
@@ -673,10 +688,10 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-      const float os = __shfl_xor(bs, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      const float om = __shfl_xor(mx, o, 64);
-      const float ou = __shfl_xor(sm, o, 64);
+      const float os = __uint_as_float(partner(__float_as_uint(bs), o));
+      const int oi = (int)partner((uint32_t)bi, o);
+      const float om = __uint_as_float(partner(__float_as_uint(mx), o));
+      const float ou = __uint_as_float(partner(__float_as_uint(sm), o));
       if (lane & o) {
         float m2 = om, s2 = ou;
         lse_merge(m2, s2, mx, sm);
@@ -697,20 +712,23 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
 
   // 2. the selected candidates, padded and sorted descending by
   // (key, -index): bitonic over 256 entries, one per thread, in registers.
-  // A stride below 64 pairs lanes of one wave (cross-lane shuffles, no
-  // barrier); strides 64 and 128 (three of the 36 stages) pair waves through
-  // LDS, alternating two buffers so one barrier per stage suffices.
+  // A stride below 64 pairs lanes of one wave (partner on both halves of the
+  // key, no barrier); strides
+  // 64 and 128 (three of the 36 stages) pair waves through LDS, alternating
+  // two buffers so one barrier per stage suffices.
   static_assert(kSampleNmax == kSelThreads, "one candidate per thread");
   const int need = V < kSampleNmax ? V : kSampleNmax;
   uint64_t key = tid < need ? cand_g[(size_t)r * kSampleNmax + tid] : 0ull;
   __shared__ uint64_t xch[2][kSampleNmax];
   int xb = 0;
+#pragma unroll
   for (int size = 2; size <= kSampleNmax; size <<= 1) {
+#pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       uint64_t other;
       if (stride < 64) {
-        const uint32_t lo = __shfl_xor((uint32_t)key, stride, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), stride, 64);
+        const uint32_t lo = partner((uint32_t)key, stride);
+        const uint32_t hi = partner((uint32_t)(key >> 32), stride);
         other = ((uint64_t)hi << 32) | lo;
       } else {
         xch[xb][tid] = key;
@@ -752,8 +770,8 @@ __global__ __launch_bounds__(kSelThreads) void k_head_select(
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const float os = __shfl_xor(sc, o, 64);
-    const int ok = __shfl_xor(kk, o, 64);
+    const float os = __uint_as_float(partner(__float_as_uint(sc), o));
+    const int ok = (int)partner((uint32_t)kk, o);
     if (os > sc || (os == sc && ok < kk)) {
       sc = os;
       kk = ok;
