@@ -157,6 +157,7 @@ struct HeadArgs {
   const SamplingParams* params;
   uint16_t* y;             // [R, V] bf16 logits (workspace)
   float* part;             // [grid, 4, RP] partials (workspace)
+  uint32_t* tot1;          // [R, 256] the selection's row histogram, cleared here
   int R, V, H, block, nstrips;
   float cap;
   int64_t vbase;
@@ -195,6 +196,8 @@ __global__ __launch_bounds__(64 * kHeadWaves) void k_head_logits(HeadArgs a) {
   const int xstride = H + 16;  // padded LDS row stride (bank spread)
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   int8_t* s_x = smem;                                                   // [RP][H+16]
+  if (blockIdx.x == 0)  // the selection's first pass adds into it after this launch
+    for (int i = threadIdx.x; i < a.R * 256; i += blockDim.x) a.tot1[i] = 0u;
   float* s_sa = reinterpret_cast<float*>(smem + (size_t)RP * xstride);  // [nb][RP] sa/127
   __shared__ float s_invt[RP];
   __shared__ uint64_t s_seed[RP];
@@ -409,7 +412,8 @@ __device__ inline uint16_t key_bf16(uint32_t k) {
 
 struct SelArgs {
   const uint16_t* y;   // [R, V]
-  uint32_t* hist1;     // [R, nc, 256]
+  uint32_t* tot1;      // [R, 256] high-byte histogram of the row (all chunks)
+  uint32_t* tot2;      // [R, 256] low-byte histogram of the row's keys in bin hb
   uint32_t* hist2;     // [R, nc, 256]
   int* thr;            // [R, 4]: hb, keys above hb, threshold key, ties needed
   int* eqpre;          // [R, nc] ties in earlier chunks
@@ -452,7 +456,10 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_hist_hi(SelArgs a) {
 #pragma unroll
   for (int q = 0; q < 16; ++q) hist_add(hist, ok ? k[q] >> 8 : 0u, ok);
   __syncthreads();
-  a.hist1[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];
+  // the row's histogram: one atomic per non-empty bin; chunk 0 also clears
+  // the low-byte one the next pass adds into
+  if (hist[tid]) atomicAdd(&a.tot1[r * 256 + tid], hist[tid]);
+  if (c == 0) a.tot2[r * 256 + tid] = 0u;
 }
 
 // Block-wide inclusive suffix sum over 256 bins (bin 255 first), 256 threads.
@@ -485,15 +492,13 @@ __device__ inline void pick_bin(int suffix, int total, int need, int base, int* 
 }
 
 // Row r's high byte hb of the 256th largest key and the count of keys in
-// higher bins, from every chunk's high-byte histogram (all kChunkThreads
+// higher bins, from the row's high-byte histogram (all kChunkThreads
 // threads call it; every thread gets the results).
 __device__ inline void row_thr_hi(const SelArgs& a, int r, int& hb, int& above_hb) {
   const int tid = threadIdx.x;
   __shared__ int tmp[4];
   __shared__ int s_bin, s_above;
-  int total = 0;
-#pragma unroll 8
-  for (int c = 0; c < a.nc; ++c) total += (int)a.hist1[((size_t)r * a.nc + c) * 256 + tid];
+  const int total = (int)a.tot1[r * 256 + tid];
   const int need = a.V < kSampleNmax ? a.V : kSampleNmax;
   if (tid == 0) { s_bin = 0; s_above = 0; }
   __syncthreads();
@@ -535,21 +540,21 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_hist_lo(SelArgs a) {
 #pragma unroll
   for (int q = 0; q < 16; ++q) hist_add(hist, ok ? k[q] & 255u : 0u, ok && (k[q] >> 8) == hb);
   __syncthreads();
-  a.hist2[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];
+  a.hist2[((size_t)r * a.nc + c) * 256 + tid] = hist[tid];  // for the ties before each chunk
+  if (hist[tid]) atomicAdd(&a.tot2[r * 256 + tid], hist[tid]);
 }
 
 // Row r's threshold key t (its 256th largest), the ties (keys == t) the
 // selection needs, and the ties in the chunks before chunk `want` (every
-// chunk's with want < 0, written to eqpre), from every chunk's low-byte
-// histogram of the keys in bin hb.  All kChunkThreads threads call it.
+// chunk's with want < 0, written to eqpre), from the row's low-byte
+// histogram of the keys in bin hb and, for the ties, every chunk's count of
+// the threshold key.  All kChunkThreads threads call it.
 __device__ inline void row_thr_lo(const SelArgs& a, int r, int want, uint32_t& t_out,
                                   int& ties_out, int& eqb_out) {
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   __shared__ int tmp[4];
   __shared__ int s_bin, s_above, s_eqb;
-  int total = 0;
-#pragma unroll 8
-  for (int c = 0; c < a.nc; ++c) total += (int)a.hist2[((size_t)r * a.nc + c) * 256 + tid];
+  const int total = (int)a.tot2[r * 256 + tid];
   const int need = a.V < kSampleNmax ? a.V : kSampleNmax;
   const int hb = a.thr[r * 4 + 0], above_hb = a.thr[r * 4 + 1];
   if (tid == 0) { s_bin = 0; s_above = above_hb; }
@@ -879,7 +884,7 @@ int head_grid(int vocab) {
 }
 
 struct HeadWs {
-  size_t y, part, hist1, hist2, thr, eqpre, cnt, cand, total;
+  size_t y, part, tot, hist2, thr, eqpre, cnt, cand, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -891,7 +896,7 @@ static HeadWs head_ws_layout(int rows, int vocab) {
   size_t o = 0;
   w.y = o; o = align256(o + (size_t)rows * vocab * 2);
   w.part = o; o = align256(o + (size_t)head_grid(vocab) * 4 * RP * sizeof(float));
-  w.hist1 = o; o = align256(o + (size_t)rows * nc * 256 * 4);
+  w.tot = o; o = align256(o + (size_t)rows * 2 * 256 * 4);
   w.hist2 = o; o = align256(o + (size_t)rows * nc * 256 * 4);
   w.thr = o; o = align256(o + (size_t)rows * 4 * 4);
   w.eqpre = o; o = align256(o + (size_t)rows * nc * 4);
@@ -913,6 +918,7 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
   a.x = x; a.xsa = xsa; a.w = w; a.ws = ws; a.params = params;
   a.y = reinterpret_cast<uint16_t*>(base + L.y);
   a.part = reinterpret_cast<float*>(base + L.part);
+  a.tot1 = reinterpret_cast<uint32_t*>(base + L.tot);
   a.R = R; a.V = V; a.H = H; a.block = block; a.nstrips = V / 16; a.cap = cap; a.vbase = vbase;
   const int grid = head_grid(V);
   const int RP = R <= 16 ? 16 : 32;
@@ -933,7 +939,8 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
 
   SelArgs s{};
   s.y = a.y;
-  s.hist1 = reinterpret_cast<uint32_t*>(base + L.hist1);
+  s.tot1 = a.tot1;
+  s.tot2 = a.tot1 + (size_t)R * 256;
   s.hist2 = reinterpret_cast<uint32_t*>(base + L.hist2);
   s.thr = reinterpret_cast<int*>(base + L.thr);
   s.eqpre = reinterpret_cast<int*>(base + L.eqpre);
@@ -943,7 +950,7 @@ hipError_t launch_flash_sample(const int8_t* x, const float* xsa, const int8_t* 
   s.nc = (V + kChunk - 1) / kChunk;
   const dim3 cg(s.nc, R), cb(kChunkThreads);
   // each chunk workgroup of hist_lo and collect derives its row's thresholds
-  // from the histograms itself (the two one-workgroup-per-row threshold
+  // from the row's histograms itself (the chunks add theirs into them) (the two one-workgroup-per-row threshold
   // launches go; BQ_SEL_FUSED=0 keeps them)
   s.fused = tune().sel_fused;
   hipLaunchKernelGGL(k_sel_hist_hi, cg, cb, 0, st, s);
