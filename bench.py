@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemv", "prefill", "moe32", "moe2048", "layer16", "head",
-                             "attn", "load", "mfma"])
+                             "attn", "load", "mfma", "stream_sweep"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
@@ -152,6 +152,9 @@ def calib_lib():
         raise RuntimeError(f"{path} is not built (python __graft_entry__.py)")
     L = C.CDLL(path)
     L.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    L.bqc_stream_sweep.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                   C.c_void_p]
+    L.bqc_stream_shape.argtypes = [C.c_int, C.c_void_p]
     L.bqc_mfma_i8.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     L.bqc_mfma_i8_ops.argtypes = [C.c_int, C.c_int, C.c_int]
     L.bqc_mfma_i8_ops.restype = C.c_double
@@ -194,6 +197,7 @@ def bench_gemv(bq, torch, steps, warmup, reps=64):
                                            act_out=(xq, sa)), reps)
     s_fused = time_graph(gf, reps, 0, 0)
     rd = bench_stream(torch, [r.data for r in replicas], N // 16, K // 64, steps, warmup)
+    rd["sweep"] = bench_stream_sweep(torch, [r.data for r in replicas], N // 16)
     return dict(s=smp, alg_bytes=alg_bytes, gbs=alg_bytes / (smp.p50 * 1e-3) / 1e9,
                 gbs_min=alg_bytes / (smp.min * 1e-3) / 1e9, s_nq=s_nq, s_lin=s_lin,
                 s_fused=s_fused, rd=rd, codes=codes, scales=scales, xq=xq, sa=sa)
@@ -235,6 +239,47 @@ def bench_stream(torch, bufs, tiles, K64, steps, warmup):
                 gbs=b16 / (same.p50 * 1e-3) / 1e9, gbs_best=b16 / (same.min * 1e-3) / 1e9,
                 large_gbs=b256 / (large.p50 * 1e-3) / 1e9,
                 incr_gbs=(b256 - b16) / ((large.p50 - same.p50) * 1e-3) / 1e9)
+
+
+def bench_stream_sweep(torch, bufs, tiles, samples=200):
+    """The streaming read of the decode GEMV's bytes (tiles x 64 KiB of
+    tile16x64 fragments per launch, over the GEMV's 64 replicas) in every
+    launch shape of bqc_stream_sweep: workgroups, waves per workgroup, loads
+    in flight per wave.  Each shape's p50 per launch with its bytes, and the
+    same grid reading nothing (its fixed cost), graph-replayed as the GEMV."""
+    import ctypes as C
+    L = calib_lib()
+    sink = torch.empty(tiles * 8 * 16, dtype=torch.int16, device="cuda")
+    ptrs = [b.data_ptr() for b in bufs]
+    n = len(ptrs)
+    nbytes = tiles * 64 * 1024
+    rows = []
+    global SAMPLES
+    keep, SAMPLES = SAMPLES, min(SAMPLES, samples)
+    try:
+        for i in range(L.bqc_stream_shapes()):
+            desc = (C.c_int * 4)()
+            L.bqc_stream_shape(i, desc)
+            w, u, spw, ks = list(desc)
+
+            def launcher(empty):
+                def f(j):
+                    rc = L.bqc_stream_sweep(ptrs[j], tiles, i, empty, sink.data_ptr(),
+                                            _stream(torch))
+                    if rc != 0:
+                        raise RuntimeError(f"bqc_stream_sweep: hipError {rc}")
+                return f
+            full = time_graph(graph_of(launcher(0), n), n, 0, 0)
+            empty = time_graph(graph_of(launcher(1), n), n, 0, 0)
+            rows.append(dict(workgroups=tiles // spw * ks, waves=w, loads_per_wave=u * spw,
+                             tiles_per_workgroup=spw, k_parts=ks,
+                             p50_us=round(full.p50 * 1e3, 3), min_us=round(full.min * 1e3, 3),
+                             GBs=round(nbytes / (full.p50 * 1e-3) / 1e9, 1),
+                             empty_p50_us=round(empty.p50 * 1e3, 3)))
+    finally:
+        SAMPLES = keep
+    best = min(rows, key=lambda r: r["p50_us"])
+    return dict(bytes_per_launch=nbytes, shapes=rows, best=best)
 
 
 def bench_mfma(torch):
@@ -516,12 +561,14 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     gq_, gsa = e(T, 2112, dt=torch.int8), e(T, 2112 // 64, dt=torch.float32)
     moe = MoeLayer(bq, torch, T, Wgu, Wd)
 
+    xqd, xsad = e(T, H, dt=torch.int8), e(T, dt=torch.float32)
+    od = e(T, H)
+
     def dense_mlp():
-        bq.norm_quant(x, gamma, 128, out=(xq, xsa))
-        bq.linear(xq, xsa, dg, out=gt)
-        bq.linear(xq, xsa, du, out=up)
+        bq.norm_quant(x, gamma, 128, out=(xqd, xsad))
+        bq.linear_pair(xqd, xsad, dg, du, outs=(gt, up))   # gate and up: one launch
         bq.block_quant(gt, 64, True, out=(gq_, gsa))   # GELU(gate)*up is elementwise (not a bq op)
-        bq.block_linear(gq_, gsa, dd, 64, out=o)
+        bq.block_linear(gq_, gsa, dd, 64, out=od)
 
     def sliding(_i=0):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
@@ -544,7 +591,7 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     ms_s = time_graph(gs_, 1, steps, 0).p50
     gf_ = graph_of(full, 1)
     ms_f = time_graph(gf_, 1, steps, 0).p50
-    gm_ = graph_of(moe, 1)
+    gm_ = graph_of(lambda _i: moe(), 1)
     ms_m = time_graph(gm_, 1, steps, 0).p50
     stack_ms = 25 * ms_s + 5 * ms_f
     return dict(sliding_layer_ms=ms_s, full_layer_ms=ms_f, moe_ms=ms_m,
@@ -926,6 +973,10 @@ def main():
         res["attn"] = bench_attn(bq, torch, args.steps)
     if wl == "load":
         res["load"] = bench_load(bq, torch)
+    if wl == "stream_sweep":
+        # the launch-shape sweep alone, over 64 replicas of the GEMV's 16 MiB
+        pool = torch.randint(-127, 128, (64, 4096 * 4096), dtype=torch.int8, device="cuda")
+        res["stream_sweep"] = bench_stream_sweep(torch, [pool[i] for i in range(64)], 256)
     if wl in ("all", "gemv", "mfma"):
         res["mfma"] = bench_mfma(torch)
     if args.calib_copy:
@@ -978,7 +1029,8 @@ def main():
             "empty_launch_p50_us": round(rd["empty"].p50 * 1e3, 3),
             "read_256MiB_per_launch": {"p50_us": round(rd["large"].p50 * 1e3, 2),
                                        "p50_GBs": round(rd["large_gbs"], 1),
-                                       "incremental_GBs_16_to_256MiB": round(rd["incr_gbs"], 1)}}
+                                       "incremental_GBs_16_to_256MiB": round(rd["incr_gbs"], 1)},
+            "launch_shape_sweep": rd["sweep"]}
     else:
         line.update(value=None, steps=0, steps_requested=args.steps, warmup=args.warmup,
                     ms_per_step=None, config={"workload": wl})
@@ -1040,6 +1092,8 @@ def main():
             stack = 25 * (l16["sliding_layer_ms"] + sl) + 5 * (l16["full_layer_ms"] + fl)
             line["decoder_layer_b16"]["stack_with_attention_ms"] = round(stack, 4)
             line["decoder_layer_b16"]["stack_with_attention_tokens_per_s"] = round(16 / (stack * 1e-3), 1)
+    if "stream_sweep" in res:
+        line["launch_shape_sweep"] = res["stream_sweep"]
     if "load" in res:
         ld = res["load"]
         line["load_safetensors_gate_up_507MB"] = {"ms": round(ld["ms"], 2),

@@ -132,6 +132,15 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
            uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, int qn, int kvn, int seq_len,
            int hidden, void* stream);
 
+/* The dense FFN's gate_proj and up_proj on one activation
+ * (gemma_4_moe_bq.mojo:756-761: two dispatch_bq_linear calls, linear.mojo:
+ * 119-149), in ONE launch over the concatenated out0|out1 output tiles, as
+ * bq_qkv does for three: out0 and out1 equal those of the two bq_linear
+ * calls bit for bit.  n0, n1 % 16 == 0, hidden % 64 == 0. */
+int bq_linear_pair(const int8_t* x_i8, const float* x_sa, const int8_t* w0, const float* w0_scale,
+                   const int8_t* w1, const float* w1_scale, uint16_t* out0, uint16_t* out1,
+                   int n0, int n1, int seq_len, int hidden, void* stream);
+
 /* Fused decode prep: bq_norm_quant of src followed by bq_linear (resp.
  * bq_qkv) on its output, with the same results: x_i8 / x_sa receive the
  * norm-quant's codes and amax, out the linear's.  No single counterpart in
@@ -151,6 +160,14 @@ int bq_norm_qkv(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float*
                 const int8_t* v_w, const float* v_scale, uint16_t* q_out, uint16_t* k_out,
                 uint16_t* v_out, int qn, int kvn, int seq_len, int hidden, int block,
                 float sqrt_n, float n_eps, void* stream);
+/* bq_norm_quant followed by bq_linear_pair (the dense FFN's prep, gate and
+ * up: gemma_4_moe_bq.mojo:749-761), one launch for the decode token as
+ * bq_norm_linear. */
+int bq_norm_linear_pair(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                        const int8_t* w0, const float* w0_scale, const int8_t* w1,
+                        const float* w1_scale, uint16_t* out0, uint16_t* out1, int n0, int n1,
+                        int seq_len, int hidden, int block, float sqrt_n, float n_eps,
+                        void* stream);
 
 /* ---- MoE ---------------------------------------------------------------- */
 

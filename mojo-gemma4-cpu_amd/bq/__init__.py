@@ -43,6 +43,8 @@ SIGNATURES = {
     "bq_qkv": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "bq_norm_linear": [_vp] * 8 + [_i, _i, _i, _i, _f, _f, _vp],
     "bq_norm_qkv": [_vp] * 13 + [_i, _i, _i, _i, _i, _f, _f, _vp],
+    "bq_linear_pair": [_vp] * 8 + [_i, _i, _i, _i, _vp],
+    "bq_norm_linear_pair": [_vp] * 10 + [_i, _i, _i, _i, _i, _f, _f, _vp],
     "bq_moe_router_logits": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_moe_route_topk": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
@@ -269,6 +271,20 @@ def qkv(x_i8, x_sa, q: ButterquantWeight, k: ButterquantWeight, v: ButterquantWe
     return qo, ko, vo
 
 
+def linear_pair(x_i8, x_sa, w0: ButterquantWeight, w1: ButterquantWeight, outs=None):
+    """linear(x, w0) and linear(x, w1) in one launch (the dense FFN's gate and
+    up projections)."""
+    m, hidden = x_i8.shape
+    if outs is None:
+        outs = tuple(torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x_i8.device)
+                     for w in (w0, w1))
+    o0, o1 = outs
+    _check(_lib.bq_linear_pair(_p(x_i8), _p(x_sa), _p(w0.data), _p(w0.scale), _p(w1.data),
+                               _p(w1.scale), _p(o0), _p(o1), w0.n_rows, w1.n_rows, m, hidden,
+                               _stream()))
+    return o0, o1
+
+
 def norm_linear(x: torch.Tensor, gamma: torch.Tensor, w: ButterquantWeight, block: int = 128,
                 sqrt_n=None, n_eps=None, want_f32: bool = False, out=None, act_out=None):
     """norm_quant(x) then linear on its codes, fused into one launch for one
@@ -309,6 +325,28 @@ def norm_qkv(x: torch.Tensor, gamma: torch.Tensor, q: ButterquantWeight, k: Butt
                             _p(k.data), _p(k.scale), _p(v.data), _p(v.scale), _p(qo), _p(ko),
                             _p(vo), q.n_rows, k.n_rows, m, h, block, sqrt_n, n_eps, _stream()))
     return (qo, ko, vo), (xq, sa)
+
+
+def norm_linear_pair(x: torch.Tensor, gamma: torch.Tensor, w0: ButterquantWeight,
+                     w1: ButterquantWeight, block: int = 128, sqrt_n=None, n_eps=None,
+                     outs=None, act_out=None):
+    """norm_quant(x) then linear_pair on its codes, one launch for one token."""
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    m, h = x.shape
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    xq, sa = act_out if act_out is not None else (
+        torch.empty((m, h), dtype=torch.int8, device=x.device),
+        torch.empty(m, dtype=torch.float32, device=x.device))
+    if outs is None:
+        outs = tuple(torch.empty((m, wt.n_rows), dtype=torch.bfloat16, device=x.device)
+                     for wt in (w0, w1))
+    o0, o1 = outs
+    _check(_lib.bq_norm_linear_pair(_p(x), _p(gamma), _p(xq), _p(sa), _p(w0.data),
+                                    _p(w0.scale), _p(w1.data), _p(w1.scale), _p(o0), _p(o1),
+                                    w0.n_rows, w1.n_rows, m, h, block, sqrt_n, n_eps, _stream()))
+    return (o0, o1), (xq, sa)
 
 
 # --------------------------------------------------------------------------

@@ -13,6 +13,10 @@
 //   int32 tiles, and 16 uint16 written per workgroup, the GEMV's 16 bf16
 //   outputs.  Its per-launch time is the
 //   ceiling of a kernel of this shape that reads these bytes.
+// bqc_stream_sweep: the same 16 MiB read over a sweep of launch shapes
+//   (workgroups, waves per workgroup, loads in flight per wave), each with
+//   its empty launch, so the GEMV's launch shape can be compared with the
+//   best shape that reads the same bytes.
 // bqc_mfma_i8: back-to-back int8 MFMAs from registers (8 or 16 independent
 //   v_mfma_i32_16x16x64_i8 chains, or 4 v_mfma_i32_32x32x32_i8 chains, per
 //   wave), 4 waves per workgroup; one int per thread written at the end.
@@ -53,6 +57,55 @@ __global__ __launch_bounds__(kWaves * 64) void k_stream_read(const int8_t* __res
 #pragma unroll
     for (int q = 0; q < kWaves; ++q) r ^= part[q * 256 + threadIdx.x];
     out[blockIdx.x * 16 + threadIdx.x] = (uint16_t)r;
+  }
+}
+
+// The launch-shape sweep of the same read: workgroup b takes SPW
+// consecutive 16-row tiles and part b % ksplit of their K (K64 / ksplit
+// fragments of each), W waves splitting that part into U fragments each, all
+// of a wave's loads issued at once (non-temporal, as above).  Each (tile,
+// part) writes its 16 uint16 to out[(tile * ksplit + part) * 16 ..].  With
+// `empty` the same grid reads nothing: the fixed cost of that launch shape.
+template <int W, int U, int SPW>
+__global__ __launch_bounds__(W * 64) void k_stream_shape(const int8_t* __restrict__ w, int K64,
+                                                         int ksplit, int empty,
+                                                         uint16_t* __restrict__ out) {
+  __shared__ int part[W * 256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int p = blockIdx.x % ksplit, g = blockIdx.x / ksplit;
+  const int F = K64 / ksplit;
+  v4i acc[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) acc[s] = v4i{0, 0, 0, 0};
+  if (!empty) {
+    v4i b[SPW][U];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      const int8_t* wb = w + ((size_t)(g * SPW + s) * K64 + (size_t)p * F + wave * U) * 1024 +
+                         lane * 16;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        b[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)u * 1024));
+    }
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[s] ^= b[s][u];
+  }
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) {
+    if (s) __syncthreads();
+    part[wave * 256 + 0 * 64 + lane] = acc[s].x;
+    part[wave * 256 + 1 * 64 + lane] = acc[s].y;
+    part[wave * 256 + 2 * 64 + lane] = acc[s].z;
+    part[wave * 256 + 3 * 64 + lane] = acc[s].w;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      int r = 0;
+#pragma unroll
+      for (int q = 0; q < W; ++q) r ^= part[q * 256 + threadIdx.x];
+      out[((size_t)(g * SPW + s) * ksplit + p) * 16 + threadIdx.x] = (uint16_t)r;
+    }
   }
 }
 
@@ -119,6 +172,55 @@ int bqc_stream_read(const int8_t* w, int tiles, int K64, int waves, uint16_t* ou
     hipLaunchKernelGGL((k_stream_read<8, 8>), dim3(tiles), dim3(8 * 64), 0, (hipStream_t)stream,
                        w, K64, out);
   return (int)hipGetLastError();
+}
+
+// The launch shapes of the sweep: {waves, fragments per wave, tiles per
+// workgroup, K parts}; a shape reads tiles x K64 fragments when waves x
+// fragments x K parts = K64 (64 here: the decode GEMV's K = 4096).
+struct StreamShape { int w, u, spw, ksplit; };
+static const StreamShape kShapes[] = {
+    {16, 4, 1, 1}, {8, 8, 1, 1}, {4, 16, 1, 1}, {2, 32, 1, 1},
+    {16, 2, 1, 2}, {8, 4, 1, 2}, {4, 8, 1, 2}, {2, 16, 1, 2},
+    {16, 1, 1, 4}, {8, 2, 1, 4}, {4, 4, 1, 4}, {2, 8, 1, 4}, {1, 16, 1, 4},
+    {8, 1, 1, 8}, {4, 2, 1, 8}, {2, 4, 1, 8}, {1, 8, 1, 8},
+    {16, 4, 2, 1}, {8, 8, 2, 1},
+};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+
+int bqc_stream_shapes(void) { return kNumShapes; }
+
+// shape i's {waves, fragments per wave, tiles per workgroup, K parts}
+int bqc_stream_shape(int i, int* desc) {
+  if (i < 0 || i >= kNumShapes || !desc) return (int)hipErrorInvalidValue;
+  desc[0] = kShapes[i].w; desc[1] = kShapes[i].u; desc[2] = kShapes[i].spw;
+  desc[3] = kShapes[i].ksplit;
+  return 0;
+}
+
+// Sweep shape i over tiles 16-row tiles of K64 = 64 fragments each (w:
+// tiles * 64 KiB, 16-byte aligned; out: tiles * ksplit * 16 uint16; tiles a
+// multiple of the shape's tiles per workgroup); empty != 0 launches the same
+// grid reading nothing.  Returns a hipError_t.
+int bqc_stream_sweep(const int8_t* w, int tiles, int i, int empty, uint16_t* out, void* stream) {
+  if (!w || !out || tiles <= 0 || i < 0 || i >= kNumShapes) return (int)hipErrorInvalidValue;
+  if (reinterpret_cast<uintptr_t>(w) & 15u) return (int)hipErrorInvalidValue;
+  const StreamShape sh = kShapes[i];
+  constexpr int K64 = 64;
+  if (sh.w * sh.u * sh.ksplit != K64 || tiles % sh.spw) return (int)hipErrorInvalidValue;
+  const dim3 g(tiles / sh.spw * sh.ksplit), b(sh.w * 64);
+  hipStream_t st = (hipStream_t)stream;
+#define BQC_SHAPE(W, U, S)                                                                   \
+  if (sh.w == W && sh.u == U && sh.spw == S) {                                              \
+    hipLaunchKernelGGL((k_stream_shape<W, U, S>), g, b, 0, st, w, K64, sh.ksplit, empty, out); \
+    return (int)hipGetLastError();                                                          \
+  }
+  BQC_SHAPE(16, 4, 1) BQC_SHAPE(8, 8, 1) BQC_SHAPE(4, 16, 1) BQC_SHAPE(2, 32, 1)
+  BQC_SHAPE(16, 2, 1) BQC_SHAPE(8, 4, 1) BQC_SHAPE(4, 8, 1) BQC_SHAPE(2, 16, 1)
+  BQC_SHAPE(16, 1, 1) BQC_SHAPE(8, 2, 1) BQC_SHAPE(4, 4, 1) BQC_SHAPE(2, 8, 1)
+  BQC_SHAPE(1, 16, 1) BQC_SHAPE(8, 1, 1) BQC_SHAPE(4, 2, 1) BQC_SHAPE(2, 4, 1)
+  BQC_SHAPE(1, 8, 1) BQC_SHAPE(16, 4, 2) BQC_SHAPE(8, 8, 2)
+#undef BQC_SHAPE
+  return (int)hipErrorInvalidValue;
 }
 
 // shape 16 (v_mfma_i32_16x16x64_i8, 32768 ops each, 8 chains), 17 (the same

@@ -284,6 +284,24 @@ int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float
   return check_hip(bq::launch_linear(a, 0, S(stream)), "qkv");
 }
 
+int bq_linear_pair(const int8_t* x_i8, const float* x_sa, const int8_t* w0, const float* w0_scale,
+                   const int8_t* w1, const float* w1_scale, uint16_t* out0, uint16_t* out1,
+                   int n0, int n1, int seq_len, int hidden, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !w0 || !w0_scale || !w1 || !w1_scale || !out0 || !out1)
+    return fail(BQ_ERR_INVALID, "bq_linear_pair: null pointer");
+  if (n0 <= 0 || n1 <= 0 || n0 % 16 || n1 % 16 || hidden <= 0 || hidden % 64)
+    return fail(BQ_ERR_SHAPE, "bq_linear_pair: need n0, n1 %% 16 == 0 and hidden %% 64 == 0");
+  if (!a16(x_i8) || !a16(w0) || !a16(w1))
+    return fail(BQ_ERR_INVALID, "bq_linear_pair: int8 operands must be 16-byte aligned");
+  bq::LinArgs a{};
+  a.seg[0] = {w0, w0_scale, out0, nullptr, n0, 0};
+  a.seg[1] = {w1, w1_scale, out1, nullptr, n1, n0 / 16};
+  a.nseg = 2;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_linear(a, 0, S(stream)), "linear_pair");
+}
+
 // shared checks of the fused norm-quant + linear entries (those of
 // bq_norm_quant and of the linear on its output)
 static int norm_linear_args(const char* who, const uint16_t* src, const uint16_t* gamma,
@@ -342,6 +360,30 @@ int bq_norm_qkv(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float*
   a.nseg = 3;
   a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
   return check_hip(bq::launch_norm_linear(a, nq, S(stream)), "norm_qkv");
+}
+
+int bq_norm_linear_pair(const uint16_t* src, const uint16_t* gamma, int8_t* x_i8, float* x_sa,
+                        const int8_t* w0, const float* w0_scale, const int8_t* w1,
+                        const float* w1_scale, uint16_t* out0, uint16_t* out1, int n0, int n1,
+                        int seq_len, int hidden, int block, float sqrt_n, float n_eps,
+                        void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  bq::NormArgs nq{};
+  const int r = norm_linear_args("bq_norm_linear_pair", src, gamma, x_i8, x_sa, hidden, block,
+                                 sqrt_n, n_eps, nq);
+  if (r != BQ_OK) return r;
+  if (!w0 || !w0_scale || !w1 || !w1_scale || !out0 || !out1)
+    return fail(BQ_ERR_INVALID, "bq_norm_linear_pair: null pointer");
+  if (n0 <= 0 || n1 <= 0 || n0 % 16 || n1 % 16)
+    return fail(BQ_ERR_SHAPE, "bq_norm_linear_pair: need n0, n1 %% 16 == 0");
+  if (!a16(w0) || !a16(w1))
+    return fail(BQ_ERR_INVALID, "bq_norm_linear_pair: int8 operands must be 16-byte aligned");
+  bq::LinArgs a{};
+  a.seg[0] = {w0, w0_scale, out0, nullptr, n0, 0};
+  a.seg[1] = {w1, w1_scale, out1, nullptr, n1, n0 / 16};
+  a.nseg = 2;
+  a.act = x_i8; a.sa = x_sa; a.M = seq_len; a.K = hidden; a.block = hidden;
+  return check_hip(bq::launch_norm_linear(a, nq, S(stream)), "norm_linear_pair");
 }
 
 int bq_moe_router_logits(const uint16_t* x, const uint16_t* router_proj,

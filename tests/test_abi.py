@@ -112,6 +112,13 @@ def test_validation_errors(L):
     assert nl(P, P, C.c_void_p(264), P, P, P, P, None, 256, 1, 2816, 128) == 1  # alignment
     assert L.bq_norm_qkv(*([P] * 13), 4096, 2050, 1, 2816, 128, f1, f1, None) == 2
     assert L.bq_norm_qkv(*([P] * 12), None, 4096, 2048, 1, 2816, 128, f1, f1, None) == 1
+    assert L.bq_linear_pair(*([P] * 8), 2112, 2100, 16, 2816, None) == 2   # n1 % 16
+    assert L.bq_linear_pair(*([P] * 8), 2112, 2112, 16, 2880 + 8, None) == 2  # hidden % 64
+    assert L.bq_linear_pair(*([P] * 7), None, 2112, 2112, 16, 2816, None) == 1
+    assert L.bq_linear_pair(C.c_void_p(264), *([P] * 7), 2112, 2112, 16, 2816, None) == 1
+    assert L.bq_norm_linear_pair(*([P] * 10), 2112, 2112, 1, 2816, 48, f1, f1, None) == 2
+    assert L.bq_norm_linear_pair(*([P] * 9), None, 2112, 2112, 1, 2816, 128, f1, f1,
+                                 None) == 1
 
 
 
@@ -163,6 +170,9 @@ def test_empty_batches_are_noops(L):
                             None) == 0
     assert L.bq_norm_qkv(*([None] * 13), 256, 128, 0, 2816, 128, C.c_float(1), C.c_float(1),
                          None) == 0
+    assert L.bq_linear_pair(*([None] * 8), 2112, 2112, 0, 2816, None) == 0
+    assert L.bq_norm_linear_pair(*([None] * 10), 2112, 2112, 0, 2816, 128, C.c_float(1),
+                                 C.c_float(1), None) == 0
     assert L.bq_moe_build_schedule(None, None, 0, 8, 0, 128, None, None, None) == 0
     assert L.bq_moe_phase1_gate_up(*([None] * 7), 128, 0, 8, 2816, 704, None) == 0
     assert L.bq_head_prep(None, None, None, None, 0, 2816, 128, C.c_float(1), C.c_float(1),
@@ -188,14 +198,30 @@ def test_calib_library_exports():
     kernels) loads and rejects out-of-contract launches before any GPU call."""
     path = os.path.join(ROOT, "mojo-gemma4-cpu_amd", "libbq_calib.so")
     lib = C.CDLL(path)
-    for n in ("bqc_stream_read", "bqc_mfma_i8", "bqc_mfma_i8_ops"):
+    for n in ("bqc_stream_read", "bqc_stream_sweep", "bqc_stream_shapes", "bqc_stream_shape",
+              "bqc_mfma_i8", "bqc_mfma_i8_ops"):
         assert hasattr(lib, n)
-    lib.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                    C.c_void_p]
+    lib.bqc_stream_sweep.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                     C.c_void_p]
+    lib.bqc_stream_shape.argtypes = [C.c_int, C.c_void_p]
+    n_shapes = lib.bqc_stream_shapes()
+    assert n_shapes >= 10
+    desc = (C.c_int * 4)()
+    for i in range(n_shapes):   # every shape reads the 64 fragments of a 4096-wide tile
+        assert lib.bqc_stream_shape(i, desc) == 0
+        w, u, spw, ks = list(desc)
+        assert w * u * ks == 64 and spw >= 1
+    assert lib.bqc_stream_shape(n_shapes, desc) != 0
+    assert lib.bqc_stream_sweep(P, 256, n_shapes, 0, P, None) != 0   # no such shape
+    assert lib.bqc_stream_sweep(C.c_void_p(17), 256, 0, 0, P, None) != 0  # misaligned
     lib.bqc_mfma_i8.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     lib.bqc_mfma_i8_ops.argtypes = [C.c_int, C.c_int, C.c_int]
     lib.bqc_mfma_i8_ops.restype = C.c_double
-    assert lib.bqc_stream_read(P, 256, 65, P, None) != 0      # K64 beyond the one-shot shape
-    assert lib.bqc_stream_read(C.c_void_p(17), 256, 64, P, None) != 0  # misaligned
+    assert lib.bqc_stream_read(P, 256, 65, 16, P, None) != 0      # K64 beyond the one-shot shape
+    assert lib.bqc_stream_read(C.c_void_p(17), 256, 64, 16, P, None) != 0  # misaligned
+    assert lib.bqc_stream_read(P, 256, 64, 12, P, None) != 0      # waves
     assert lib.bqc_mfma_i8(24, 4, 8, P, None) != 0           # no such MFMA tile
     assert lib.bqc_mfma_i8(17, 4, 7, P, None) != 0           # odd iterations on 16 chains
     assert lib.bqc_mfma_i8_ops(32, 1024, 2048) == 262144.0 * 2048 * 1024 * 4

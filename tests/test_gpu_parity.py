@@ -255,6 +255,38 @@ def test_qkv_matches_three_linears(gpu, O, M):
         np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
 
 
+@pytest.mark.parametrize("M,K", [(1, 2816), (16, 2816), (17, 512), (300, 1024)])
+def test_linear_pair(gpu, O, M, K):
+    """gate and up in one launch = the two linears (and the oracle), bit-exact."""
+    (q0, s0, W0), (q1, s1, W1) = (weight(gpu, O, n, K, 128, seed=sd)
+                                  for n, sd in ((288, 1), (160, 2)))
+    x = O.synth_normal_bf16(6, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    o0, o1 = gpu.linear_pair(dev(xq), dev(sa), W0, W1)
+    for o, q, s, W in ((o0, q0, s0, W0), (o1, q1, s1, W1)):
+        np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
+        p, cs = O.pack_and_colsum(q)
+        rb, _ = O.linear(xq, sa, p, s, cs, W.n_rows)
+        np.testing.assert_array_equal(host(o), rb)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2816), (1, 4096), (3, 2816)])
+def test_norm_linear_pair(gpu, O, M, K):
+    """norm-quant + gate and up in one call = norm_quant then the two linears."""
+    (q0, s0, W0), (q1, s1, W1) = (weight(gpu, O, n, K, 128, seed=sd)
+                                  for n, sd in ((2112, 1), (2112, 2)))
+    x = O.synth_normal_bf16(7, 1.0, (M, K))
+    gamma = O.f32_to_bf16(O.synth_normal_f32(9, 0.3, (K,)) + 1.0)
+    (o0, o1), (xq, sa) = gpu.norm_linear_pair(dev(x), dev(gamma), W0, W1, 128)
+    rxq, rsa = O.norm_quant(x, gamma, 128)
+    np.testing.assert_array_equal(host(xq), rxq)
+    np.testing.assert_array_equal(host(sa), rsa)
+    for o, q, s, W in ((o0, q0, s0, W0), (o1, q1, s1, W1)):
+        p, cs = O.pack_and_colsum(q)
+        rb, _ = O.linear(rxq, rsa, p, s, cs, W.n_rows)
+        np.testing.assert_array_equal(host(o), rb)
+
+
 @pytest.mark.parametrize("M,K,N,B", [(1, 2816, 256, 128), (1, 4096, 512, 128), (1, 2816, 128, 256),
                                      (1, 4096, 256, 512), (1, 512, 256, 64), (1, 1024, 128, 512),
                                      (1, 2304, 256, 256), (1, 768, 128, 16), (3, 2816, 256, 128),
