@@ -318,7 +318,7 @@ def bench_mfma(torch):
 def bench_prefill(bq, torch, steps, warmup, reps=32):
     M, N, K = 512, 4096, 4096
     gen = torch.Generator(device="cuda").manual_seed(0)
-    _, scales, W0 = quantized(bq, torch, N, K, 128, gen)
+    codes, scales, W0 = quantized(bq, torch, N, K, 128, gen)
     replicas = [W0] + [bq.ButterquantWeight(W0.data.clone(), scales, N, K) for _ in range(reps - 1)]
     xg = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn(M, K, generator=xg, device="cuda").to(torch.bfloat16)
@@ -331,7 +331,8 @@ def bench_prefill(bq, torch, steps, warmup, reps=32):
     return dict(s=smp, ops=ops, tops=tops, int8_frac=tops / INT8_PEAK_TOPS,
                 bf16_frac=tops / BF16_PEAK_TFLOPS,
                 alg_bytes=N * K + N * 4 + M * K + M * 4 + M * N * 2,
-                vendor=vendor_gemm(torch, M, N, K, reps))
+                vendor=vendor_gemm(torch, M, N, K, reps),
+                cpu_inputs=(codes, scales, xq, sa))
 
 
 def vendor_gemm(torch, M, N, K, reps):
@@ -540,10 +541,16 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     T = 16
     gen = torch.Generator(device="cuda").manual_seed(0)
     d = "cuda"
-    mk = lambda n, k, b: quantized(bq, torch, n, k, b, gen)[2]
-    sq, sk, sv, so = mk(4096, H, 128), mk(2048, H, 128), mk(2048, H, 128), mk(H, 4096, 256)
-    fq, fk, fo = mk(8192, H, 128), mk(1024, H, 128), mk(H, 8192, 512)
-    dg, du, dd = mk(2112, H, 128), mk(2112, H, 128), mk(H, 2112, 64)
+    host = {}
+
+    def mk(n, k, b, name):
+        codes, scales, w = quantized(bq, torch, n, k, b, gen)
+        host[name] = (codes.cpu().numpy(), scales.cpu().numpy(), b)
+        return w
+    sq, sk, sv, so = (mk(4096, H, 128, "sq"), mk(2048, H, 128, "sk"), mk(2048, H, 128, "sv"),
+                      mk(H, 4096, 256, "so"))
+    fq, fk, fo = mk(8192, H, 128, "fq"), mk(1024, H, 128, "fk"), mk(H, 8192, 512, "fo")
+    dg, du, dd = mk(2112, H, 128, "dg"), mk(2112, H, 128, "du"), mk(H, 2112, 64, "dd")
     xg = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn(T, H, generator=xg, device=d).to(torch.bfloat16)
     gamma = torch.ones(H, dtype=torch.bfloat16, device=d)
@@ -594,8 +601,10 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     gm_ = graph_of(lambda _i: moe(), 1)
     ms_m = time_graph(gm_, 1, steps, 0).p50
     stack_ms = 25 * ms_s + 5 * ms_f
+    bf = lambda t: t.view(torch.int16).cpu().numpy().view("uint16")
+    host.update(x=bf(x), attn_s=bf(attn_s), attn_f=bf(attn_f), moe=moe)
     return dict(sliding_layer_ms=ms_s, full_layer_ms=ms_f, moe_ms=ms_m,
-                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3))
+                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3), cpu_inputs=host)
 
 
 def bench_attn(bq, torch, steps):
@@ -768,13 +777,37 @@ def _cpu_samples(call, seconds, warm=30, cap=600):
     return float(np.median(ts)), float(min(ts)), len(ts)
 
 
+def l3_bytes(cpus):
+    """Total L3 of the distinct L3 instances serving `cpus` (sysfs cache
+    index3: size and shared_cpu_list), or None if sysfs does not say."""
+    seen, total = set(), 0
+    for c in cpus:
+        d = f"/sys/devices/system/cpu/cpu{c}/cache/index3/"
+        try:
+            with open(d + "shared_cpu_list") as f:
+                key = f.read().strip()
+            with open(d + "size") as f:
+                txt = f.read().strip()
+        except OSError:
+            return None
+        if key in seen:
+            continue
+        seen.add(key)
+        mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(txt[-1:].upper(), 1)
+        total += int(txt.rstrip("KMGkmg")) * mult
+    return total or None
+
+
 def cpu_baseline_gemv(codes, scales, xq, sa, seconds, topo):
     """The reference CPU path (VNNI u8 x i8 with colsums, 32-row tiles over
     worker_range, matmul_workers threads), ported to C in
     oracle/cpu_baseline.c, on the host cores: the same decode GEMV (M=1,
     K=N=4096) on the GPU run's own weight codes and quantized activation.
-    First with threads pinned one per physical core of one NUMA node (the
-    value), then on all allowed CPUs."""
+    Like the GPU leg, consecutive calls rotate over weight replicas, here
+    enough that the bytes touched between two uses of a replica are at least
+    twice the L3 that serves the pinned CPUs (read from sysfs), so each call
+    streams its weights from DRAM.  First with threads pinned one per
+    physical core of one NUMA node (the value), then on all allowed CPUs."""
     import ctypes as C
 
     import numpy as np
@@ -795,23 +828,179 @@ def cpu_baseline_gemv(codes, scales, xq, sa, seconds, topo):
     for leg, pins in (("node", topo["node_pin"]), ("all", topo["all_pin"])):
         O.cpu_pin(pins)
         n = len(pins)
-        med, mn, cnt = _cpu_samples(
-            lambda: lib.bqcpu_linear(ptr(xq), ptr(sa), 1, ptr(p), ptr(s), ptr(cs), N, K, ptr(out), n),
-            seconds / 2)
+        l3 = l3_bytes(pins)
+        reps = min(128, max(2, 1 + -(-2 * (l3 or (256 << 20)) // p.nbytes)))
+        pool = np.empty((reps, p.size), np.int8)
+        pool[:] = p
+        wp = [ptr(pool[i]) for i in range(reps)]
+        it = [0]
+
+        def call():
+            i = it[0] = (it[0] + 1) % reps
+            lib.bqcpu_linear(ptr(xq), ptr(sa), 1, wp[i], ptr(s), ptr(cs), N, K, ptr(out), n)
+        med, mn, cnt = _cpu_samples(call, seconds / 2)
+        cached = _cpu_samples(
+            lambda: lib.bqcpu_linear(ptr(xq), ptr(sa), 1, wp[0], ptr(s), ptr(cs), N, K, ptr(out),
+                                     n), seconds / 4)
+        del pool
         legs[leg] = dict(value=round(alg_bytes / med / 1e9, 2), p50_us=round(med * 1e6, 1),
                          min_us=round(mn * 1e6, 1), best_GBs=round(alg_bytes / mn / 1e9, 2),
-                         samples=cnt, threads=n, cpus=pins)
+                         samples=cnt, threads=n, cpus=pins, weight_replicas=reps,
+                         l3_bytes_of_pinned_cpus=l3,
+                         one_replica_GBs=round(alg_bytes / cached[0] / 1e9, 2))
     nd = legs["node"]
     return dict(value=nd["value"], unit="GB/s", cores=nd["threads"], kind="port",
-                sample=f"decode GEMV M=1 K=N=4096 on the GPU run's codes and activation; "
-                       f"p50 of {nd['samples']} calls after 30 warmups, {nd['threads']} threads "
-                       f"pinned one per physical core on NUMA node {topo['node']}; "
-                       f"ISA {lib.bqcpu_isa().decode()}; gcc -O3 -fopenmp, OMP_WAIT_POLICY="
-                       f"{os.environ.get('OMP_WAIT_POLICY')}",
+                sample=f"decode GEMV M=1 K=N=4096 on the GPU run's codes and activation, "
+                       f"rotated over {nd['weight_replicas']} weight replicas (>= 2x the "
+                       f"{nd['l3_bytes_of_pinned_cpus']} B of L3 serving the pinned CPUs) so "
+                       f"the weights stream from DRAM; p50 of {nd['samples']} calls after 30 "
+                       f"warmups, {nd['threads']} threads pinned one per physical core on NUMA "
+                       f"node {topo['node']}; ISA {lib.bqcpu_isa().decode()}; gcc -O3 -fopenmp, "
+                       f"OMP_WAIT_POLICY={os.environ.get('OMP_WAIT_POLICY')}",
                 p50_us=nd["p50_us"], min_us=nd["min_us"], all_cpus=legs["all"],
                 topology={k: topo[k] for k in ("cpu_model", "physical_cores", "numa_nodes",
                                                "logical_cpus_online", "allowed_logical_cpus",
                                                "allowed_physical_cores")})
+
+
+def cpu_baseline_prefill(codes, scales, xq, sa, seconds, topo):
+    """The reference CPU path of the prefill linear (M=512, K=N=4096;
+    dispatch_bq_linear's VNNI branch, the one an EPYC host takes: no AMX)
+    on the GPU run's own weight codes and quantized activation, both legs as
+    the GEMV's.  int8 TOP/s = 2*M*N*K / p50."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    lib = O.cpu()
+    q = codes.cpu().numpy()
+    s_ = scales.cpu().numpy().astype(np.float32)
+    N, K = q.shape
+    p, cs = O.pack_and_colsum(q)
+    xq = np.ascontiguousarray(xq.cpu().numpy())
+    sa = np.ascontiguousarray(sa.cpu().numpy().astype(np.float32))
+    M = xq.shape[0]
+    out = np.empty((M, N), np.uint16)
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+    ops = 2.0 * M * N * K
+    legs = {}
+    for leg, pins in (("node", topo["node_pin"]), ("all", topo["all_pin"])):
+        O.cpu_pin(pins)
+        med, mn, cnt = _cpu_samples(
+            lambda: lib.bqcpu_linear(ptr(xq), ptr(sa), M, ptr(p), ptr(s_), ptr(cs), N, K,
+                                     ptr(out), len(pins)), seconds / 2)
+        legs[leg] = dict(tops=round(ops / med / 1e12, 3), p50_ms=round(med * 1e3, 3),
+                         min_ms=round(mn * 1e3, 3), samples=cnt, threads=len(pins))
+    nd = legs["node"]
+    return dict(value=nd["tops"], unit="TOP/s", cores=nd["threads"], kind="port",
+                sample=f"prefill linear M=512 K=N=4096 on the GPU run's codes and activation; "
+                       f"p50 of {nd['samples']} calls, {nd['threads']} threads pinned one per "
+                       f"physical core on NUMA node {topo['node']}; ISA "
+                       f"{lib.bqcpu_isa().decode()}", p50_ms=nd["p50_ms"], all_cpus=legs["all"])
+
+
+def cpu_baseline_layer16(bq, torch, host, Wgu, Wd, seconds, topo):
+    """The reference CPU path of the batch-16 decoder layer's quantized
+    projections, in the reference's calls (gemma_4_moe_bq.mojo:418-627,
+    716-805): norm-quant, q|k|v as one linear over the concatenated tiles
+    (dispatch_bq_qkv), block-quant + o_proj, norm-quant, gate|up, FWHT64
+    block-quant + down, and the 128-expert MoE layer (bqcpu_moe_layer) -- on
+    the GPU run's own weights and inputs; sliding and full layers, both legs
+    as the GEMV's; stack = 25 sliding + 5 full layers."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    lib = O.cpu()
+    T = 16
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+
+    def packed(*names):
+        """VNNI-packed weights of one or more row-concatenated projections."""
+        qs = [host[n][0] for n in names]
+        q = np.concatenate(qs) if len(qs) > 1 else qs[0]
+        b = host[names[0]][2]
+        blk = q.shape[1] if b == 128 else b   # per-row weights carry one colsum block
+        p, cs = O.pack_and_colsum(q, None if b == 128 else blk, b == 128)
+        sc = np.concatenate([host[n][1] for n in names]).astype(np.float32)
+        return p, sc, cs, q.shape[0], q.shape[1], b
+    W = {k: packed(*v) for k, v in (("sqkv", ("sq", "sk", "sv")), ("so", ("so",)),
+                                    ("fqk", ("fq", "fk")), ("fo", ("fo",)),
+                                    ("dgu", ("dg", "du")), ("dd", ("dd",)))}
+    gamma = np.full(H, 0x3F80, np.uint16)
+    sqrt_n, n_eps = O.norm_consts(H)
+    x, attn = host["x"], {"s": host["attn_s"], "f": host["attn_f"]}
+    xq, xsa = np.empty((T, H), np.int8), np.empty(T, np.float32)
+    bufs = {}
+
+    def lin(key, act, sa, nt):
+        p, sc, cs, n, k, b = W[key]
+        out = bufs.setdefault(key, np.empty((T, n), np.uint16))
+        if b == 128:
+            lib.bqcpu_linear(ptr(act), ptr(sa), T, ptr(p), ptr(sc), ptr(cs), n, k, ptr(out), nt)
+        else:
+            lib.bqcpu_block_linear(ptr(act), ptr(sa), T, ptr(p), ptr(sc), ptr(cs), n, k, b,
+                                   ptr(out), nt)
+        return out
+
+    def bquant(src, block, fwht, nt):
+        rows, cols = src.shape
+        q_ = bufs.setdefault(("q", cols, block), np.empty((rows, cols), np.int8))
+        s_ = bufs.setdefault(("s", cols, block), np.empty((rows, cols // block), np.float32))
+        lib.bqcpu_block_quant(ptr(src), ptr(q_), ptr(s_), rows, cols, block, int(fwht), nt)
+        return q_, s_
+
+    def nquant(nt):
+        lib.bqcpu_norm_quant(ptr(x), ptr(gamma), ptr(xq), ptr(xsa), T, H, 128,
+                             C.c_float(sqrt_n), C.c_float(n_eps), nt)
+
+    moe = host["moe"]
+    gu = bq.unpack(Wgu.data, Wgu.n_rows, Wgu.k).cpu().numpy().reshape(Wgu.n_rows, Wgu.k)
+    dn = bq.unpack(Wd.data, Wd.n_rows, Wd.k).cpu().numpy().reshape(Wd.n_rows, Wd.k)
+    gp, gcs = O.pack_and_colsum(gu)
+    dp, dcs = O.pack_and_colsum(dn, 64, False)
+    del gu, dn
+    cl = O.CpuMoeLayer(T, E, TOPK, H, I, gp, Wgu.scale.cpu().numpy(), gcs, dp,
+                       Wd.scale.cpu().numpy(), dcs)
+    mx = moe.x.view(torch.int16).cpu().numpy().view(np.uint16)
+    lg = moe.logits.cpu().numpy()
+    pes = np.full(E, 0x3F80, np.uint16)
+
+    def layer(kind, nt):
+        nquant(nt)
+        lin("sqkv" if kind == "s" else "fqk", xq, xsa, nt)
+        oq, osa = bquant(attn[kind], 256 if kind == "s" else 512, False, nt)
+        lin("so" if kind == "s" else "fo", oq, osa, nt)
+        nquant(nt)                                  # the FFN's own norm-quant
+        gu_out = lin("dgu", xq, xsa, nt)
+        gq, gsa = bquant(np.ascontiguousarray(gu_out[:, :2112]), 64, True, nt)
+        lin("dd", gq, gsa, nt)
+        cl(lg, mx, gamma, pes, nt)
+    legs = {}
+    for leg, pins in (("node", topo["node_pin"]), ("all", topo["all_pin"])):
+        O.cpu_pin(pins)
+        r = {}
+        for kind in ("s", "f"):
+            med, mn, cnt = _cpu_samples(lambda: layer(kind, len(pins)), seconds / 4)
+            r[kind] = (med, mn, cnt)
+        stack = 25 * r["s"][0] + 5 * r["f"][0]
+        legs[leg] = dict(sliding_p50_ms=round(r["s"][0] * 1e3, 3),
+                         full_p50_ms=round(r["f"][0] * 1e3, 3), stack_ms=round(stack * 1e3, 2),
+                         stack_tokens_per_s=round(T / stack, 1), samples=r["s"][2],
+                         threads=len(pins))
+    nd = legs["node"]
+    return dict(value=nd["stack_tokens_per_s"], unit="tokens/s", cores=nd["threads"],
+                kind="port",
+                sample=f"all quantized projections + MoE of one decoder layer at decode batch 16 "
+                       f"(sliding and full), the GPU run's weights and inputs; p50 of "
+                       f"{nd['samples']} layers, {nd['threads']} threads pinned one per physical "
+                       f"core on NUMA node {topo['node']}; stack = 25 sliding + 5 full",
+                **{k: v for k, v in nd.items() if k not in ("samples", "threads")},
+                all_cpus=legs["all"])
 
 
 def cpu_baseline_moe(bq, torch, Wgu, Wd, layers, seconds, topo):
@@ -1080,7 +1269,8 @@ def main():
                     "basis": "touched experts' weight and scale bytes / p50 layer time"}
             line[f"moe_layer_T{T}"] = d
     if "layer16" in res:
-        line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()}
+        line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()
+                                     if k != "cpu_inputs"}
         if "attn" in res:
             # the same stack with each layer's attention step (prep + int8-KV
             # attention at decode batch 16: sliding layers at a full 1024
@@ -1109,15 +1299,21 @@ def main():
         line["head_flash_sample_v262144"]["alg_bytes"] = hd["alg_bytes"]
     if "attn" in res:
         line["attention_int8_kv"] = res["attn"]
-    if not args.no_cpu and ("gemv" in res or MOE_LAYERS):
+    if not args.no_cpu and ("gemv" in res or "prefill" in res or MOE_LAYERS):
         topo = cpu_topology()
         if "gemv" in res:
             gv = res["gemv"]
             line["cpu_baseline"] = cpu_baseline_gemv(gv["codes"], gv["scales"], gv["xq"], gv["sa"],
                                                      args.cpu_seconds, topo)
+        if "prefill" in res:
+            line["cpu_baseline_prefill"] = cpu_baseline_prefill(*res["prefill"]["cpu_inputs"],
+                                                                args.cpu_seconds, topo)
         if MOE_LAYERS:
             line["cpu_baseline_moe"] = cpu_baseline_moe(bq, torch, *moe_w, MOE_LAYERS,
                                                         args.cpu_seconds, topo)
+        if "layer16" in res:
+            line["cpu_baseline_layer16"] = cpu_baseline_layer16(
+                bq, torch, res["layer16"]["cpu_inputs"], *moe_w, args.cpu_seconds, topo)
     print(json.dumps(line))
 
 
