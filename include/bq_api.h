@@ -54,7 +54,11 @@ typedef struct bq_route {
 } bq_route;
 
 /* ---- runtime ------------------------------------------------------------ */
-int bq_init(int device);                 /* select + warm the device */
+/* Select and warm the device; read the BQ_* tuning switches of the
+ * environment.  The switches are published atomically: a launch on another
+ * thread during bq_init runs with the old or the new values (each a valid
+ * configuration with the same results). */
+int bq_init(int device);
 const char* bq_last_error(void);         /* message of the last failure (thread-local) */
 int bq_stream_synchronize(void* stream); /* join, like fanout_dispatch's join_all */
 const char* bq_version(void);
@@ -228,9 +232,12 @@ int bq_moe_route_schedule(const float* logits, const uint16_t* per_expert_scale,
  * norm-quant's shapes (hidden % 256 == 0, hidden <= 4096) it is one launch,
  * in which workgroups quantize the rows while others take the top-k: up to
  * 16 tokens one workgroup takes every top-k and builds the schedule, above
- * that the last top-k workgroup to finish builds it (a device-scope counter
- * of the library's, reset by that workgroup: calls on one device must not
- * overlap in time, as stream order gives).  Above 1024 slots with block 128
+ * that the last top-k workgroup to finish builds it, found through a
+ * device-scope counter of the library's that its increment wraps back to 0.
+ * Each stream of a device gets its own counter on first use (up to 256
+ * streams per device; later streams take the separate launches), so calls
+ * on different streams may overlap; calls on one stream run in order.
+ * Above 1024 slots with block 128
  * the top-k and the norm-quant share one launch and the schedule follows;
  * otherwise the separate launches.  The checks of both calls apply. */
 int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "../../include/bq_api.h"
@@ -47,8 +48,13 @@ int api_failv(int code, const char* fmt, va_list ap) {
 }
 
 namespace {
-Tune g_tune{};
-std::once_flag g_tune_once;
+// The tuning settings in force: each tune_init publishes a new immutable
+// Tune through this pointer (release / acquire), so a launch on another
+// thread reads either the old settings or the new ones, never a torn copy.
+// Replaced settings are never freed (a launch may still be reading them);
+// each is a few dozen bytes, once per bq_init.
+std::atomic<const Tune*> g_tune{nullptr};
+std::mutex g_tune_mu;
 
 // The allocation-free phase 2 (bq_moe_phase2_down_noalloc) keeps its
 // workspace -- the per-route f32 rows of the down projection -- in this
@@ -84,6 +90,7 @@ int env_int(const char* name) {
 hipError_t scratch_address(int device, void** out) { return scratch_ptr(device, out); }
 
 void tune_init(int device) {
+  std::lock_guard<std::mutex> lock(g_tune_mu);
   Tune t{};
   t.gemv_waves = env_int("BQ_GEMV_WAVES");
   t.tile_bm = env_int("BQ_TILE_BM");
@@ -115,18 +122,22 @@ void tune_init(int device) {
       cus <= 0)
     cus = 256;
   t.cus = cus;
-  g_tune = t;
+  g_tune.store(new Tune(t), std::memory_order_release);
 }
 
 const Tune& tune() {
-  std::call_once(g_tune_once, [] {
-    if (g_tune.cus == 0) {
-      int dev = 0;
-      if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-      tune_init(dev);
+  const Tune* t = g_tune.load(std::memory_order_acquire);
+  if (!t) {  // a process that never called bq_init: read the switches once
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    {
+      std::lock_guard<std::mutex> lock(g_tune_mu);
+      t = g_tune.load(std::memory_order_acquire);
     }
-  });
-  return g_tune;
+    if (!t) tune_init(dev);
+    t = g_tune.load(std::memory_order_acquire);
+  }
+  return *t;
 }
 }  // namespace bq
 
@@ -520,21 +531,34 @@ size_t bq_moe_phase2_workspace_size(int seq_len, int top_k, int hidden) {
   return bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
 }
 
+// The checks both phase-2 entry points share (all but the workspace), in one
+// order, so the two return the same status for the same arguments.
+static int phase2_args(const char* who, const int8_t* bucket_i8, const float* bucket_sa,
+                       const int32_t* expert_offset, const bq_route* routes,
+                       const int8_t* w_down, const float* down_scale, float* moe_accum,
+                       uint16_t* moe_out, int top_k, int hidden, int inter, int block) {
+  if (!bucket_i8 || !bucket_sa || !expert_offset || !routes || !w_down || !down_scale ||
+      !moe_accum || !moe_out)
+    return fail(BQ_ERR_INVALID, "%s: null pointer", who);
+  if (top_k <= 0 || top_k > 16) return fail(BQ_ERR_UNSUPPORTED, "%s: top_k %d not in [1,16]", who, top_k);
+  if (!pow2(block) || block < 64 || inter % block || inter % 64 || hidden % 16 || hidden <= 0)
+    return fail(BQ_ERR_SHAPE, "%s: need block a power of two >= 64 dividing inter, hidden %% 16 == 0", who);
+  if (inter / block > 64) return fail(BQ_ERR_UNSUPPORTED, "%s: inter/block = %d > 64", who, inter / block);
+  if (!a16(bucket_i8) || !a16(w_down) || !a16(moe_accum) || !a16(moe_out))
+    return fail(BQ_ERR_INVALID, "%s: int8 operands, moe_accum and moe_out must be 16-byte aligned", who);
+  return BQ_OK;
+}
+
 int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                        const int32_t* expert_offset, const bq_route* routes, const int8_t* w_down,
                        const float* down_scale, float* moe_accum, uint16_t* moe_out,
                        int experts_per_rank, int seq_len, int top_k, int hidden, int inter,
                        int block, void* workspace, size_t workspace_bytes, void* stream) {
   if (seq_len <= 0) return BQ_OK;
-  if (!bucket_i8 || !bucket_sa || !expert_offset || !routes || !w_down || !down_scale ||
-      !moe_accum || !moe_out || !workspace)
-    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: null pointer");
-  if (top_k <= 0 || top_k > 16) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: top_k %d not in [1,16]", top_k);
-  if (!pow2(block) || block < 64 || inter % block || inter % 64 || hidden % 16 || hidden <= 0)
-    return fail(BQ_ERR_SHAPE, "bq_moe_phase2_down: need block a power of two >= 64 dividing inter, hidden %% 16 == 0");
-  if (inter / block > 64) return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down: inter/block = %d > 64", inter / block);
-  if (!a16(bucket_i8) || !a16(w_down) || !a16(moe_accum) || !a16(moe_out))
-    return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: int8 operands, moe_accum and moe_out must be 16-byte aligned");
+  const int r = phase2_args("bq_moe_phase2_down", bucket_i8, bucket_sa, expert_offset, routes,
+                            w_down, down_scale, moe_accum, moe_out, top_k, hidden, inter, block);
+  if (r != BQ_OK) return r;
+  if (!workspace) return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: null pointer");
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(BQ_ERR_INVALID, "bq_moe_phase2_down: workspace must be 256-byte aligned");
   const size_t need = bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
@@ -553,31 +577,27 @@ int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
                                uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
                                int hidden, int inter, int block, void* stream) {
   if (seq_len <= 0) return BQ_OK;
-  if (top_k <= 0 || top_k > 16 || hidden <= 0)
-    return fail(BQ_ERR_UNSUPPORTED, "bq_moe_phase2_down_noalloc: top_k %d not in [1,16]", top_k);
+  int r = phase2_args("bq_moe_phase2_down_noalloc", bucket_i8, bucket_sa, expert_offset, routes,
+                      w_down, down_scale, moe_accum, moe_out, top_k, hidden, inter, block);
+  if (r != BQ_OK) return r;
   // the workspace is seq_len*top_k f32 rows of hidden (bq_moe_phase2_workspace_size)
-  const size_t bytes = (size_t)seq_len * (size_t)top_k * (size_t)hidden * sizeof(float);
-  if (bytes > bq::kNoallocScratchBytes)
+  const size_t need = bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
+  if (need > bq::kNoallocScratchBytes)
     return fail(BQ_ERR_UNSUPPORTED,
                 "bq_moe_phase2_down_noalloc: seq_len*top_k*hidden*4 = %zu bytes exceeds the "
                 "%zu-byte static scratch (use bq_moe_phase2_down with a workspace)",
-                bytes, bq::kNoallocScratchBytes);
+                need, bq::kNoallocScratchBytes);
   int device = 0;
-  int r = check_hip(hipGetDevice(&device), "hipGetDevice");
+  r = check_hip(hipGetDevice(&device), "hipGetDevice");
   if (r) return r;
   void* ws = nullptr;
   r = check_hip(bq::scratch_address(device, &ws), "scratch symbol address");
   if (r) return r;
-  r = bq_moe_phase2_down(bucket_i8, bucket_sa, expert_offset, routes, w_down, down_scale,
-                         moe_accum, moe_out, experts_per_rank, seq_len, top_k, hidden, inter,
-                         block, ws, bq::kNoallocScratchBytes, stream);
-  if (r && r != BQ_ERR_HIP) {
-    // re-label the shared validation's message with this entry point's name
-    char msg[sizeof(g_err)];
-    snprintf(msg, sizeof(msg), "%s", g_err);
-    return fail(r, "bq_moe_phase2_down_noalloc <- %s", msg);
-  }
-  return r;
+  return check_hip(bq::launch_moe_phase2(bucket_i8, bucket_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_down,
+                                         down_scale, moe_accum, moe_out, experts_per_rank, seq_len,
+                                         seq_len * top_k, hidden, inter, block, ws, S(stream)),
+                   "moe_phase2_noalloc");
 }
 
 }  // extern "C"

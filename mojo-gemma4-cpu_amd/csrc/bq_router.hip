@@ -16,6 +16,7 @@
 //   The wave takes k successive maxima of a 64-bit key that encodes that
 //   order, so the selected list is the reference's list entry for entry.
 #include <mutex>
+#include <unordered_map>
 
 #include "bq_device.hpp"
 #include "bq_kernels.hpp"
@@ -333,14 +334,17 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
 // token.  The last top-k workgroup to finish builds the schedule from every
 // workgroup's routes (schedule_small, one thread per slot): each top-k
 // workgroup fences its route stores at device scope before it counts itself
-// done on *done, and the last one fences again before it reads them.  That
-// one resets *done for the next launch, so launches on one device must not
-// overlap (stream order gives that).  With ONE > 0 (up to 16 tokens) a single
+// done on *done, and the last one fences again before it reads them.  The
+// count wraps to 0 on the last workgroup's increment (atomicInc), ready for
+// the next launch on the same counter.  Each stream of a device has its own
+// counter (prep_counter), so launches that overlap on different streams do
+// not share one, and launches on one stream run in order.  With ONE > 0 (up to 16 tokens) a single
 // workgroup after the norm-quant ones takes every token's top-k and builds
 // the schedule from LDS (route_schedule_block), with no hand-off.
 constexpr int kPrepThreads = kSchedSmallSlots;   // 16 waves
 constexpr int kPrepTopkTokens = kPrepThreads / 64;
-__device__ unsigned g_prep_done = 0;
+constexpr int kPrepCounters = 256;  // streams per device with a counter of their own
+__device__ unsigned g_prep_done[kPrepCounters];  // zero-initialized at load
 
 template <int NE, int NSEG, int SPW, int ONE = 0>  // ONE: tokens per wave of the one route workgroup
 __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
@@ -425,7 +429,8 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   __syncthreads();
   if (tid == 0) {
     __threadfence();
-    s_last = atomicAdd(done, 1u) == gridDim.x - (unsigned)nq_blocks - 1u;
+    const unsigned last = gridDim.x - (unsigned)nq_blocks - 1u;
+    s_last = atomicInc(done, last) == last;  // the last increment wraps the count to 0
     if (s_last) __threadfence();
   }
   __syncthreads();
@@ -434,7 +439,6 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   const int ex = route_idx[sc];
   const float wx = route_w[sc];
   schedule_small(tid < slots ? ex : -1, wx, top_k, E, s_wc, s_cnt, expert_offset, routes);
-  if (tid == 0) *done = 0u;  // for the next launch
 }
 
 template <int NE>
@@ -498,10 +502,15 @@ hipError_t launch_route_schedule(const float* logits, const uint16_t* pes, int T
   return hipGetLastError();
 }
 
-// g_prep_done's address on the current device, looked up once per device
-static hipError_t prep_counter(unsigned** out) {
+// The completion counter of stream `st` on the current device: slot i of
+// g_prep_done, the slots handed out to streams in order of first use (the
+// array's address looked up once per device).  *out is null once every slot
+// of the device is taken; the caller then runs the prep as separate launches,
+// which need no counter.
+static hipError_t prep_counter(hipStream_t st, unsigned** out) {
   constexpr int kDevices = 64;
   static unsigned* addr[kDevices] = {};
+  static std::unordered_map<hipStream_t, int> slot[kDevices];
   static std::mutex mu;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -514,7 +523,15 @@ static hipError_t prep_counter(unsigned** out) {
     if (e != hipSuccess) return e;
     addr[dev] = static_cast<unsigned*>(p);
   }
-  *out = addr[dev];
+  auto it = slot[dev].find(st);
+  if (it == slot[dev].end()) {
+    if ((int)slot[dev].size() >= kPrepCounters) {
+      *out = nullptr;
+      return hipSuccess;
+    }
+    it = slot[dev].emplace(st, (int)slot[dev].size()).first;
+  }
+  *out = addr[dev] + it->second;
   return hipSuccess;
 }
 
@@ -566,9 +583,16 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
   const int unit = block > 128 ? block / 128 : 1;
   int spw = (ns + 7) / 8;
   spw = (spw + unit - 1) / unit * unit;
-  const bool fused = T * top_k <= kSchedSmallSlots && hidden % 256 == 0 && hidden <= 4096 &&
-                     tune().nq_pair && tune().moe_prep && !(reinterpret_cast<uintptr_t>(xq) & 1u) &&
-                     (ns + spw - 1) / spw <= 8;
+  const bool one = tune().prep_one && T <= kPrepTopkTokens;
+  unsigned* done = nullptr;
+  bool fused = T * top_k <= kSchedSmallSlots && hidden % 256 == 0 && hidden <= 4096 &&
+               tune().nq_pair && tune().moe_prep && !(reinterpret_cast<uintptr_t>(xq) & 1u) &&
+               (ns + spw - 1) / spw <= 8;
+  if (fused && !one) {  // the spread form's hand-off needs the stream's counter
+    const hipError_t ra = prep_counter(st, &done);
+    if (ra != hipSuccess) return ra;
+    fused = done != nullptr;
+  }
   // larger batches with FWHT block 128: top-k and norm-quant in one launch,
   // then the schedule (the conditions of launch_norm_quant's v8 path)
   const bool wide = !fused && T * top_k > kSchedSmallSlots && block == 128 && hidden % 256 == 0 &&
@@ -602,9 +626,6 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
     if (r != hipSuccess) return r;
     return launch_norm_quant(src, gamma, xq, sa, T, hidden, block, sqrt_n, n_eps, st);
   }
-  unsigned* done = nullptr;
-  const hipError_t ra = prep_counter(&done);
-  if (ra != hipSuccess) return ra;
   const int nq_blocks = (T + 1) / 2;
   // up to 16 tokens one workgroup takes every top-k (one token per wave) and
   // builds the schedule from LDS, with no cross-workgroup hand-off: the
@@ -612,7 +633,6 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
   // wave) the spread top-k with the last-workgroup schedule is faster (the
   // prep alone 9.2 vs 13.2 us, the layer 125.4 vs 129.3 us).  BQ_PREP_ONE=0
   // keeps the spread form.
-  const bool one = tune().prep_one && T <= kPrepTopkTokens;
   const dim3 g(nq_blocks + (one ? 1 : (T + kPrepTopkTokens - 1) / kPrepTopkTokens)), b(kPrepThreads);
   const float sc = fwht_scale_host(block);
   const int ne = (E + 63) / 64;

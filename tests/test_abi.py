@@ -102,6 +102,17 @@ def test_validation_errors(L):
                                 C.c_void_p(256), 0, None) == 2
     assert L.bq_moe_phase2_down(P, P, P, P, P, P, P, P, 128, 4, 8, 2816, 704, 64,
                                 C.c_void_p(100), 1 << 30, None) == 1
+    # the allocation-free phase 2 validates exactly as the workspace entry point
+    ws = C.c_void_p(256)
+    for args, code in (((128, 4, 8, 0, 704, 64), 2),        # hidden <= 0
+                       ((128, 4, 8, 2816 + 8, 704, 64), 2),  # hidden % 16
+                       ((128, 4, 0, 2816, 704, 64), 4),      # top_k
+                       ((128, 4, 17, 2816, 704, 64), 4),
+                       ((128, 4, 8, 2816, 700, 64), 2),      # inter % block
+                       ((128, 4, 8, 2816, 704, 96), 2)):     # block
+        assert L.bq_moe_phase2_down(*([P] * 8), *args, ws, 1 << 30, None) == code
+        assert L.bq_moe_phase2_down_noalloc(*([P] * 8), *args, None) == code
+    assert L.bq_moe_phase2_down_noalloc(*([P] * 7), None, 128, 4, 8, 2816, 704, 64, None) == 1
     f1 = C.c_float(1)
     nl = lambda *a: L.bq_norm_linear(*a, f1, f1, None)
     assert nl(P, P, P, P, P, P, P, None, 256, 1, 2816, 48) == 2        # FWHT block

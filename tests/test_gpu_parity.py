@@ -444,6 +444,35 @@ def test_moe_prep(gpu, O, T, E, k, H, B, pes):
         np.testing.assert_array_equal(host(sa), rsa)
 
 
+def test_moe_prep_two_streams(gpu, O):
+    """The spread form's completion counter is per stream: two streams run
+    preps of different batches at the same time, each bit-exact."""
+    import torch
+    E, k, H, B = 128, 8, 2816, 128
+    cases = []
+    for T in (32, 48):
+        logits = O.synth_normal_f32(90 + T, 1.0, (T, E))
+        x = O.synth_normal_bf16(91 + T, 1.0, (T, H))
+        g = O.f32_to_bf16(O.synth_normal_f32(92, 0.3, (H,)) + 1.0)
+        ridx, rw = O.route_topk_softmax(logits, k, None)
+        reo, rroutes = O.build_schedule(ridx, rw, E)
+        cases.append((dev(logits), dev(x), dev(g), ridx, rw, reo, rroutes))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for _ in range(20):
+        outs = []
+        for (lg, x, g, *_), st in zip(cases, streams):
+            with torch.cuda.stream(st):
+                outs.append(gpu.moe_prep(lg, x, g, k, None, block=B))
+        torch.cuda.synchronize()
+        for (_, _, _, ridx, rw, reo, rroutes), (idx, w, eo, routes, xq, sa) in zip(cases, outs):
+            np.testing.assert_array_equal(host(idx), ridx)
+            np.testing.assert_array_equal(host(w), rw)
+            np.testing.assert_array_equal(host(eo), reo)
+            r = host(routes)
+            np.testing.assert_array_equal(r[:, 0], rroutes["token"])
+            np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
+
+
 def test_moe_prep_batches_in_a_row(gpu, O):
     """calls of different batch sizes after each other (grids of different
     workgroup counts share the completion counter) match the separate calls"""

@@ -1,7 +1,8 @@
 """bq_moe_phase2_down_noalloc (phase 2 on the library's static per-GPU
 scratch) against bq_moe_phase2_down (caller workspace), through the C ABI:
-bit-identical accum and out on two calls in a row, the second with fewer
-tokens, so the scratch holds the first call's rows when the second starts;
+bit-identical accum and out on calls in a row, each with fewer tokens than
+the one before, so the scratch holds the previous call's rows when the next
+starts (the first fills it to within 32 KiB of its size);
 sizes past the scratch are rejected before anything is launched."""
 import numpy as np
 import pytest
@@ -27,7 +28,10 @@ def test_noalloc_matches_workspace_entry(gpu, O, moe_model):
     import torch
     m = moe_model
     E, H = m["E"], m["H"]
-    for T, seed in ((96, 11), (24, 13)):   # the second call is smaller
+    # each call smaller than the one before; 279 tokens fill the scratch to
+    # within 32 KiB of its 24 MiB (279 * 8 * 2816 * 4 bytes), 279 and 256 take
+    # the whole-row combine, 96 and 24 the 256-column one
+    for T, seed in ((279, 7), (256, 9), (96, 11), (24, 13)):
         print(f"noalloc phase 2: T={T}", flush=True)
         eo, routes, bi8, bsa = _layer_inputs(gpu, O, m, T, seed)
         acc_ws, out_ws = gpu.moe_phase2(bi8, bsa, eo, routes, m["Wd"], E, T, 8, H)
