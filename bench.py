@@ -158,6 +158,10 @@ def calib_lib():
     L.bqc_mfma_i8.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     L.bqc_mfma_i8_ops.argtypes = [C.c_int, C.c_int, C.c_int]
     L.bqc_mfma_i8_ops.restype = C.c_double
+    L.bqc_lds_read.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.bqc_dma_l2.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                             C.c_void_p, C.c_void_p]
+    L.bqc_mfma_chain.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     return L
 
 
@@ -312,6 +316,74 @@ def bench_mfma(torch):
                      "p50_TOPs": round(ops / (np.median(ts) * 1e-3) / 1e12, 1),
                      "ops_per_launch": ops}
     res["launch"] = f"{blocks} workgroups x 4 waves ({cus} CUs), {iters} iterations"
+    return res
+
+
+def bench_probes(torch):
+    """The measured ceilings the tiled kernels are designed against
+    (libbq_calib.so): LDS read bytes per clock per CU (ds_read_b128,
+    conflict-free), L2-resident global -> LDS DMA (whole 128-byte lines vs
+    the raw 16 x 64-byte MFMA fragment), the latency of a dependent
+    v_mfma_i32_16x16x64_i8 chain, and the streaming read of 256 MiB per
+    launch over the sweep's launch shapes (4 replicas, 1 GiB).  Cycle counts
+    come from each workgroup's own shader clock; one workgroup per CU."""
+    import numpy as np
+    L = calib_lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    st = _stream(torch)
+    cyc = torch.empty(cus, dtype=torch.int64, device="cuda")
+    res = {}
+
+    def timed(launch, reps=5):
+        best = None
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            rc = launch()
+            b.record()
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError(f"calib probe: hipError {rc}")
+            ms, c = a.elapsed_time(b), float(cyc.float().median().item())
+            if best is None or ms < best[0]:
+                best = (ms, c)
+        return best
+
+    fold = torch.empty(cus * 1024, dtype=torch.int32, device="cuda")
+    iters = 256
+    lds = {}
+    for waves in (4, 8, 16):
+        ms, c = timed(lambda: L.bqc_lds_read(waves, cus, iters, cyc.data_ptr(), fold.data_ptr(), st))
+        per_block = waves * 64 * 16 * 8 * iters
+        lds[f"{waves}_waves"] = {"B_per_clk_per_cu": round(per_block / c, 1),
+                                 "TBs": round(per_block * cus / (ms * 1e-3) / 1e12, 1)}
+    res["lds_read_b128"] = lds
+    rows, stride = 512, 4096  # a 2 MiB source every workgroup reads
+    src = torch.randint(-127, 128, (rows * stride,), dtype=torch.int8, device="cuda")
+    dma = {}
+    for shape, name in ((0, "lines_8x128B"), (1, "fragments_16x64B")):
+        for waves in (4, 8):  # 32 or 64 KiB in flight per CU
+            ms, c = timed(lambda: L.bqc_dma_l2(shape, waves, src.data_ptr(), stride, rows, cus,
+                                                64, cyc.data_ptr(), st))
+            per_block = waves * 8 * 1024 * 64
+            dma[f"{name}_{waves * 8}KiB_in_flight"] = {
+                "B_per_clk_per_cu": round(per_block / c, 1),
+                "TBs": round(per_block * cus / (ms * 1e-3) / 1e12, 1)}
+    res["dma_l2_to_lds"] = dma
+    n = 4096
+    out = torch.empty(64, dtype=torch.int32, device="cuda")
+    cyc1 = torch.empty(1, dtype=torch.int64, device="cuda")
+    rc = L.bqc_mfma_chain(n, 1, cyc1.data_ptr(), out.data_ptr(), st)
+    torch.cuda.synchronize()
+    if rc != 0:
+        raise RuntimeError(f"bqc_mfma_chain: hipError {rc}")
+    res["mfma_16x16x64_i8_chain_cycles_per_link"] = round(int(cyc1.item()) / n, 1)
+    big = torch.randint(-127, 128, (4, 256 << 20), dtype=torch.int8, device="cuda")
+    sw = bench_stream_sweep(torch, [big[i] for i in range(4)], 4096, samples=50)
+    res["stream_256MiB"] = {"best": sw["best"],
+                            "shapes": [{k: r[k] for k in ("workgroups", "waves", "loads_per_wave",
+                                                          "p50_us", "GBs")} for r in sw["shapes"]]}
+    del big
     return res
 
 
@@ -603,8 +675,28 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     stack_ms = 25 * ms_s + 5 * ms_f
     bf = lambda t: t.view(torch.int16).cpu().numpy().view("uint16")
     host.update(x=bf(x), attn_s=bf(attn_s), attn_f=bf(attn_f), moe=moe)
+    # algorithmic bytes of one layer call: every weight (codes + per-row
+    # scales) read once, the touched experts' weights, and each launch's
+    # activations in and out
+    wb = lambda n, k: n * k + 4 * n
+    nq = lambda k: 2 * T * k + 2 * k + T * k + 4 * T            # norm-quant: bf16 in, int8 + scale out
+    lin = lambda n, k, nb=1: T * k + 4 * T * nb + 2 * T * n     # linear: int8 + scales in, bf16 out
+    bqz = lambda k, b: 2 * T * k + T * k + 4 * T * (k // b)     # block-quant
+    mlp = (nq(H) + 2 * wb(2112, H) + lin(2 * 2112, H) + bqz(2112, 64) + wb(H, 2112) +
+           lin(H, 2112, 2112 // 64))
+    sliding_b = (nq(H) + wb(4096, H) + wb(2048, H) + wb(2048, H) + lin(8192, H) +
+                 bqz(4096, 256) + wb(H, 4096) + lin(H, 4096, 16) + mlp)
+    full_b = (nq(H) + wb(8192, H) + wb(1024, H) + lin(9216, H) + bqz(8192, 512) +
+              wb(H, 8192) + lin(H, 8192, 16) + mlp)
+    eo = moe.eo.cpu().numpy()
+    touched = int((eo[1:] - eo[:-1] > 0).sum())
+    R = T * TOPK
+    moe_b = (touched * (2 * I * H + 2 * I * 4 + H * I + H * 4) + 4 * T * E + nq(H) +
+             R * (I + 4 * (I // 64)) * 2 + R * H * 4 * 2 + T * H * (4 + 2))
     return dict(sliding_layer_ms=ms_s, full_layer_ms=ms_f, moe_ms=ms_m,
-                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3), cpu_inputs=host)
+                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3), cpu_inputs=host,
+                experts_touched=touched, sliding_bytes=sliding_b + moe_b, full_bytes=full_b + moe_b,
+                moe_bytes=moe_b)
 
 
 def bench_attn(bq, torch, steps):
@@ -1168,6 +1260,8 @@ def main():
         res["stream_sweep"] = bench_stream_sweep(torch, [pool[i] for i in range(64)], 256)
     if wl in ("all", "gemv", "mfma"):
         res["mfma"] = bench_mfma(torch)
+    if wl in ("all", "mfma", "stream_sweep"):
+        res["probes"] = bench_probes(torch)
     if args.calib_copy:
         calib_copy(torch)
 
@@ -1225,6 +1319,8 @@ def main():
                     ms_per_step=None, config={"workload": wl})
     if "mfma" in res:
         line["mfma_i8_measured"] = res["mfma"]
+    if "probes" in res:
+        line["measured_ceilings"] = res["probes"]
     if "prefill" in res:
         p = res["prefill"]
         line["prefill_gemm_m512"] = {
@@ -1269,8 +1365,23 @@ def main():
                     "basis": "touched experts' weight and scale bytes / p50 layer time"}
             line[f"moe_layer_T{T}"] = d
     if "layer16" in res:
-        line["decoder_layer_b16"] = {k: round(v, 4) for k, v in res["layer16"].items()
-                                     if k != "cpu_inputs"}
+        l16 = res["layer16"]
+        line["decoder_layer_b16"] = {k: round(v, 4) for k, v in l16.items()
+                                     if k not in ("cpu_inputs", "sliding_bytes", "full_bytes",
+                                                  "moe_bytes", "experts_touched")}
+        gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
+        s_gbs = gbs(l16["sliding_bytes"], l16["sliding_layer_ms"])
+        line["decoder_layer_b16"]["experts_touched"] = l16["experts_touched"]
+        line["decoder_layer_b16"]["roofline"] = {
+            "bound": "hbm", "achieved": round(s_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(s_gbs / HBM_PEAK_GBS, 4),
+            "traffic": _traffic("decoder_layer_b16_traffic.txt"),
+            "alg_bytes": l16["sliding_bytes"],
+            "full_layer_GBs": round(gbs(l16["full_bytes"], l16["full_layer_ms"]), 1),
+            "full_layer_alg_bytes": l16["full_bytes"],
+            "moe_GBs": round(gbs(l16["moe_bytes"], l16["moe_ms"]), 1),
+            "basis": "sliding layer: every projection's weights once, the touched experts' "
+                     "weights, each launch's activations in and out / p50 layer time"}
         if "attn" in res:
             # the same stack with each layer's attention step (prep + int8-KV
             # attention at decode batch 16: sliding layers at a full 1024

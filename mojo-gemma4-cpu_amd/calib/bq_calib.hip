@@ -20,6 +20,10 @@
 // bqc_mfma_i8: back-to-back int8 MFMAs from registers (8 or 16 independent
 //   v_mfma_i32_16x16x64_i8 chains, or 4 v_mfma_i32_32x32x32_i8 chains, per
 //   wave), 4 waves per workgroup; one int per thread written at the end.
+// bqc_lds_read, bqc_dma_l2, bqc_mfma_chain: the LDS, L2 -> LDS and MFMA
+//   latency figures behind the tiled kernels' design.  Each workgroup times
+//   itself in shader clocks (s_memtime after a barrier at both ends) and
+//   writes its cycle count, so the figures come out per clock.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -153,6 +157,95 @@ __global__ __launch_bounds__(256) void k_mfma_i8(int iters, int* __restrict__ ou
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// LDS read rate: W waves, each lane reading 16-byte words of a 64 KiB LDS
+// buffer, 64 consecutive words per wave and instruction (conflict-free),
+// 8 reads in flight per iteration; the words are XOR-folded so no read is
+// dropped.  cyc[block] = the block's cycles; fold[block * W*64 + t] = folds.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_lds_read(int iters, long long* __restrict__ cyc,
+                                                     int* __restrict__ fold) {
+  // 96 KiB, of which the first 64 are read: one workgroup per CU
+  __shared__ v4i buf[6144];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  for (int i = t; i < 4096; i += W * 64) buf[i] = v4i{i, i * 3, i ^ 5, i + 7};
+  __syncthreads();
+  const long long c0 = clock64();
+  int acc = 0;
+  for (int i = 0; i < iters; ++i) {
+    v4i b[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b[u] = buf[((((i * 8 + u) * 7 + wave) & 63) << 6) + lane];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= (b[u].x ^ b[u].y) ^ (b[u].z ^ b[u].w);
+  }
+  __syncthreads();
+  const long long c1 = clock64();
+  if (t == 0) cyc[blockIdx.x] = c1 - c0;
+  fold[blockIdx.x * W * 64 + t] = acc;
+}
+
+// L2-resident global -> LDS DMA (global_load_lds_dwordx4, 1 KiB per
+// instruction): W waves, each issuing 8 DMAs per iteration into its own 8
+// KiB of LDS and waiting for them.  The source is `rows` rows of `stride`
+// bytes; shape 0 reads 8 rows x 128 bytes per DMA (whole 128-byte lines),
+// shape 1 16 rows x 64 bytes (the raw 16x16x64 MFMA fragment), walking the
+// source's row blocks, then its column blocks.  Every block reads the same
+// small source, so after the first pass L2 serves it.
+template <int W, int SHAPE>
+__global__ __launch_bounds__(W * 64) void k_dma_l2(const int8_t* __restrict__ src, int stride,
+                                                   int rows, int iters, long long* __restrict__ cyc) {
+  // 96 KiB (one workgroup per CU), of which W * 8 KiB are written
+  static_assert(W * 8 <= 96, "LDS");
+  __shared__ __attribute__((aligned(16))) int8_t lds[96 * 1024];
+  const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  // this lane's row and 16-byte chunk within a DMA's block of rows
+  const int r = SHAPE == 0 ? lane >> 3 : lane & 15;
+  const int c = SHAPE == 0 ? lane & 7 : lane >> 4;
+  constexpr int RPD = SHAPE == 0 ? 8 : 16;    // rows per DMA
+  constexpr int CPD = SHAPE == 0 ? 128 : 64;  // bytes of a row per DMA
+  const int col_blocks = stride / CPD, row_blocks = rows / RPD;
+  const uint32_t l0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lds;
+  __syncthreads();
+  const long long c0 = clock64();
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      // DMA index; workgroups start 37 blocks apart, so the CUs sharing an
+      // L2 read different lines at any moment
+      const int q = (i * 8 + d) * W + wave + (int)blockIdx.x * 37;
+      const int rb = q % row_blocks, cb = (q / row_blocks) % col_blocks;
+      const int8_t* g = src + (size_t)(rb * RPD + r) * stride + cb * CPD + c * 16;
+      const uint32_t l = __builtin_amdgcn_readfirstlane(l0 + (uint32_t)((wave * 8 + d) * 1024));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                   :: "s"(l), "v"(g) : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __syncthreads();
+  const long long c1 = clock64();
+  if (t == 0) cyc[blockIdx.x] = c1 - c0;
+}
+
+// One wave's dependent v_mfma_i32_16x16x64_i8 chain (each MFMA takes the
+// previous one's result as its accumulator): cycles per link.
+__global__ __launch_bounds__(64) void k_mfma_chain(int n, long long* __restrict__ cyc,
+                                                   int* __restrict__ out) {
+  const int t = threadIdx.x;
+  const v4i a = {t, t * 3, t * 5, t * 7}, b = {t ^ 1, t ^ 2, t ^ 3, t ^ 4};
+  v4i c = {t, 0, 0, 0};
+  const long long c0 = clock64();
+  for (int i = 0; i < n; ++i) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  // the last link's result is read before the clock stops
+  int s = c.x + c.y + c.z + c.w;
+  s = __builtin_amdgcn_readfirstlane(s);
+  const long long c1 = clock64();
+  if (t == 0) cyc[blockIdx.x] = c1 - c0;
+  out[blockIdx.x * 64 + t] = s + t;
+}
+
 }  // namespace
 
 extern "C" {
@@ -244,6 +337,49 @@ int bqc_mfma_i8(int shape, int blocks, int iters, int* out, void* stream) {
 double bqc_mfma_i8_ops(int shape, int blocks, int iters) {
   const double per = 262144.0;  // 8 x 32768 = 16 x 32768 / 2 = 4 x 65536
   return per * iters * (double)blocks * 4.0;  // 4 waves per block
+}
+
+// LDS read rate: blocks of `waves` (4, 8 or 16) waves, iters x 8 reads of 16
+// bytes per lane; cyc: blocks long longs (cycles per block), fold: blocks *
+// waves * 64 ints.  Bytes read per block: waves * 64 * 16 * 8 * iters.
+int bqc_lds_read(int waves, int blocks, int iters, long long* cyc, int* fold, void* stream) {
+  if (!cyc || !fold || blocks <= 0 || iters <= 0) return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  if (waves == 4) hipLaunchKernelGGL(k_lds_read<4>, dim3(blocks), dim3(256), 0, st, iters, cyc, fold);
+  else if (waves == 8) hipLaunchKernelGGL(k_lds_read<8>, dim3(blocks), dim3(512), 0, st, iters, cyc, fold);
+  else if (waves == 16) hipLaunchKernelGGL(k_lds_read<16>, dim3(blocks), dim3(1024), 0, st, iters, cyc, fold);
+  else return (int)hipErrorInvalidValue;
+  return (int)hipGetLastError();
+}
+
+// L2-resident LDS DMA: blocks of `waves` (4 or 8) waves, iters x 8 DMAs of 1
+// KiB per wave; shape 0 = 8 rows x 128 bytes, 1 = 16 rows x 64 bytes per
+// DMA.  src: rows x stride bytes, 16-byte aligned (stride a multiple of 128,
+// rows a multiple of 16).  cyc: blocks long longs.  Bytes per block: waves *
+// 8 * 1024 * iters.
+int bqc_dma_l2(int shape, int waves, const int8_t* src, int stride, int rows, int blocks,
+               int iters, long long* cyc, void* stream) {
+  if (!src || !cyc || blocks <= 0 || iters <= 0 || stride <= 0 || stride % 128 || rows <= 0 ||
+      rows % 16 || (shape != 0 && shape != 1) || (reinterpret_cast<uintptr_t>(src) & 15u))
+    return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+#define BQC_DMA(W, S)                                                                        \
+  if (waves == W && shape == S) {                                                            \
+    hipLaunchKernelGGL((k_dma_l2<W, S>), dim3(blocks), dim3(W * 64), 0, st, src, stride, rows, \
+                       iters, cyc);                                                          \
+    return (int)hipGetLastError();                                                           \
+  }
+  BQC_DMA(4, 0) BQC_DMA(4, 1) BQC_DMA(8, 0) BQC_DMA(8, 1)
+#undef BQC_DMA
+  return (int)hipErrorInvalidValue;
+}
+
+// A dependent chain of n v_mfma_i32_16x16x64_i8 in one wave per block; cyc:
+// blocks long longs, out: blocks * 64 ints.
+int bqc_mfma_chain(int n, int blocks, long long* cyc, int* out, void* stream) {
+  if (!cyc || !out || n <= 0 || blocks <= 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mfma_chain, dim3(blocks), dim3(64), 0, (hipStream_t)stream, n, cyc, out);
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -210,7 +210,7 @@ def test_calib_library_exports():
     path = os.path.join(ROOT, "mojo-gemma4-cpu_amd", "libbq_calib.so")
     lib = C.CDLL(path)
     for n in ("bqc_stream_read", "bqc_stream_sweep", "bqc_stream_shapes", "bqc_stream_shape",
-              "bqc_mfma_i8", "bqc_mfma_i8_ops"):
+              "bqc_mfma_i8", "bqc_mfma_i8_ops", "bqc_lds_read", "bqc_dma_l2", "bqc_mfma_chain"):
         assert hasattr(lib, n)
     lib.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                     C.c_void_p]
@@ -236,3 +236,15 @@ def test_calib_library_exports():
     assert lib.bqc_mfma_i8(24, 4, 8, P, None) != 0           # no such MFMA tile
     assert lib.bqc_mfma_i8(17, 4, 7, P, None) != 0           # odd iterations on 16 chains
     assert lib.bqc_mfma_i8_ops(32, 1024, 2048) == 262144.0 * 2048 * 1024 * 4
+    # the probes' argument checks (no launch reaches the GPU)
+    lib.bqc_lds_read.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    lib.bqc_dma_l2.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                               C.c_void_p, C.c_void_p]
+    lib.bqc_mfma_chain.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    assert lib.bqc_lds_read(12, 4, 8, P, P, None) != 0            # waves
+    assert lib.bqc_lds_read(8, 4, 0, P, P, None) != 0             # iterations
+    assert lib.bqc_dma_l2(2, 8, P, 4096, 512, 4, 8, P, None) != 0   # no such shape
+    assert lib.bqc_dma_l2(0, 8, P, 4000, 512, 4, 8, P, None) != 0   # stride not whole lines
+    assert lib.bqc_dma_l2(0, 8, P, 4096, 500, 4, 8, P, None) != 0   # rows not whole blocks
+    assert lib.bqc_dma_l2(0, 8, C.c_void_p(17), 4096, 512, 4, 8, P, None) != 0  # misaligned
+    assert lib.bqc_mfma_chain(0, 1, P, P, None) != 0
