@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
   const int x = route_idx[sc];
   const float w = route_w[sc];
   const int e = (tid < slots && x >= ebase && x < ebase + E) ? x - ebase : -1;
-  schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
+  schedule_small(e, w, top_k, E, slots, s_wc, s_cnt, expert_offset, routes);
 }
 
 // Skinny (16-record m-tile) kernels for decode-sized batches.  Each wave owns

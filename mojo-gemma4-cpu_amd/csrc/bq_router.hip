@@ -194,6 +194,12 @@ __device__ inline void topk_tokens(const float* const (&rows)[TPW],
   for (int i = 0; i < TPW; ++i)
 #pragma unroll
     for (int q = 0; q < NE; ++q) lgv[i][q] = rows[i][min(lane + 64 * q, E - 1)];
+  // the per-expert scales of this lane's experts, loaded beside the logits:
+  // the winners' scales are then a lane exchange, not a second dependent
+  // global load after the top-k
+  float pev[NE];
+#pragma unroll
+  for (int q = 0; q < NE; ++q) pev[q] = pes ? bf16_to_f32(pes[min(lane + 64 * q, E - 1)]) : 1.0f;
   uint64_t local[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
@@ -248,7 +254,14 @@ __device__ inline void topk_tokens(const float* const (&rows)[TPW],
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const float inv_sum = 1.0f / sum[i];
-    const float sc = (lane < top_k && pes) ? bf16_to_f32(pes[my_e[i]]) : 1.0f;
+    // expert my_e's scale sits in lane my_e % 64, slot my_e / 64
+    float sc = 1.0f;
+#pragma unroll
+    for (int q = 0; q < NE; ++q) {
+      const float v = __shfl(pev[q], my_e[i] & 63, kWave);
+      if ((my_e[i] >> 6) == q) sc = v;
+    }
+    if (!(lane < top_k && pes)) sc = 1.0f;
     out_e[i] = my_e[i];
     out_w[i] = my_ev[i] * inv_sum * sc;
   }
@@ -311,7 +324,7 @@ __device__ inline void route_schedule_block(
   const bool live = tid < T * top_k;
   const int e = live ? s_e[tid] : -1;
   const float w = live ? s_w[tid] : 0.0f;
-  schedule_small(e, w, top_k, E, s_wc, s_cnt, expert_offset, routes);
+  schedule_small(e, w, top_k, E, T * top_k, s_wc, s_cnt, expert_offset, routes);
 }
 
 template <int NE, int TPW>
@@ -438,7 +451,7 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   const int slots = T * top_k, sc = min(tid, slots - 1);
   const int ex = route_idx[sc];
   const float wx = route_w[sc];
-  schedule_small(tid < slots ? ex : -1, wx, top_k, E, s_wc, s_cnt, expert_offset, routes);
+  schedule_small(tid < slots ? ex : -1, wx, top_k, E, slots, s_wc, s_cnt, expert_offset, routes);
 }
 
 template <int NE>
