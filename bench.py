@@ -162,6 +162,8 @@ def calib_lib():
     L.bqc_dma_l2.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                              C.c_void_p, C.c_void_p]
     L.bqc_mfma_chain.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.bqc_vmem_l2.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                              C.c_void_p, C.c_void_p, C.c_void_p]
     return L
 
 
@@ -370,6 +372,15 @@ def bench_probes(torch):
                 "B_per_clk_per_cu": round(per_block / c, 1),
                 "TBs": round(per_block * cus / (ms * 1e-3) / 1e12, 1)}
     res["dma_l2_to_lds"] = dma
+    vm = {}
+    for waves in (4, 8):
+        ms, c = timed(lambda: L.bqc_vmem_l2(waves, src.data_ptr(), stride, rows, cus, 64,
+                                             cyc.data_ptr(), fold.data_ptr(), st))
+        per_block = waves * 8 * 1024 * 64
+        vm[f"lines_8x128B_{waves * 8}KiB_in_flight"] = {
+            "B_per_clk_per_cu": round(per_block / c, 1),
+            "TBs": round(per_block * cus / (ms * 1e-3) / 1e12, 1)}
+    res["vmem_l2_to_vgpr"] = vm
     n = 4096
     out = torch.empty(64, dtype=torch.int32, device="cuda")
     cyc1 = torch.empty(1, dtype=torch.int64, device="cuda")

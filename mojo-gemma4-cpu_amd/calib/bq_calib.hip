@@ -20,7 +20,8 @@
 // bqc_mfma_i8: back-to-back int8 MFMAs from registers (8 or 16 independent
 //   v_mfma_i32_16x16x64_i8 chains, or 4 v_mfma_i32_32x32x32_i8 chains, per
 //   wave), 4 waves per workgroup; one int per thread written at the end.
-// bqc_lds_read, bqc_dma_l2, bqc_mfma_chain: the LDS, L2 -> LDS and MFMA
+// bqc_lds_read, bqc_dma_l2, bqc_vmem_l2, bqc_mfma_chain: the LDS, L2 -> LDS,
+//   L2 -> VGPR and MFMA
 //   latency figures behind the tiled kernels' design.  Each workgroup times
 //   itself in shader clocks (s_memtime after a barrier at both ends) and
 //   writes its cycle count, so the figures come out per clock.
@@ -229,6 +230,40 @@ __global__ __launch_bounds__(W * 64) void k_dma_l2(const int8_t* __restrict__ sr
   if (t == 0) cyc[blockIdx.x] = c1 - c0;
 }
 
+// The same reads as k_dma_l2's shape 0 (8 rows x 128 bytes per wave
+// instruction, workgroups staggered) into VGPRs instead of LDS: each wave
+// issues 8 global_load_dwordx4 per iteration and folds them (XOR) before the
+// next, so 8 KiB per wave are in flight.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_vmem_l2(const int8_t* __restrict__ src, int stride,
+                                                    int rows, int iters, long long* __restrict__ cyc,
+                                                    int* __restrict__ fold) {
+  // 96 KiB of LDS, unused: one workgroup per CU, as the DMA probe
+  __shared__ int pad[96 * 256];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int r = lane >> 3, c = lane & 7;
+  const int col_blocks = stride / 128, row_blocks = rows / 8;
+  if (iters < 0) pad[t] = 0;  // never: keeps the allocation
+  __syncthreads();
+  const long long c0 = clock64();
+  v4i acc = {0, 0, 0, 0};
+  for (int i = 0; i < iters; ++i) {
+    v4i b[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int q = (i * 8 + d) * W + wave + (int)blockIdx.x * 37;
+      const int rb = q % row_blocks, cb = (q / row_blocks) % col_blocks;
+      b[d] = *reinterpret_cast<const v4i*>(src + (size_t)(rb * 8 + r) * stride + cb * 128 + c * 16);
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc ^= b[d];
+  }
+  __syncthreads();
+  const long long c1 = clock64();
+  if (t == 0) cyc[blockIdx.x] = c1 - c0;
+  fold[blockIdx.x * W * 64 + t] = acc.x ^ acc.y ^ acc.z ^ acc.w ^ (iters < 0 ? pad[t] : 0);
+}
+
 // One wave's dependent v_mfma_i32_16x16x64_i8 chain (each MFMA takes the
 // previous one's result as its accumulator): cycles per link.
 __global__ __launch_bounds__(64) void k_mfma_chain(int n, long long* __restrict__ cyc,
@@ -372,6 +407,24 @@ int bqc_dma_l2(int shape, int waves, const int8_t* src, int stride, int rows, in
   BQC_DMA(4, 0) BQC_DMA(4, 1) BQC_DMA(8, 0) BQC_DMA(8, 1)
 #undef BQC_DMA
   return (int)hipErrorInvalidValue;
+}
+
+// k_dma_l2's shape-0 reads into VGPRs: blocks of `waves` (4 or 8) waves,
+// iters x 8 loads of 1 KiB per wave (src as for bqc_dma_l2); cyc: blocks
+// long longs, fold: blocks * waves * 64 ints.
+int bqc_vmem_l2(int waves, const int8_t* src, int stride, int rows, int blocks, int iters,
+                long long* cyc, int* fold, void* stream) {
+  if (!src || !cyc || !fold || blocks <= 0 || iters <= 0 || stride <= 0 || stride % 128 ||
+      rows <= 0 || rows % 16 || (reinterpret_cast<uintptr_t>(src) & 15u))
+    return (int)hipErrorInvalidValue;
+  hipStream_t st = (hipStream_t)stream;
+  if (waves == 4)
+    hipLaunchKernelGGL(k_vmem_l2<4>, dim3(blocks), dim3(256), 0, st, src, stride, rows, iters, cyc, fold);
+  else if (waves == 8)
+    hipLaunchKernelGGL(k_vmem_l2<8>, dim3(blocks), dim3(512), 0, st, src, stride, rows, iters, cyc, fold);
+  else
+    return (int)hipErrorInvalidValue;
+  return (int)hipGetLastError();
 }
 
 // A dependent chain of n v_mfma_i32_16x16x64_i8 in one wave per block; cyc:

@@ -210,7 +210,8 @@ def test_calib_library_exports():
     path = os.path.join(ROOT, "mojo-gemma4-cpu_amd", "libbq_calib.so")
     lib = C.CDLL(path)
     for n in ("bqc_stream_read", "bqc_stream_sweep", "bqc_stream_shapes", "bqc_stream_shape",
-              "bqc_mfma_i8", "bqc_mfma_i8_ops", "bqc_lds_read", "bqc_dma_l2", "bqc_mfma_chain"):
+              "bqc_mfma_i8", "bqc_mfma_i8_ops", "bqc_lds_read", "bqc_dma_l2", "bqc_mfma_chain",
+              "bqc_vmem_l2"):
         assert hasattr(lib, n)
     lib.bqc_stream_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                     C.c_void_p]
