@@ -373,7 +373,7 @@ def bench_probes(torch):
                 "TBs": round(per_block * cus / (ms * 1e-3) / 1e12, 1)}
     res["dma_l2_to_lds"] = dma
     vm = {}
-    for waves in (4, 8):
+    for waves in (4, 8, 16):
         ms, c = timed(lambda: L.bqc_vmem_l2(waves, src.data_ptr(), stride, rows, cus, 64,
                                              cyc.data_ptr(), fold.data_ptr(), st))
         per_block = waves * 8 * 1024 * 64

@@ -409,7 +409,7 @@ int bqc_dma_l2(int shape, int waves, const int8_t* src, int stride, int rows, in
   return (int)hipErrorInvalidValue;
 }
 
-// k_dma_l2's shape-0 reads into VGPRs: blocks of `waves` (4 or 8) waves,
+// k_dma_l2's shape-0 reads into VGPRs: blocks of `waves` (4, 8 or 16) waves,
 // iters x 8 loads of 1 KiB per wave (src as for bqc_dma_l2); cyc: blocks
 // long longs, fold: blocks * waves * 64 ints.
 int bqc_vmem_l2(int waves, const int8_t* src, int stride, int rows, int blocks, int iters,
@@ -422,6 +422,8 @@ int bqc_vmem_l2(int waves, const int8_t* src, int stride, int rows, int blocks, 
     hipLaunchKernelGGL(k_vmem_l2<4>, dim3(blocks), dim3(256), 0, st, src, stride, rows, iters, cyc, fold);
   else if (waves == 8)
     hipLaunchKernelGGL(k_vmem_l2<8>, dim3(blocks), dim3(512), 0, st, src, stride, rows, iters, cyc, fold);
+  else if (waves == 16)
+    hipLaunchKernelGGL(k_vmem_l2<16>, dim3(blocks), dim3(1024), 0, st, src, stride, rows, iters, cyc, fold);
   else
     return (int)hipErrorInvalidValue;
   return (int)hipGetLastError();
