@@ -155,29 +155,42 @@ __device__ inline uint64_t cand_key(float lg, int e) {
 
 __device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-// One step of a wave max over 64-bit keys through DPP lane moves (a VALU
-// op, no LDS round trip).  Rows outside ROW_MASK keep their own value.
+// One step of a wave max through a DPP lane move (a VALU op, no LDS round
+// trip).  Rows outside ROW_MASK keep their own value.
 template <int CTRL, int ROW_MASK>
-__device__ inline uint64_t dpp_max_step(uint64_t v) {
-  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
-  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
-  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
-  return umax64(v, ((uint64_t)ohi << 32) | olo);
+__device__ inline uint32_t dpp_max_step32(uint32_t v) {
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+  return v > o ? v : o;
 }
 
 // Wave-uniform maximum: quad swaps (xor 1, xor 2), half-row and row
 // mirrors leave every lane of a 16-lane row with the row maximum; the
 // row_bcast15 / row_bcast31 steps carry it up so lane 63 holds the wave's.
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-  v = dpp_max_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-  v = dpp_max_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-  v = dpp_max_step<0x141, 0xF>(v);  // row_half_mirror
-  v = dpp_max_step<0x140, 0xF>(v);  // row_mirror
-  v = dpp_max_step<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
-  v = dpp_max_step<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+  v = dpp_max_step32<0xB1, 0xF>(v);
+  v = dpp_max_step32<0x4E, 0xF>(v);
+  v = dpp_max_step32<0x141, 0xF>(v);
+  v = dpp_max_step32<0x140, 0xF>(v);
+  v = dpp_max_step32<0x142, 0xA>(v);
+  v = dpp_max_step32<0x143, 0xC>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The wave maximum of 64-bit candidate keys (0 when every key is 0):
+// the maximum of the high words first (32-bit), then the low word of the
+// one lane holding it, or -- only when several lanes tie on the high word
+// -- the maximum of those lanes' low words.
+__device__ inline uint64_t wave_max_key(uint64_t v) {
+  const uint32_t hi = (uint32_t)(v >> 32), lo = (uint32_t)v;
+  const uint32_t m = wave_max_u32(hi);
+  if (m == 0u) return 0ull;  // no candidate left anywhere (uniform)
+  const uint64_t tie = __ballot(hi == m);
+  uint32_t l;
+  if (__popcll(tie) == 1)  // uniform
+    l = (uint32_t)__builtin_amdgcn_readlane((int)lo, (int)__builtin_ctzll(tie));
+  else
+    l = wave_max_u32(hi == m ? lo : 0u);
+  return ((uint64_t)m << 32) | l;
 }
 
 // TPW tokens' top_k routes on one wave, their candidate chains interleaved:
@@ -212,19 +225,18 @@ __device__ inline void topk_tokens(const float* const (&rows)[TPW],
 #pragma unroll
     for (int q = 1; q < NE; ++q) local[i] = umax64(local[i], key[i][q]);
   }
-  float mx[TPW], sum[TPW], my_ev[TPW];
+  // lane k keeps route k's logit and expert; the softmax follows the loop
+  float my_lg[TPW], sum[TPW], my_ev[TPW];
   int my_e[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    mx[i] = 0.0f;
-    sum[i] = 0.0f;
-    my_ev[i] = 0.0f;
+    my_lg[i] = kRouterSentinel;
     my_e[i] = 0;
   }
   for (int k = 0; k < top_k; ++k) {
     uint64_t best[TPW];
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) best[i] = wave_max_u64(local[i]);
+    for (int i = 0; i < TPW; ++i) best[i] = wave_max_key(local[i]);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       float lg = kRouterSentinel;
@@ -240,16 +252,24 @@ __device__ inline void topk_tokens(const float* const (&rows)[TPW],
 #pragma unroll
         for (int q = 1; q < NE; ++q) local[i] = umax64(local[i], key[i][q]);
       }
-      // RouterMergeKernel (:276-293): max = merged[0].logit, exp of the
-      // difference, sum in slot order
-      if (k == 0) mx[i] = lg;
-      const float ev = fast_exp_softmax_biased(lg - mx[i]);
-      sum[i] = sum[i] + ev;
       if (lane == k) {
-        my_ev[i] = ev;
+        my_lg[i] = lg;
         my_e[i] = e;
       }
     }
+  }
+  // RouterMergeKernel (:276-293): max = merged[0].logit, exp of the
+  // difference, sum in slot order -- every route's exp at once (lane k),
+  // then the sum over k in order
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_lg[i]), 0));
+    const float ev = fast_exp_softmax_biased(my_lg[i] - mx);
+    float s = 0.0f;
+    for (int k = 0; k < top_k; ++k)
+      s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), k));
+    sum[i] = s;
+    my_ev[i] = lane < top_k ? ev : 0.0f;
   }
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
