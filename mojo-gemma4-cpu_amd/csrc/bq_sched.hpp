@@ -14,9 +14,9 @@ constexpr int kSchedSmallSlots = 1024;
 // Called by all kSchedSmallSlots threads of the workgroup; thread tid owns
 // route slot tid = token * top_k + k, with e its expert (0..E-1, or -1 for
 // no slot) and w its weight; threads tid >= slots hold no slot, so only the
-// first ceil(slots / 64) waves take part in the counts.  A slot's record is its expert's offset plus
-// the number of earlier slots routed to the same expert -- the (expert,
-// token, k) order.  Earlier slots of the same wave are counted from the
+// first ceil(slots / 64) waves take part in the counts.  A slot's record is
+// its expert's offset plus the number of earlier slots routed to the same
+// expert -- the (expert, token, k) order.  Earlier slots of the same wave are counted from the
 // wave's experts staged in LDS (each lane compares the lanes below it: no
 // serial pass per distinct expert); earlier waves' slots through an
 // exclusive prefix over the waves' per-expert counts (s_wc, LDS atomics),
