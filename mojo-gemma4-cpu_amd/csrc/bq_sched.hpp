@@ -16,11 +16,12 @@ constexpr int kSchedSmallSlots = 1024;
 // no slot) and w its weight; threads tid >= slots hold no slot, so only the
 // first ceil(slots / 64) waves take part in the counts.  A slot's record is
 // its expert's offset plus the number of earlier slots routed to the same
-// expert -- the (expert, token, k) order.  Earlier slots of the same wave are counted from the
-// wave's experts staged in LDS (each lane compares the lanes below it: no
-// serial pass per distinct expert); earlier waves' slots through an
-// exclusive prefix over the waves' per-expert counts (s_wc, LDS atomics),
-// and the experts' offsets through a scan of their totals (s_cnt).
+// expert -- the (expert, token, k) order.  Earlier slots of the same wave
+// are counted from the wave's experts staged in LDS (each lane compares the
+// lanes below it: no serial pass per distinct expert); earlier waves' slots
+// through an exclusive prefix over the waves' per-expert counts (s_wc, LDS
+// atomics), and the experts' offsets through a scan of their totals
+// (s_cnt).
 constexpr int kSchedWavesSmall = kSchedSmallSlots / 64;
 
 __device__ inline void schedule_small(int e, float w, int top_k, int E, int slots,
