@@ -679,16 +679,6 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
   };
   load_ep4(first);
 
-  // LDS byte offset of this lane's activation operand in subtile 0 of stage
-  // 0, for even (a_base[0]) and odd (a_base[1]) k-steps: record lane % 16 of
-  // the subtile, 16-byte chunk (ks & 1) * 4 + lane / 16 under the block
-  // swizzle.  The swizzle term (chunk ^ row ^ block parity) is the same for
-  // every subtile (two whole 8-row blocks), so subtile s adds s * 2048 and
-  // stage st adds st * FA * 1024 -- constants, not per-k-step registers.
-  const int lr = lane & 15, lb = lr >> 3, lrow = lr & 7;
-  const int a_base[2] = {lb * 1024 + lrow * 128 + (((lane >> 4) ^ lrow ^ lb) * 16),
-                         lb * 1024 + lrow * 128 + (((4 + (lane >> 4)) ^ lrow ^ lb) * 16)};
-
   int cur_mt = -1, lds_mt = -1, r0 = 0, r1 = 0, nmi = 0;
   const uint32_t a_lds = lds_addr(abuf);
   for (int item = first; item < last; ++item) {
@@ -776,14 +766,15 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
       if (active) {  // wave-uniform
 #pragma unroll
         for (int ks = 0; ks < KMAX; ++ks) {
-          const int st = ks >> 1;
+          const int st = ks >> 1, c = (ks & 1) * 4 + (lane >> 4);
           v4i a[2];
           float adv[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
+            const int m = (mp + h) * 16 + (lane & 15), bb = m >> 3, r = m & 7;
             a[h] = *reinterpret_cast<const v4i*>(
-                &abuf[mp * 2048 + a_base[ks & 1] + st * FA * 1024 + h * 2048]);
-            adv[h] = sa[ks * BM + (mp + h) * 16 + lr];
+                &abuf[(st * FA + bb) * 1024 + r * 128 + ((c ^ r ^ (bb & 1)) * 16)]);
+            adv[h] = sa[ks * BM + m];
           }
           v4i t[2][NI];
 #pragma unroll
