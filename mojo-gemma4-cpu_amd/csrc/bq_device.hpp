@@ -419,35 +419,73 @@ __device__ inline v16i mfma32x32x32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave by DPP adds: row_shr 1,
+// 2, 4, 8 within each 16-lane row, then row_bcast15 / row_bcast31 carry the
+// row totals up (lanes a DPP move does not reach add 0).
+__device__ inline int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
 // Map a global m-tile index (BM records per tile, tiles of consecutive
 // experts concatenated) to (expert, first record, end record).  Every lane of
-// the calling wave gets the same answer.
+// the calling wave gets the same answer.  Up to 256 experts every lane's
+// expert offsets are requested at once (one memory round trip, not one per
+// 64 experts) and the tile counts are prefix-summed with DPP adds.
 __device__ inline bool find_mtile(const int32_t* __restrict__ eo, int E, int BM, int mt,
                                   int max_routes, int& e, int& r0, int& r1) {
   const int lane = lane_id();
+  if (E <= 0) return false;
+  if (E <= 256) {
+    int lo[4], hi[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ex = min(lane + 64 * q, E - 1);  // lanes past E read a valid offset, count 0
+      lo[q] = eo[ex];
+      hi[q] = eo[ex + 1];
+    }
+    int carry = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (64 * q >= E) break;  // uniform
+      const int tiles = lane + 64 * q < E ? (hi[q] - lo[q] + BM - 1) / BM : 0;
+      const int inc = wave_incl_scan(tiles), excl = inc - tiles;
+      const bool hit = tiles > 0 && mt >= carry + excl && mt < carry + inc;
+      const unsigned long long m = __ballot(hit);
+      if (m) {  // uniform
+        const int l = __ffsll((long long)m) - 1;
+        e = 64 * q + l;
+        const int local = mt - carry - __builtin_amdgcn_readlane(excl, l);
+        r0 = __builtin_amdgcn_readlane(lo[q], l) + local * BM;
+        r1 = min(min(__builtin_amdgcn_readlane(hi[q], l), r0 + BM), max_routes);
+        return r0 < r1;
+      }
+      carry += __builtin_amdgcn_readlane(inc, 63);
+    }
+    return false;
+  }
   int carry = 0;
   for (int base = 0; base < E; base += 64) {
     const int ex = base + lane;
     int tiles = 0;
     if (ex < E) tiles = (eo[ex + 1] - eo[ex] + BM - 1) / BM;
-    int inc = tiles;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += y;
-    }
-    const int excl = inc - tiles;
+    const int inc = wave_incl_scan(tiles), excl = inc - tiles;
     const bool hit = tiles > 0 && mt >= carry + excl && mt < carry + inc;
     const unsigned long long m = __ballot(hit);
     if (m) {
       const int l = __ffsll((long long)m) - 1;
       e = base + l;
-      const int local = mt - carry - __shfl(excl, l, kWave);
+      const int local = mt - carry - __builtin_amdgcn_readlane(excl, l);
       r0 = eo[e] + local * BM;
       r1 = min(min(eo[e + 1], r0 + BM), max_routes);
       return r0 < r1;
     }
-    carry += __shfl(inc, 63, kWave);
+    carry += __builtin_amdgcn_readlane(inc, 63);
   }
   return false;
 }
