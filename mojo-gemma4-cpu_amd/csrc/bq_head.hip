@@ -566,12 +566,7 @@ __device__ inline void row_thr_lo(const SelArgs& a, int r, int want, uint32_t& t
   // ties (key == threshold) in the chunks before each chunk: exclusive scan
   // over chunks (nc <= 256: thread c holds chunk c)
   const int e = tid < a.nc ? (int)a.hist2[((size_t)r * a.nc + tid) * 256 + lb] : 0;
-  int incl = e;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += u;
-  }
+  int incl = wave_incl_scan(e);
   if (lane == 63) tmp[wave] = incl;
   __syncthreads();
   int before = 0;
@@ -613,12 +608,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_collect(SelArgs a) {
   int n_eq = 0;
 #pragma unroll
   for (int q = 0; q < 16; ++q) n_eq += (ok && k[q] == t) ? 1 : 0;
-  int inc_e = n_eq;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(inc_e, o, 64);
-    if (lane >= o) inc_e += u;
-  }
+  int inc_e = wave_incl_scan(n_eq);
   if (lane == 63) tmp_e[wave] = inc_e;
   __syncthreads();
   int be = 0;
@@ -634,12 +624,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_sel_collect(SelArgs a) {
   }
   // one global atomic per workgroup reserves the chunk's slots
   const int n_sel = __popc(sel);
-  int inc_s = n_sel;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(inc_s, o, 64);
-    if (lane >= o) inc_s += u;
-  }
+  int inc_s = wave_incl_scan(n_sel);
   if (lane == 63) tmp_s[wave] = inc_s;
   __syncthreads();
   if (tid == 0) {

@@ -92,12 +92,7 @@ __global__ __launch_bounds__(kSchedThreads) void k_build_schedule(
       int v[4], sum = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) { v[i] = cnt[lane * 4 + i]; sum += v[i]; }
-      int inc = sum;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(inc, o, kWave);
-        if (lane >= o) inc += y;
-      }
+      int inc = wave_incl_scan(sum);
       int ex = inc - sum;
 #pragma unroll
       for (int i = 0; i < 4; ++i) { cnt[lane * 4 + i] = ex; ex += v[i]; }
@@ -373,12 +368,7 @@ __global__ __launch_bounds__(256) void k_combine(
       while (lo + run < hi0 && run < kMaxTopK && routes[lo + run].token == t) ++run;
     }
     // exclusive prefix of the run lengths over this chunk's experts
-    int inc = run;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += v;
-    }
+    int inc = wave_incl_scan(run);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
     int base = cnt, total = 0;

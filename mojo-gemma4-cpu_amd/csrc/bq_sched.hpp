@@ -70,12 +70,7 @@ __device__ inline void schedule_small(int e, float w, int top_k, int E, int slot
       v[j] = ex < E ? s_cnt[ex] : 0;
       sum += v[j];
     }
-    int inc = sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += y;
-    }
+    int inc = wave_incl_scan(sum);
     int off = inc - sum;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

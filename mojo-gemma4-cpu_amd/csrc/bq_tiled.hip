@@ -611,12 +611,7 @@ __global__ __launch_bounds__(512) void k_down_breg(TiledArgs args) {
     for (int base = 0; base < E; base += 64) {
       const int ex = base + lane;
       const int tiles = ex < E ? max(0, (args.eo[ex + 1] - args.eo[ex] + BM - 1) / BM) : 0;
-      int inc = tiles;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(inc, o, kWave);
-        if (lane >= o) inc += y;
-      }
+      int inc = wave_incl_scan(tiles);
       if (ex < E) s_tp[ex] = carry + inc - tiles;
       carry += __shfl(inc, 63, kWave);
     }
