@@ -59,13 +59,20 @@ __device__ inline int64_t paged_slot(const int32_t* __restrict__ rows, int shift
 
 // sum over the 16 lanes of each aligned 16-lane group in the order of a
 // SIMD[f32, 16].reduce_add (halving tree: j + 8, j + 4, j + 2, j + 1); the
-// result is broadcast to the group
+// result is broadcast to the group.  Lane j of each row adds lane j + H of
+// the same row by a DPP row shift (the lanes whose partner falls outside the
+// row compute values no one reads), so lane 0 of each row ends with the
+// tree's sum; readlane brings the four row sums back.
 __device__ inline float tree16(float v) {
-  v = v + __shfl_down(v, 8, 16);
-  v = v + __shfl_down(v, 4, 16);
-  v = v + __shfl_down(v, 2, 16);
-  v = v + __shfl_down(v, 1, 16);
-  return __shfl(v, lane_id() & ~15, kWave);
+  v = v + row_shl<8>(v);
+  v = v + row_shl<4>(v);
+  v = v + row_shl<2>(v);
+  v = v + row_shl<1>(v);
+  const int x = __float_as_int(v);
+  const int s0 = __builtin_amdgcn_readlane(x, 0), s1 = __builtin_amdgcn_readlane(x, 16);
+  const int s2 = __builtin_amdgcn_readlane(x, 32), s3 = __builtin_amdgcn_readlane(x, 48);
+  const int row = lane_id() >> 4;
+  return __int_as_float(row == 0 ? s0 : row == 1 ? s1 : row == 2 ? s2 : s3);
 }
 
 __device__ inline float max87(float x) { return x > -87.0f ? x : -87.0f; }

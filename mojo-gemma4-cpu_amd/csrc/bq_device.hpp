@@ -202,9 +202,15 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
-// max over aligned groups of `width` lanes (width a power of two <= 64)
+// max over aligned groups of `width` lanes (width a power of two <= 64), on
+// the VALU lane moves of xlane_partner (defined below)
 __device__ inline float group_max(float v, int width) {
-  for (int o = width >> 1; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  if (width > 32) v = fmaxf(v, xlane_partner<32>(v));
+  if (width > 16) v = fmaxf(v, xlane_partner<16>(v));
+  if (width > 8) v = fmaxf(v, xlane_partner<8>(v));
+  if (width > 4) v = fmaxf(v, xlane_partner<4>(v));
+  if (width > 2) v = fmaxf(v, xlane_partner<2>(v));
+  if (width > 1) v = fmaxf(v, xlane_partner<1>(v));
   return v;
 }
 
