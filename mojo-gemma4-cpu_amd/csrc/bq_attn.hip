@@ -140,16 +140,25 @@ __global__ __launch_bounds__(256) void k_attn_prep(PrepArgs a) {
 
   // head_inv_rms (head_prep.mojo:9-16): chain k of 16 takes x[16i + k] in i
   // order (product first, then fma), then the 16-lane tree.  x[16i + k] is
-  // value i / 4 of lane 16 * (i % 4) + k.
-  const int k = lane & 15;
-  float ssq = 0.0f;
+  // value i / 4 of lane 16 * (i % 4) + k: the row moves of row_to_row0 bring
+  // it to lane k of row 0, which runs the chains (the other rows' sums are
+  // not used), and lane 0 ends the tree.
+  float ssq = v[0] * v[0];
 #pragma unroll
-  for (int i = 0; i < HD / 16; ++i) {
-    const float x = __shfl(v[i / 4], 16 * (i % 4) + k, kWave);
-    ssq = i == 0 ? x * x : fmaf(x, x, ssq);
+  for (int i4 = 0; i4 < R; ++i4) {
+    if (i4 > 0) ssq = fmaf(v[i4], v[i4], ssq);
+    const float x1 = row_to_row0<1>(v[i4]), x2 = row_to_row0<2>(v[i4]);
+    const float x3 = row_to_row0<3>(v[i4]);
+    ssq = fmaf(x1, x1, ssq);
+    ssq = fmaf(x2, x2, ssq);
+    ssq = fmaf(x3, x3, ssq);
   }
-  ssq = tree16(ssq);
-  const float inv = a.sqrt_n / __builtin_sqrtf(__shfl(ssq, 0, kWave) + a.n_eps);
+  ssq = ssq + row_shl<8>(ssq);
+  ssq = ssq + row_shl<4>(ssq);
+  ssq = ssq + row_shl<2>(ssq);
+  ssq = ssq + row_shl<1>(ssq);
+  ssq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssq), 0));
+  const float inv = a.sqrt_n / __builtin_sqrtf(ssq + a.n_eps);
 
   const uint16_t* gamma = is_q ? a.q_norm : a.k_norm;
 #pragma unroll
@@ -204,8 +213,7 @@ __global__ __launch_bounds__(256) void k_attn_prep(PrepArgs a) {
     qs += c;
   }
   if (is_q) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) qs += __shfl_xor(qs, o, kWave);
+    qs = __builtin_amdgcn_readlane(wave_incl_scan(qs), 63);  // integer sum: exact
     if (lane == 0) {
       a.qi_bias[(int64_t)tok * a.num_q + h] = (float)qs * 128.0f;
       a.f_q[(int64_t)tok * a.num_q + h] = amax;
