@@ -209,10 +209,29 @@ def bench_gemv(bq, torch, steps, warmup, reps=64):
                 s_fused=s_fused, rd=rd, codes=codes, scales=scales, xq=xq, sa=sa)
 
 
+def _env_int(name):
+    try:
+        return int(os.environ.get(name, "0"))
+    except ValueError:
+        return 0
+
+
+def gemv_kernel():
+    """(kernel name, waves per workgroup) of the decode GEMV (M = 1, per-row,
+    K = 4096) as the library's launcher picks it: k_gemv_m1 with
+    BQ_GEMV_M1_WAVES (2, 4, 8; default 4), or k_linear_skinny when
+    BQ_GEMV_WAVES (4, 8, 16) is set."""
+    g = _env_int("BQ_GEMV_WAVES")
+    if g:
+        w = 16 if g >= 16 else 4 if g <= 4 else 8
+        return f"k_linear_skinny<{w}, false, {64 // w}>", w
+    m1 = _env_int("BQ_GEMV_M1_WAVES") or 4
+    w = 2 if m1 <= 2 else 8 if m1 >= 8 else 4
+    return f"k_gemv_m1<{w}, {64 // w}>", w
+
+
 def gemv_waves():
-    """Waves per workgroup of the decode GEMV: the library's default (16) or
-    BQ_GEMV_WAVES when that selects 8."""
-    return 8 if os.environ.get("BQ_GEMV_WAVES") == "8" else 16
+    return gemv_kernel()[1]
 
 
 def bench_stream(torch, bufs, tiles, K64, steps, warmup):
@@ -1174,10 +1193,11 @@ def calib_copy(torch):
 
 
 def launch_histogram(path, reps=64):
-    """Per-launch durations of k_linear_skinny and k_stream_read from a
-    rocprofv3 kernel trace of `bench.py --workload gemv`: for each kernel the
-    longest run of back-to-back dispatches of it alone (the pure GEMV graph
-    and the streaming-read graph, eager warm calls included), its
+    """Per-launch durations of the GEMV (k_gemv_m1 or k_linear_skinny) and
+    k_stream_read from a rocprofv3 kernel trace of `bench.py --workload gemv`:
+    for each kernel the longest run of back-to-back dispatches of it alone
+    (the pure GEMV graph and the streaming-read graph, eager warm calls
+    included), its
     percentiles, a histogram, the spread of per-replica medians (dispatch i
     of a run reads replica i mod 64) and the position of the slow launches
     inside each 64-launch replay."""
@@ -1190,7 +1210,7 @@ def launch_histogram(path, reps=64):
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
     rows.sort()
     out = []
-    for key in ("k_linear_skinny", "k_stream_read"):
+    for key in ("k_gemv_m1", "k_linear_skinny", "k_stream_read"):
         best, cur = [], []
         for st, en, name in rows:
             if key in name:
@@ -1317,7 +1337,7 @@ def main():
                                        f"{len(smp.ms)} graph replays of 64 launches; "
                                        "measured_peak = the same-launch-shape streaming read "
                                        "of the same replicas (p50)"})
-        line["gemv_detail"] = {"kernel": f"k_linear_skinny<{gemv_waves()}, false, {64 // gemv_waves()}>",
+        line["gemv_detail"] = {"kernel": gemv_kernel()[0],
                                "alg_bytes_per_launch": gv["alg_bytes"],
                                "best_GBs": round(gv["gbs_min"], 1), **smp.summary(),
                                "norm_quant": gv["s_nq"].summary(),

@@ -4,11 +4,11 @@
 //
 // bqc_stream_read: the decode GEMV's launch shape and read pattern with the
 //   arithmetic taken out.  One workgroup per 16-row tile of a tile16x64
-//   weight (tile t at byte t * K64 * 1024), W = 8 or 16 waves splitting the
-//   K64 fragments of 1 KiB evenly, each lane loading its 16 bytes of every
+//   weight (tile t at byte t * K64 * 1024), W = 2, 4, 8 or 16 waves splitting
+//   the K64 fragments of 1 KiB evenly, each lane loading its 16 bytes of every
 //   fragment of its slice, the whole slice requested at once with
-//   non-temporal loads (k_linear_skinny<16, false, 4> and <8, false, 8> do
-//   exactly this for K <= 4096).  Each wave's bytes are XOR-folded into one 16-byte value per
+//   non-temporal loads (k_gemv_m1<2, 32> and <4, 16>, k_linear_skinny<16,
+//   false, 4> and <8, false, 8> do exactly this for K <= 4096).  Each wave's bytes are XOR-folded into one 16-byte value per
 //   lane, the waves' partial tiles reduced through LDS as the GEMV reduces its
 //   int32 tiles, and 16 uint16 written per workgroup, the GEMV's 16 bf16
 //   outputs.  Its per-launch time is the
@@ -290,15 +290,19 @@ extern "C" {
 // GEMV's one-shot shape; K64 = 0 launches the same grid reading nothing (the
 // fixed cost of a launch).  Returns a hipError_t.
 int bqc_stream_read(const int8_t* w, int tiles, int K64, int waves, uint16_t* out, void* stream) {
-  if (!w || !out || tiles <= 0 || K64 < 0 || K64 > 64 || (waves != 8 && waves != 16))
+  if (!w || !out || tiles <= 0 || K64 < 0 || K64 > 64 ||
+      (waves != 2 && waves != 4 && waves != 8 && waves != 16))
     return (int)hipErrorInvalidValue;
   if (reinterpret_cast<uintptr_t>(w) & 15u) return (int)hipErrorInvalidValue;
+  const hipStream_t st = (hipStream_t)stream;
   if (waves == 16)
-    hipLaunchKernelGGL((k_stream_read<16, 4>), dim3(tiles), dim3(16 * 64), 0, (hipStream_t)stream,
-                       w, K64, out);
+    hipLaunchKernelGGL((k_stream_read<16, 4>), dim3(tiles), dim3(16 * 64), 0, st, w, K64, out);
+  else if (waves == 8)
+    hipLaunchKernelGGL((k_stream_read<8, 8>), dim3(tiles), dim3(8 * 64), 0, st, w, K64, out);
+  else if (waves == 4)
+    hipLaunchKernelGGL((k_stream_read<4, 16>), dim3(tiles), dim3(4 * 64), 0, st, w, K64, out);
   else
-    hipLaunchKernelGGL((k_stream_read<8, 8>), dim3(tiles), dim3(8 * 64), 0, (hipStream_t)stream,
-                       w, K64, out);
+    hipLaunchKernelGGL((k_stream_read<2, 32>), dim3(tiles), dim3(2 * 64), 0, st, w, K64, out);
   return (int)hipGetLastError();
 }
 

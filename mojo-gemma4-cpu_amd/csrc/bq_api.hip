@@ -93,6 +93,7 @@ void tune_init(int device) {
   std::lock_guard<std::mutex> lock(g_tune_mu);
   Tune t{};
   t.gemv_waves = env_int("BQ_GEMV_WAVES");
+  t.gemv_m1_waves = env_int("BQ_GEMV_M1_WAVES");
   t.tile_bm = env_int("BQ_TILE_BM");
   t.tile_bn = env_int("BQ_TILE_BN");
   t.ring = env_int("BQ_RING");

@@ -191,6 +191,99 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// M = 1, per-row (the decode GEMV)
+// ---------------------------------------------------------------------------
+// f(std::integral_constant<int, I>{}) for I = I0 .. I1 - 1, in order
+template <int I0, int I1, typename F>
+__device__ inline void static_for(F&& f) {
+  if constexpr (I0 < I1) {
+    f(std::integral_constant<int, I0>{});
+    static_for<I0 + 1, I1>(f);
+  }
+}
+
+// the four dwords of x as lane (lane + R) of the same 16-lane row holds them
+// (DPP row_shl:R); R = 0 is x itself
+template <int R>
+__device__ inline v4i row_shl_v4(const v4i& x) {
+  if constexpr (R == 0) {
+    return x;
+  } else {
+    v4i r;
+    r.x = __builtin_amdgcn_update_dpp(x.x, x.x, 0x100 + R, 0xF, 0xF, false);
+    r.y = __builtin_amdgcn_update_dpp(x.y, x.y, 0x100 + R, 0xF, 0xF, false);
+    r.z = __builtin_amdgcn_update_dpp(x.z, x.z, 0x100 + R, 0xF, 0xF, false);
+    r.w = __builtin_amdgcn_update_dpp(x.w, x.w, 0x100 + R, 0xF, 0xF, false);
+    return r;
+  }
+}
+
+// One workgroup of WAVES waves per 16-row n-tile; wave w owns k-steps
+// [w*per, (w+1)*per), per = ceil(K/64 / WAVES) <= U.  At M = 1 only row 0 of
+// the MFMA's A operand is stored, and row 0 is lane 16c's 16-byte chunk c of
+// the k-step.  So one 16-byte load per lane brings 16 k-steps' activation
+// (lane 16c + r: chunk c of k-step r), and a DPP row_shl:r moves k-step r's
+// chunks to lanes 16c when it is multiplied (the other rows are never
+// stored).  The activation and the scales are requested before the weights;
+// loads return in issue order, so the MFMA of k-step u waits only for
+// weight fragments 0..u and the products overlap the stream.  NC independent
+// chains of exact int32 sums: after the last fragment lands one MFMA, three
+// adds and the cross-wave sum remain.  Same y = (f32(acc) * (sa*(1/127))) *
+// ws[n] epilogue as k_linear_skinny (gemm.mojo:133-142).
+// (one workgroup per CU at the model's widths: waves_per_eu(1, 2) lets the
+// compiler hold every fragment in registers instead of sinking the loads)
+template <int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_gemv_m1(LinArgs args) {
+  constexpr int NC = U >= 4 ? 4 : U;  // accumulator chains
+  constexpr int NA = (U + 15) / 16;   // activation loads per lane
+  __shared__ int part[WAVES * 16];
+  int nt;
+  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
+  const int K64 = args.K >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int per = (K64 + WAVES - 1) / WAVES;
+  const int kt0 = min(K64, wave * per), kt1 = min(K64, kt0 + per);
+  const int last = max(kt1 - 1, 0);  // loads past the wave's range read this k-step
+  v4i xa[NA];
+#pragma unroll
+  for (int g = 0; g < NA; ++g)
+    xa[g] = ld16(args.act + (size_t)min(kt0 + 16 * g + (lane & 15), last) * 64 + (lane >> 4) * 16);
+  const float ews = seg.ws[nt * 16 + (lane & 15)];
+  const float ead = args.sa[0] * kInv127;
+  asm volatile("" ::: "memory");  // the weight loads go out after these
+  const int8_t* wb = seg.w + (size_t)nt * K64 * 1024 + lane * 16;
+  v4i bf[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    bf[u] = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(wb + (size_t)min(kt0 + u, last) * 1024));
+  asm volatile("" ::: "memory");  // all of them before any product
+  const v4i zero = {0, 0, 0, 0};
+  v4i c[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) c[j] = zero;
+  static_for<0, U>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    const v4i a = kt0 + u < kt1 ? row_shl_v4<u % 16>(xa[u / 16]) : zero;
+    c[u % NC] = mfma16x16x64(a, bf[u], c[u % NC]);
+  });
+  int s = c[0].x;
+#pragma unroll
+  for (int j = 1; j < NC; ++j) s += c[j].x;  // row 0, column lane (lanes 0..15)
+  if (lane < 16) part[wave * 16 + lane] = s;
+  __syncthreads();
+  if (threadIdx.x >= 16) return;
+  int acc = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) acc += part[w * 16 + lane];
+  const float y = (float)acc * ead * ews;
+  const int n = nt * 16 + lane;
+  seg.out[n] = f32_to_bf16(y);
+  if (seg.out_f32) seg.out_f32[n] = y;
+}
+
+// ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
 hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
@@ -198,6 +291,16 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
   if (a.M <= 16) {
     int tiles = 0;
     for (int q = 0; q < a.nseg; ++q) tiles += a.seg[q].n / 16;
+    // M = 1 per-row up to K = 4096: k_gemv_m1 (BQ_GEMV_WAVES sends it to the
+    // general kernel below)
+    if (a.M == 1 && !per_block && !tune().gemv_waves && a.K <= 4096) {
+      const int w1 = tune().gemv_m1_waves ? tune().gemv_m1_waves : 4;
+      dim3 g1(tiles);
+      if (w1 <= 2) hipLaunchKernelGGL((k_gemv_m1<2, 32>), g1, dim3(128), 0, st, a);
+      else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8>), g1, dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((k_gemv_m1<4, 16>), g1, dim3(256), 0, st, a);
+      return hipGetLastError();
+    }
     // 16 waves split K so that each wave's whole slice (<= 4 fragments for
     // K <= 4096) is requested at once: the full weight is in flight within
     // the first memory latency.  K = N = 4096, M = 1: 4.86 -> 4.72 us against

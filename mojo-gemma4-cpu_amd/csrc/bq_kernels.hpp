@@ -13,7 +13,9 @@ namespace bq {
 // and the device's compute-unit count, read once: at bq_init, or at the
 // first launch of a process that never called it.
 struct Tune {
-  int gemv_waves;   // BQ_GEMV_WAVES: waves per decode-GEMV workgroup (4, 8, 16; default 16)
+  int gemv_waves;   // BQ_GEMV_WAVES: waves per workgroup of the general M <= 16 kernel (4, 8, 16;
+                   // default 16); set, it also takes M = 1 per-row from k_gemv_m1
+  int gemv_m1_waves;  // BQ_GEMV_M1_WAVES: waves per k_gemv_m1 workgroup (2, 4, 8)
   int tile_bm;      // BQ_TILE_BM: rows per tiled prefill tile (32, 64, 128)
   int tile_bn;      // BQ_TILE_BN: columns per tiled tile (128, 256)
   int ring;         // BQ_RING: LDS ring stages of the tiled kernels

@@ -28,6 +28,38 @@ def test_gemv_waves_per_row(gpu, O, tune_env, waves, M, K):
     np.testing.assert_array_equal(host(ob), rb)
 
 
+@pytest.mark.parametrize("waves", [0, 2, 4, 8])
+@pytest.mark.parametrize("K", [64, 128, 192, 1024, 2816, 4096, 8192])
+def test_gemv_m1_waves(gpu, O, tune_env, waves, K):
+    """M = 1 per-row (k_gemv_m1 up to K = 4096, the general kernel above; 0 =
+    the default wave count): small K leaves some waves no k-step."""
+    tune_env(BQ_GEMV_M1_WAVES=waves)
+    N, B = 96, min(K, 128) if K % 128 == 0 else 64
+    q, s, W = weight(gpu, O, N, K, B, seed=8)
+    p, cs = O.pack_and_colsum(q)
+    x = O.synth_normal_bf16(9, 1.0, (1, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), B)
+    ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+    rb, rf = O.linear(xq, sa, p, s, cs, N)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
+@pytest.mark.parametrize("waves", [2, 4, 8])
+def test_gemv_m1_segments(gpu, O, tune_env, waves):
+    """q/k/v of one token in one k_gemv_m1 launch: each segment = the oracle."""
+    tune_env(BQ_GEMV_M1_WAVES=waves)
+    K = 2816
+    ws = [weight(gpu, O, n, K, 128, seed=sd) for n, sd in ((256, 1), (128, 2), (64, 3))]
+    x = O.synth_normal_bf16(10, 1.0, (1, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    outs = gpu.qkv(dev(xq), dev(sa), *(w[2] for w in ws))
+    for o, (q, s, _) in zip(outs, ws):
+        p, cs = O.pack_and_colsum(q)
+        rb, _ = O.linear(xq, sa, p, s, cs, q.shape[0])
+        np.testing.assert_array_equal(host(o), rb)
+
+
 @pytest.mark.parametrize("waves", [4, 8, 16])
 @pytest.mark.parametrize("M,K,B", [(1, 2112, 64), (16, 2112, 64), (16, 4096, 256),
                                    (7, 8192, 512), (16, 4096, 512), (2, 2816, 256)])
