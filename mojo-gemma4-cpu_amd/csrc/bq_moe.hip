@@ -241,8 +241,13 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 // holds columns 4 (L/16) .. +3 of a strip for record L % 16, so a drain
 // reads one activation scale per lane and a record's four y values are one
 // 16-byte store; the integer dot of each (record, column) is the same.
+// Up to two weight fragments per k-step slot the kernel fits 64 registers,
+// eight waves per SIMD (waves_per_eu(8)): a 16-token batch's 86 experts x 22
+// workgroups then fit in one round on 256 CUs instead of leaving ~100
+// workgroups for a second.
 template <int U, int NS>
-__global__ __launch_bounds__(256) void k_moe_down_skinny(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(U * NS <= 2 ? 8 : 1)))
+void k_moe_down_skinny(
     const int8_t* __restrict__ b_i8, const float* __restrict__ b_sa,
     const int32_t* __restrict__ eo, const Route* __restrict__ routes,
     const int8_t* __restrict__ w_d, const float* __restrict__ d_scale, float* __restrict__ y,
@@ -496,7 +501,7 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
-      // one k-step per register slot and two strips per wave (58 VGPRs, seven
+      // one k-step per register slot and two strips per wave (57 VGPRs, eight
       // waves per SIMD; BQ_DOWN_SKINNY): the 32-token layer 127.6 us against
       // 128.0-130.6 us for 1-4 k-steps x 1-4 strips
       const int ut = tune().down_skinny;
