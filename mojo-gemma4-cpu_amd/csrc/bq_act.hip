@@ -412,7 +412,9 @@ __global__ __launch_bounds__(512) void k_norm_quant_v8_row(
     int8_t* __restrict__ xq, float* __restrict__ sa, int hidden, float sqrt_n, float n_eps,
     float fwht_scale) {
   __shared__ float s_max[8];
-  const int lane = lane_id(), wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // (the launch's waves, from hidden rather than blockDim: reading blockDim
+  // would add the runtime's implicit arguments to the kernel's argument block)
+  const int lane = lane_id(), wave = threadIdx.x >> 6, nw = (hidden + 511) >> 9;
   const int t = blockIdx.x, nseg = hidden >> 7;
   const uint16_t* row = src + (size_t)t * hidden;
   const uint32_t* xr = reinterpret_cast<const uint32_t*>(row) + lane;
@@ -468,7 +470,7 @@ template <int LPB>
 __global__ __launch_bounds__(256) void k_block_quant(
     const uint16_t* __restrict__ src, int8_t* __restrict__ xq, float* __restrict__ sa,
     size_t nchunks, int apply_fwht, float fwht_scale) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
   const size_t c = i < nchunks ? i : nchunks - 1;  // whole LPB groups are in or out
   const int lane = lane_id();
   float v[8];

@@ -39,14 +39,36 @@ __device__ inline LinSeg pick_seg(const LinArgs& a, int nt_global, int& nt_local
   return r;
 }
 
+// A one-segment call's arguments: 64 bytes, one scalar-cache line (the
+// three-segment LinArgs spans three).  They are read before any address is
+// known, and a smaller argument block measured shorter launches (the decode
+// GEMV 4.545 -> 4.447 us).
+struct Seg1Args {
+  const int8_t* w;    // tile16x64 codes [n, K]
+  const float* ws;    // per-row weight scale [n]
+  const int8_t* act;  // int8 [M, K] row-major
+  const float* sa;    // per-row [M] or per-block [M, K/block] activation scales
+  uint16_t* out;      // bf16 [M, n]
+  float* out_f32;     // optional f32 [M, n]
+  int n, M, K, block;  // output rows; rows, K and the activation block
+};
+
+__device__ inline LinSeg seg_of(const LinArgs& a, int& nt) { return pick_seg(a, blockIdx.x, nt); }
+__device__ inline LinSeg seg_of(const Seg1Args& a, int& nt) {
+  LinSeg r;
+  r.w = a.w; r.ws = a.ws; r.out = a.out; r.out_f32 = a.out_f32; r.n = a.n; r.tile0 = 0;
+  nt = blockIdx.x;
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // skinny: M <= 16
 // ---------------------------------------------------------------------------
-template <int WAVES, bool PER_BLOCK, int U>
-__global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
+template <int WAVES, bool PER_BLOCK, int U, class Args>
+__global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(Args args) {
   extern __shared__ int lds[];  // per-row: WAVES*256 ints; per-block: nb*256 ints
   int nt;
-  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
+  const LinSeg seg = seg_of(args, nt);
   const int K = args.K, K64 = K >> 6, M = args.M;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int fpb = args.block >> 6;  // fragments per K block (power of two)
@@ -232,14 +254,14 @@ __device__ inline v4i row_shl_v4(const v4i& x) {
 // ws[n] epilogue as k_linear_skinny (gemm.mojo:133-142).
 // (one workgroup per CU at the model's widths: waves_per_eu(1, 2) lets the
 // compiler hold every fragment in registers instead of sinking the loads)
-template <int WAVES, int U>
+template <int WAVES, int U, class Args>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void k_gemv_m1(LinArgs args) {
+void k_gemv_m1(Args args) {
   constexpr int NC = U >= 4 ? 4 : U;  // accumulator chains
   constexpr int NA = (U + 15) / 16;   // activation loads per lane
   __shared__ int part[WAVES * 16];
   int nt;
-  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
+  const LinSeg seg = seg_of(args, nt);
   const int K64 = args.K >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int per = (K64 + WAVES - 1) / WAVES;
@@ -286,6 +308,11 @@ void k_gemv_m1(LinArgs args) {
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
+static Seg1Args seg1_args(const LinArgs& a) {
+  const LinSeg& s0 = a.seg[0];
+  return Seg1Args{s0.w, s0.ws, a.act, a.sa, s0.out, s0.out_f32, s0.n, a.M, a.K, a.block};
+}
+
 hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (a.M <= 16) {
@@ -296,9 +323,14 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     if (a.M == 1 && !per_block && !tune().gemv_waves && a.K <= 4096) {
       const int w1 = tune().gemv_m1_waves ? tune().gemv_m1_waves : 4;
       dim3 g1(tiles);
-      if (w1 <= 2) hipLaunchKernelGGL((k_gemv_m1<2, 32>), g1, dim3(128), 0, st, a);
-      else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8>), g1, dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((k_gemv_m1<4, 16>), g1, dim3(256), 0, st, a);
+      auto go = [&](const auto& args) {
+        using A = std::decay_t<decltype(args)>;
+        if (w1 <= 2) hipLaunchKernelGGL((k_gemv_m1<2, 32, A>), g1, dim3(128), 0, st, args);
+        else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8, A>), g1, dim3(512), 0, st, args);
+        else hipLaunchKernelGGL((k_gemv_m1<4, 16, A>), g1, dim3(256), 0, st, args);
+      };
+      if (a.nseg == 1) go(seg1_args(a));
+      else go(a);
       return hipGetLastError();
     }
     // 16 waves split K so that each wave's whole slice (<= 4 fragments for
@@ -309,19 +341,24 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     const int waves = tune().gemv_waves ? tune().gemv_waves : 16;
     const int nb = a.K / a.block;
     dim3 g(tiles);
-    if (waves >= 16) {
-      const size_t lds = (size_t)(per_block ? nb : 16) * 256 * sizeof(int);
-      if (per_block) hipLaunchKernelGGL((k_linear_skinny<16, true, 4>), g, dim3(1024), lds, st, a);
-      else hipLaunchKernelGGL((k_linear_skinny<16, false, 4>), g, dim3(1024), lds, st, a);
-    } else if (waves <= 4) {
-      const size_t lds = (size_t)(per_block ? nb : 4) * 256 * sizeof(int);
-      if (per_block) hipLaunchKernelGGL((k_linear_skinny<4, true, 16>), g, dim3(256), lds, st, a);
-      else hipLaunchKernelGGL((k_linear_skinny<4, false, 16>), g, dim3(256), lds, st, a);
-    } else {
-      const size_t lds = (size_t)(per_block ? nb : 8) * 256 * sizeof(int);
-      if (per_block) hipLaunchKernelGGL((k_linear_skinny<8, true, 8>), g, dim3(512), lds, st, a);
-      else hipLaunchKernelGGL((k_linear_skinny<8, false, 8>), g, dim3(512), lds, st, a);
-    }
+    auto go = [&](const auto& args) {
+      using A = std::decay_t<decltype(args)>;
+      if (waves >= 16) {
+        const size_t lds = (size_t)(per_block ? nb : 16) * 256 * sizeof(int);
+        if (per_block) hipLaunchKernelGGL((k_linear_skinny<16, true, 4, A>), g, dim3(1024), lds, st, args);
+        else hipLaunchKernelGGL((k_linear_skinny<16, false, 4, A>), g, dim3(1024), lds, st, args);
+      } else if (waves <= 4) {
+        const size_t lds = (size_t)(per_block ? nb : 4) * 256 * sizeof(int);
+        if (per_block) hipLaunchKernelGGL((k_linear_skinny<4, true, 16, A>), g, dim3(256), lds, st, args);
+        else hipLaunchKernelGGL((k_linear_skinny<4, false, 16, A>), g, dim3(256), lds, st, args);
+      } else {
+        const size_t lds = (size_t)(per_block ? nb : 8) * 256 * sizeof(int);
+        if (per_block) hipLaunchKernelGGL((k_linear_skinny<8, true, 8, A>), g, dim3(512), lds, st, args);
+        else hipLaunchKernelGGL((k_linear_skinny<8, false, 8, A>), g, dim3(512), lds, st, args);
+      }
+    };
+    if (a.nseg == 1) go(seg1_args(a));
+    else go(a);
     return hipGetLastError();
   }
   // prefer the largest M tile that still yields >= 256 workgroups (one per CU)

@@ -256,7 +256,7 @@ void k_moe_down_skinny(
   int e, r0, r1;
   if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;  // whole workgroup
   const int K = inter, K64 = K >> 6, fpb = block >> 6, nb = K / block;
-  for (int i = threadIdx.x; i < 16 * nb; i += blockDim.x) {
+  for (int i = threadIdx.x; i < 16 * nb; i += 256) {  // 256-thread blocks
     const int row = r0 + i / nb;
     s_sa[i] = b_sa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
   }

@@ -462,7 +462,9 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   __syncthreads();
   if (tid == 0) {
     __threadfence();
-    const unsigned last = gridDim.x - (unsigned)nq_blocks - 1u;
+    // top-k workgroups less one (from T, not gridDim: reading gridDim would
+    // add the runtime's implicit arguments to the kernel's argument block)
+    const unsigned last = (unsigned)((T + kPrepTopkTokens - 1) / kPrepTopkTokens) - 1u;
     s_last = atomicInc(done, last) == last;  // the last increment wraps the count to 0
     if (s_last) __threadfence();
   }
