@@ -53,6 +53,11 @@ struct Seg1Args {
   int n, M, K, block;  // output rows; rows, K and the activation block
 };
 
+static Seg1Args seg1_args(const LinArgs& a) {
+  const LinSeg& s0 = a.seg[0];
+  return Seg1Args{s0.w, s0.ws, a.act, a.sa, s0.out, s0.out_f32, s0.n, a.M, a.K, a.block};
+}
+
 __device__ inline LinSeg seg_of(const LinArgs& a, int& nt) { return pick_seg(a, blockIdx.x, nt); }
 __device__ inline LinSeg seg_of(const Seg1Args& a, int& nt) {
   LinSeg r;
@@ -308,11 +313,6 @@ void k_gemv_m1(Args args) {
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-static Seg1Args seg1_args(const LinArgs& a) {
-  const LinSeg& s0 = a.seg[0];
-  return Seg1Args{s0.w, s0.ws, a.act, a.sa, s0.out, s0.out_f32, s0.n, a.M, a.K, a.block};
-}
-
 hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (a.M <= 16) {
@@ -388,14 +388,14 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
 // V8 (FWHT block 128): wave w transforms values 512 w .. 512 w + 511 with 8
 // consecutive values per lane (nq_v8_transform), the codes one 8-byte store
 // per lane; otherwise the pair layout's SPW segments per wave.
-template <int NSEG, int SPW, bool V8 = false>
-__global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormArgs nq) {
+template <int NSEG, int SPW, bool V8, class Args>
+__global__ __launch_bounds__(512) void k_norm_linear_skinny(Args args, NormArgs nq) {
   constexpr int WAVES = 8, U = 8;
   __shared__ __attribute__((aligned(16))) int8_t s_x[64 * WAVES * U];  // the row's codes
   __shared__ int lds[WAVES * 256];
   __shared__ float s_f[WAVES];  // per-wave amax
   int nt;
-  const LinSeg seg = pick_seg(args, blockIdx.x, nt);
+  const LinSeg seg = seg_of(args, nt);
   const int K = args.K, K64 = K >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int per = (K64 + WAVES - 1) / WAVES;
@@ -518,17 +518,22 @@ static bool launch_norm_linear_fused(const LinArgs& a, const NormArgs& nq, hipSt
   const dim3 g(tiles), b(512);
   // FWHT block 128 (the model's): 8 values per lane for the transform
   // (16-byte aligned gain, 8-byte aligned codes)
-  if (nq.block == 128 && tune().nq_v8 && !(reinterpret_cast<uintptr_t>(nq.gamma) & 15u) &&
-      !(reinterpret_cast<uintptr_t>(nq.xq) & 7u)) {
-#define BQ_NL8(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_linear_skinny<N, 1, true>), g, b, 0, st, a, nq); return true; }
-    BQ_NL8(8) BQ_NL8(16) BQ_NL8(22) BQ_NL8(24) BQ_NL8(32)
+  const bool v8 = nq.block == 128 && tune().nq_v8 && !(reinterpret_cast<uintptr_t>(nq.gamma) & 15u) &&
+                  !(reinterpret_cast<uintptr_t>(nq.xq) & 7u);
+  auto go = [&](const auto& args) -> bool {
+    using A = std::decay_t<decltype(args)>;
+    if (v8) {
+#define BQ_NL8(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_linear_skinny<N, 1, true, A>), g, b, 0, st, args, nq); return true; }
+      BQ_NL8(8) BQ_NL8(16) BQ_NL8(22) BQ_NL8(24) BQ_NL8(32)
 #undef BQ_NL8
-  }
-#define BQ_NL(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_linear_skinny<N, S>), g, b, 0, st, a, nq); return true; }
-  BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
-  BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
+    }
+#define BQ_NL(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_linear_skinny<N, S, false, A>), g, b, 0, st, args, nq); return true; }
+    BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
+    BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
 #undef BQ_NL
-  return false;
+    return false;
+  };
+  return a.nseg == 1 ? go(seg1_args(a)) : go(a);
 }
 
 hipError_t launch_norm_linear(const LinArgs& a, const NormArgs& nq_in, hipStream_t st) {
