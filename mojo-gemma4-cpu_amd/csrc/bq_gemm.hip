@@ -70,7 +70,7 @@ __device__ inline LinSeg seg_of(const Seg1Args& a, int& nt) {
 // skinny: M <= 16
 // ---------------------------------------------------------------------------
 template <int WAVES, bool PER_BLOCK, int U, class Args>
-__global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(Args args) {
+__device__ __forceinline__ void linear_skinny(const Args& args) {
   extern __shared__ int lds[];  // per-row: WAVES*256 ints; per-block: nb*256 ints
   int nt;
   const LinSeg seg = seg_of(args, nt);
@@ -217,6 +217,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(Args args) {
   if (seg.out_f32) seg.out_f32[(size_t)i * seg.n + n] = y;
 }
 
+// A one-segment call's arguments as the kernel's own scalars: the dispatch
+// preloads the first 14 dwords into SGPRs (the build's kernarg preload), so
+// everything the addresses need -- K, M, block and the weight, activation and
+// scale pointers, in that order -- is there at the first instruction; only
+// out_f32 and n, read by the epilogue, are loaded.
+#define BQ_SEG1_PARAMS                                                                          \
+  int K, int M, int block, const int8_t *w, const int8_t *act, const float *ws, const float *sa, \
+      uint16_t *out, float *out_f32, int n
+#define BQ_SEG1_FIELDS w, ws, act, sa, out, out_f32, n, M, K, block
+#define BQ_SEG1_ARGS(s) \
+  s.K, s.M, s.block, s.w, s.act, s.ws, s.sa, s.out, s.out_f32, s.n
+
+template <int WAVES, bool PER_BLOCK, int U>
+__global__ __launch_bounds__(WAVES * 64) void k_linear_skinny(LinArgs args) {
+  linear_skinny<WAVES, PER_BLOCK, U>(args);
+}
+template <int WAVES, bool PER_BLOCK, int U>
+__global__ __launch_bounds__(WAVES * 64) void k_linear_skinny_1(BQ_SEG1_PARAMS) {
+  linear_skinny<WAVES, PER_BLOCK, U>(Seg1Args{BQ_SEG1_FIELDS});
+}
+
 // ---------------------------------------------------------------------------
 // M = 1, per-row (the decode GEMV)
 // ---------------------------------------------------------------------------
@@ -260,8 +281,7 @@ __device__ inline v4i row_shl_v4(const v4i& x) {
 // (one workgroup per CU at the model's widths: waves_per_eu(1, 2) lets the
 // compiler hold every fragment in registers instead of sinking the loads)
 template <int WAVES, int U, class Args>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void k_gemv_m1(Args args) {
+__device__ __forceinline__ void gemv_m1(const Args& args) {
   constexpr int NC = U >= 4 ? 4 : U;  // accumulator chains
   constexpr int NA = (U + 15) / 16;   // activation loads per lane
   __shared__ int part[WAVES * 16];
@@ -310,6 +330,17 @@ void k_gemv_m1(Args args) {
   if (seg.out_f32) seg.out_f32[n] = y;
 }
 
+template <int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_gemv_m1(LinArgs args) {
+  gemv_m1<WAVES, U>(args);
+}
+template <int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_gemv_m1_1(BQ_SEG1_PARAMS) {
+  gemv_m1<WAVES, U>(Seg1Args{BQ_SEG1_FIELDS});
+}
+
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
@@ -323,14 +354,19 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     if (a.M == 1 && !per_block && !tune().gemv_waves && a.K <= 4096) {
       const int w1 = tune().gemv_m1_waves ? tune().gemv_m1_waves : 4;
       dim3 g1(tiles);
-      auto go = [&](const auto& args) {
-        using A = std::decay_t<decltype(args)>;
-        if (w1 <= 2) hipLaunchKernelGGL((k_gemv_m1<2, 32, A>), g1, dim3(128), 0, st, args);
-        else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8, A>), g1, dim3(512), 0, st, args);
-        else hipLaunchKernelGGL((k_gemv_m1<4, 16, A>), g1, dim3(256), 0, st, args);
-      };
-      if (a.nseg == 1) go(seg1_args(a));
-      else go(a);
+      if (a.nseg == 1) {
+        const Seg1Args s1 = seg1_args(a);
+#define BQ_GO(W, U_, B) \
+  hipLaunchKernelGGL((k_gemv_m1_1<W, U_>), g1, dim3(B), 0, st, BQ_SEG1_ARGS(s1))
+        if (w1 <= 2) BQ_GO(2, 32, 128);
+        else if (w1 >= 8) BQ_GO(8, 8, 512);
+        else BQ_GO(4, 16, 256);
+#undef BQ_GO
+      } else {
+        if (w1 <= 2) hipLaunchKernelGGL((k_gemv_m1<2, 32>), g1, dim3(128), 0, st, a);
+        else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8>), g1, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_m1<4, 16>), g1, dim3(256), 0, st, a);
+      }
       return hipGetLastError();
     }
     // 16 waves split K so that each wave's whole slice (<= 4 fragments for
@@ -341,24 +377,25 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
     const int waves = tune().gemv_waves ? tune().gemv_waves : 16;
     const int nb = a.K / a.block;
     dim3 g(tiles);
-    auto go = [&](const auto& args) {
-      using A = std::decay_t<decltype(args)>;
-      if (waves >= 16) {
-        const size_t lds = (size_t)(per_block ? nb : 16) * 256 * sizeof(int);
-        if (per_block) hipLaunchKernelGGL((k_linear_skinny<16, true, 4, A>), g, dim3(1024), lds, st, args);
-        else hipLaunchKernelGGL((k_linear_skinny<16, false, 4, A>), g, dim3(1024), lds, st, args);
-      } else if (waves <= 4) {
-        const size_t lds = (size_t)(per_block ? nb : 4) * 256 * sizeof(int);
-        if (per_block) hipLaunchKernelGGL((k_linear_skinny<4, true, 16, A>), g, dim3(256), lds, st, args);
-        else hipLaunchKernelGGL((k_linear_skinny<4, false, 16, A>), g, dim3(256), lds, st, args);
-      } else {
-        const size_t lds = (size_t)(per_block ? nb : 8) * 256 * sizeof(int);
-        if (per_block) hipLaunchKernelGGL((k_linear_skinny<8, true, 8, A>), g, dim3(512), lds, st, args);
-        else hipLaunchKernelGGL((k_linear_skinny<8, false, 8, A>), g, dim3(512), lds, st, args);
-      }
-    };
-    if (a.nseg == 1) go(seg1_args(a));
-    else go(a);
+    const Seg1Args s1 = seg1_args(a);
+    const bool one = a.nseg == 1;
+#define BQ_GO(W, PB, U_)                                                                        \
+  do {                                                                                          \
+    const size_t lds = (size_t)(PB ? nb : W) * 256 * sizeof(int);                              \
+    if (one)                                                                                    \
+      hipLaunchKernelGGL((k_linear_skinny_1<W, PB, U_>), g, dim3(64 * W), lds, st,              \
+                         BQ_SEG1_ARGS(s1));                                                      \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_linear_skinny<W, PB, U_>), g, dim3(64 * W), lds, st, a);            \
+  } while (0)
+    if (waves >= 16) {
+      if (per_block) BQ_GO(16, true, 4); else BQ_GO(16, false, 4);
+    } else if (waves <= 4) {
+      if (per_block) BQ_GO(4, true, 16); else BQ_GO(4, false, 16);
+    } else {
+      if (per_block) BQ_GO(8, true, 8); else BQ_GO(8, false, 8);
+    }
+#undef BQ_GO
     return hipGetLastError();
   }
   // prefer the largest M tile that still yields >= 256 workgroups (one per CU)
