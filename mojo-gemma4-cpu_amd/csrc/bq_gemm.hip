@@ -426,7 +426,7 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
 // consecutive values per lane (nq_v8_transform), the codes one 8-byte store
 // per lane; otherwise the pair layout's SPW segments per wave.
 template <int NSEG, int SPW, bool V8, class Args>
-__global__ __launch_bounds__(512) void k_norm_linear_skinny(Args args, NormArgs nq) {
+__device__ __forceinline__ void norm_linear_skinny(const Args& args, const NormArgs& nq) {
   constexpr int WAVES = 8, U = 8;
   __shared__ __attribute__((aligned(16))) int8_t s_x[64 * WAVES * U];  // the row's codes
   __shared__ int lds[WAVES * 256];
@@ -540,6 +540,22 @@ __global__ __launch_bounds__(512) void k_norm_linear_skinny(Args args, NormArgs 
   if (seg.out_f32) seg.out_f32[n] = y;
 }
 
+template <int NSEG, int SPW, bool V8>
+__global__ __launch_bounds__(512) void k_norm_linear_skinny(LinArgs args, NormArgs nq) {
+  norm_linear_skinny<NSEG, SPW, V8>(args, nq);
+}
+// one segment, scalar arguments: the first 14 dwords (preloaded) hold what
+// the row loads and the weight stream need first -- K, the FWHT block, the
+// row and gain, the weights and their scales, sqrt_n, n_eps, the FWHT scale
+template <int NSEG, int SPW, bool V8>
+__global__ __launch_bounds__(512) void k_norm_linear_skinny_1(
+    int K, int block, const uint16_t* src, const uint16_t* gamma, const int8_t* w, const float* ws,
+    float sqrt_n, float n_eps, float fwht_scale, int8_t* xq, float* sa, uint16_t* out,
+    float* out_f32, int n) {
+  norm_linear_skinny<NSEG, SPW, V8>(Seg1Args{w, ws, nullptr, nullptr, out, out_f32, n, 1, K, K},
+                                    NormArgs{src, gamma, xq, sa, block, sqrt_n, n_eps, fwht_scale});
+}
+
 // the fused kernel's shapes: one token, the pair-layout norm-quant's shapes
 // (hidden % 256 == 0, hidden <= 4096), per-row weights
 static bool launch_norm_linear_fused(const LinArgs& a, const NormArgs& nq, hipStream_t st) {
@@ -557,20 +573,29 @@ static bool launch_norm_linear_fused(const LinArgs& a, const NormArgs& nq, hipSt
   // (16-byte aligned gain, 8-byte aligned codes)
   const bool v8 = nq.block == 128 && tune().nq_v8 && !(reinterpret_cast<uintptr_t>(nq.gamma) & 15u) &&
                   !(reinterpret_cast<uintptr_t>(nq.xq) & 7u);
-  auto go = [&](const auto& args) -> bool {
-    using A = std::decay_t<decltype(args)>;
-    if (v8) {
-#define BQ_NL8(N) if (ns <= N) { hipLaunchKernelGGL((k_norm_linear_skinny<N, 1, true, A>), g, b, 0, st, args, nq); return true; }
-      BQ_NL8(8) BQ_NL8(16) BQ_NL8(22) BQ_NL8(24) BQ_NL8(32)
+  const Seg1Args s1 = seg1_args(a);
+  const bool one = a.nseg == 1;
+#define BQ_NLL(N, S, V)                                                                          \
+  do {                                                                                           \
+    if (one)                                                                                     \
+      hipLaunchKernelGGL((k_norm_linear_skinny_1<N, S, V>), g, b, 0, st, s1.K, nq.block, nq.src, \
+                         nq.gamma, s1.w, s1.ws, nq.sqrt_n, nq.n_eps, nq.fwht_scale, nq.xq, nq.sa, \
+                         s1.out, s1.out_f32, s1.n);                                              \
+    else                                                                                         \
+      hipLaunchKernelGGL((k_norm_linear_skinny<N, S, V>), g, b, 0, st, a, nq);                   \
+    return true;                                                                                 \
+  } while (0)
+  if (v8) {
+#define BQ_NL8(N) if (ns <= N) BQ_NLL(N, 1, true);
+    BQ_NL8(8) BQ_NL8(16) BQ_NL8(22) BQ_NL8(24) BQ_NL8(32)
 #undef BQ_NL8
-    }
-#define BQ_NL(N, S) if (ns <= N && spw == S) { hipLaunchKernelGGL((k_norm_linear_skinny<N, S, false, A>), g, b, 0, st, args, nq); return true; }
-    BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
-    BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
+  }
+#define BQ_NL(N, S) if (ns <= N && spw == S) BQ_NLL(N, S, false);
+  BQ_NL(8, 1) BQ_NL(8, 2) BQ_NL(8, 4) BQ_NL(16, 2) BQ_NL(16, 4)
+  BQ_NL(24, 3) BQ_NL(24, 4) BQ_NL(32, 4)
 #undef BQ_NL
-    return false;
-  };
-  return a.nseg == 1 ? go(seg1_args(a)) : go(a);
+#undef BQ_NLL
+  return false;
 }
 
 hipError_t launch_norm_linear(const LinArgs& a, const NormArgs& nq_in, hipStream_t st) {
