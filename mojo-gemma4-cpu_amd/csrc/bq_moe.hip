@@ -142,12 +142,14 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
 // through LDS to the fused FWHT64 block-quant (inter % 64 == 0: no wave of
 // the group is idle).
 template <int U>
+// (the scalars the m-tile lookup and the first addresses need come first:
+// the dispatch preloads the first 14 argument dwords into SGPRs)
 __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
-    const int8_t* __restrict__ x_i8, const float* __restrict__ x_sa,
-    const int32_t* __restrict__ eo, const Route* __restrict__ routes,
-    const int8_t* __restrict__ w_gu, const float* __restrict__ gu_scale,
-    uint16_t* __restrict__ bucket, int8_t* __restrict__ bi8, float* __restrict__ bsa,
-    float fwht64, int E, int hidden, int inter, int max_routes) {
+    int E, int hidden, int inter, int max_routes, const int32_t* __restrict__ eo,
+    const Route* __restrict__ routes, const int8_t* __restrict__ w_gu,
+    const int8_t* __restrict__ x_i8, const float* __restrict__ gu_scale,
+    const float* __restrict__ x_sa, uint16_t* __restrict__ bucket, int8_t* __restrict__ bi8,
+    float* __restrict__ bsa, float fwht64) {
   __shared__ __attribute__((aligned(16))) uint16_t qtile[16 * 64];
   int e, r0, r1;
   if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;
@@ -248,10 +250,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 template <int U, int NS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(U * NS <= 2 ? 8 : 1)))
 void k_moe_down_skinny(
-    const int8_t* __restrict__ b_i8, const float* __restrict__ b_sa,
-    const int32_t* __restrict__ eo, const Route* __restrict__ routes,
-    const int8_t* __restrict__ w_d, const float* __restrict__ d_scale, float* __restrict__ y,
-    int E, int hidden, int inter, int block, int max_routes) {
+    int E, int hidden, int inter, int block, int max_routes, const int32_t* __restrict__ eo,
+    const Route* __restrict__ routes, const float* __restrict__ b_sa,
+    const int8_t* __restrict__ w_d, const int8_t* __restrict__ b_i8,
+    const float* __restrict__ d_scale, float* __restrict__ y) {
   __shared__ float s_sa[16 * 64];
   int e, r0, r1;
   if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;  // whole workgroup
@@ -466,9 +468,9 @@ hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_
   dim3 g((inter / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
 #define BQ_GU(U)                                                                                  \
   case U:                                                                                         \
-    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, x_i8, x_sa, eo, routes, w_gu,       \
-                       gu_scale, bucket, bi8, bsa, fwht_scale_host(64), experts, hidden, inter,  \
-                       max_routes);                                                               \
+    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, experts, hidden, inter, max_routes,  \
+                       eo, routes, w_gu, x_i8, gu_scale, x_sa, bucket, bi8, bsa,                  \
+                       fwht_scale_host(64));                                                      \
     break;
   switch (tune().gu_skinny) {  // 2 or 6 k-steps per register slot; 4 measured best
     BQ_GU(2) BQ_GU(6)
@@ -508,8 +510,8 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
 #define BQ_DS(U, NS)                                                                              \
   case U * 10 + NS: {                                                                             \
     dim3 g((hidden / 16 + 4 * NS - 1) / (4 * NS), mtile_bound(max_routes, experts, 16)), b(256); \
-    hipLaunchKernelGGL((k_moe_down_skinny<U, NS>), g, b, 0, st, bucket_i8, bucket_sa, eo, routes, \
-                       w_down, down_scale, y, experts, hidden, inter, block, max_routes);         \
+    hipLaunchKernelGGL((k_moe_down_skinny<U, NS>), g, b, 0, st, experts, hidden, inter, block,    \
+                       max_routes, eo, routes, bucket_sa, w_down, bucket_i8, down_scale, y);      \
     break;                                                                                        \
   }
       switch (ut) {
