@@ -218,16 +218,16 @@ def _env_int(name):
 
 def gemv_kernel():
     """(kernel name, waves per workgroup) of the decode GEMV (M = 1, per-row,
-    K = 4096) as the library's launcher picks it: k_gemv_m1 with
-    BQ_GEMV_M1_WAVES (2, 4, 8; default 4), or k_linear_skinny when
-    BQ_GEMV_WAVES (4, 8, 16) is set."""
+    K = 4096, one output segment) as the library's launcher picks it:
+    k_gemv_m1_1 with BQ_GEMV_M1_WAVES (2, 4, 8; default 4), or
+    k_linear_skinny_1 when BQ_GEMV_WAVES (4, 8, 16) is set."""
     g = _env_int("BQ_GEMV_WAVES")
     if g:
         w = 16 if g >= 16 else 4 if g <= 4 else 8
-        return f"k_linear_skinny<{w}, false, {64 // w}>", w
+        return f"k_linear_skinny_1<{w}, false, {64 // w}>", w
     m1 = _env_int("BQ_GEMV_M1_WAVES") or 4
     w = 2 if m1 <= 2 else 8 if m1 >= 8 else 4
-    return f"k_gemv_m1<{w}, {64 // w}>", w
+    return f"k_gemv_m1_1<{w}, {64 // w}>", w
 
 
 def gemv_waves():
