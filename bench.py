@@ -496,15 +496,18 @@ class MoeLayer:
         self.out = torch.empty(T, H, dtype=torch.bfloat16, device=d)
         self.side = torch.cuda.Stream()  # default priority
 
-    def __call__(self, _i=0, fused=True, overlap=3):
+    def __call__(self, _i=0, fused=True, overlap=3, prep=True):
         # overlap 3: bq_moe_prep (top-k, schedule and norm-quant in one launch
         # up to 1024 route slots); 1: bq_moe_route_schedule then the
         # norm-quant; 2: the norm-quant on a second stream beside the routing
         # (measured slower: the graph's cross-stream joins cost more than the
-        # overlap saves); 0: the reference's three calls
+        # overlap saves); 0: the reference's three calls.  prep=False: the
+        # caller has already made idx/w/eo/routes/xq/xsa (bq_ffn_prep)
         import torch
         bq, T = self.bq, self.T
-        if overlap == 3:
+        if not prep:
+            pass
+        elif overlap == 3:
             bq.moe_prep(self.logits, self.x, self.gamma, TOPK, self.pes, 128,
                         out=(self.idx, self.w, self.eo, self.routes, self.xq, self.xsa))
         elif overlap == 2:
@@ -669,23 +672,27 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     gt, up = e(T, 2112), e(T, 2112)
     gq_, gsa = e(T, 2112, dt=torch.int8), e(T, 2112 // 64, dt=torch.float32)
     moe = MoeLayer(bq, torch, T, Wgu, Wd)
+    moe.x = x   # the dense MLP and the MoE both read the post-attention residual
 
     xqd, xsad = e(T, H, dt=torch.int8), e(T, dt=torch.float32)
     od = e(T, H)
 
-    def dense_mlp():
-        bq.norm_quant(x, gamma, 128, out=(xqd, xsad))
+    def ffn():
+        # routing, schedule and both norm-quants of x (the MoE's gamma and the
+        # dense MLP's) in one launch (bq_ffn_prep)
+        bq.ffn_prep(moe.logits, x, moe.gamma, gamma, TOPK, moe.pes, 128,
+                    out=(moe.idx, moe.w, moe.eo, moe.routes, moe.xq, moe.xsa, xqd, xsad))
         bq.linear_pair(xqd, xsad, dg, du, outs=(gt, up))   # gate and up: one launch
         bq.block_quant(gt, 64, True, out=(gq_, gsa))   # GELU(gate)*up is elementwise (not a bq op)
         bq.block_linear(gq_, gsa, dd, 64, out=od)
+        moe(prep=False)
 
     def sliding(_i=0):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
         bq.qkv(xq, xsa, sq, sk, sv, outs=(q_s, k_s, v_s))
         bq.block_quant(attn_s, 256, False, out=(oq_s, osa_s))
         bq.block_linear(oq_s, osa_s, so, 256, out=o)
-        dense_mlp()
-        moe()
+        ffn()
 
     def full(_i=0):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
@@ -693,8 +700,7 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
         bq.linear(xq, xsa, fk, out=k_f)               # k_eq_v: one projection for K and V
         bq.block_quant(attn_f, 512, False, out=(oq_f, osa_f))
         bq.block_linear(oq_f, osa_f, fo, 512, out=o)
-        dense_mlp()
-        moe()
+        ffn()
 
     gs_ = graph_of(sliding, 1)
     ms_s = time_graph(gs_, 1, steps, 0).p50
@@ -712,7 +718,8 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     nq = lambda k: 2 * T * k + 2 * k + T * k + 4 * T            # norm-quant: bf16 in, int8 + scale out
     lin = lambda n, k, nb=1: T * k + 4 * T * nb + 2 * T * n     # linear: int8 + scales in, bf16 out
     bqz = lambda k, b: 2 * T * k + T * k + 4 * T * (k // b)     # block-quant
-    mlp = (nq(H) + 2 * wb(2112, H) + lin(2 * 2112, H) + bqz(2112, 64) + wb(H, 2112) +
+    # the dense MLP's norm-quant shares the MoE's read of x (one bq_ffn_prep launch)
+    mlp = (nq(H) - 2 * T * H + 2 * wb(2112, H) + lin(2 * 2112, H) + bqz(2112, 64) + wb(H, 2112) +
            lin(H, 2112, 2112 // 64))
     sliding_b = (nq(H) + wb(4096, H) + wb(2048, H) + wb(2048, H) + lin(8192, H) +
                  bqz(4096, 256) + wb(H, 4096) + lin(H, 4096, 16) + mlp)

@@ -246,6 +246,21 @@ int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uin
                 int32_t* expert_offset, bq_route* routes, int8_t* x_i8, float* x_sa,
                 void* stream);
 
+/* bq_moe_prep plus the decoder layer's dense-MLP norm-quant of the same
+ * input: dispatch_bq_norm_quant(x_main, pre_ffn_norm) and the MoE block's
+ * prep (modeling/gemma_4_moe_bq.mojo:749-753 and 673-688), which read the
+ * same hidden states with different gains.  dense_i8 / dense_sa =
+ * bq_norm_quant(x, dense_gamma, block); the other outputs are bq_moe_prep's.
+ * Where bq_moe_prep is one launch, the dense rows are quantized by more
+ * workgroups of that launch; otherwise the dense norm-quant runs first as a
+ * launch of its own.  Both norm-quants use the same hidden, block, sqrt_n and
+ * n_eps (the model's).  The checks of bq_moe_prep apply. */
+int bq_ffn_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,
+                const uint16_t* gamma, const uint16_t* dense_gamma, int seq_len, int experts,
+                int top_k, int hidden, int block, float sqrt_n, float n_eps, int32_t* route_idx,
+                float* route_w, int32_t* expert_offset, bq_route* routes, int8_t* x_i8,
+                float* x_sa, int8_t* dense_i8, float* dense_sa, void* stream);
+
 /* dispatch_bq_phase1_gate_up[hidden, gate_up, inter] (moe.mojo:132-164):
  * for every route record rec of expert e (rows of w_gate_up: gate
  * [0,inter), up [inter, 2*inter) of expert e, expert stride 2*inter*hidden):

@@ -50,6 +50,7 @@ SIGNATURES = {
     "bq_moe_build_schedule": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp],
     "bq_moe_route_schedule": [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "bq_moe_prep": [_vp] * 4 + [_i] * 5 + [_f, _f] + [_vp] * 7,
+    "bq_ffn_prep": [_vp] * 5 + [_i] * 5 + [_f, _f] + [_vp] * 9,
     "bq_head_prep": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _vp],
     "bq_flash_sample_workspace_size": [_i, _i],
     "bq_flash_sample": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, C.c_int64, _vp, _sz,
@@ -437,6 +438,40 @@ def moe_prep(logits: torch.Tensor, x: torch.Tensor, gamma: torch.Tensor, top_k: 
                             block, sqrt_n, n_eps, _p(idx), _p(w), _p(eo), _p(routes), _p(xq),
                             _p(sa), _stream()))
     return idx, w, eo, routes, xq, sa
+
+
+def ffn_prep(logits: torch.Tensor, x: torch.Tensor, gamma: torch.Tensor,
+             dense_gamma: torch.Tensor, top_k: int, per_expert_scale: torch.Tensor | None = None,
+             block: int = 128, sqrt_n=None, n_eps=None, out=None):
+    """moe_prep plus the dense MLP's norm-quant of the same x with dense_gamma
+    (bq_ffn_prep: one launch where moe_prep is one) ->
+    (route_idx, route_w, expert_offset, routes, x_i8, x_sa, dense_i8, dense_sa)."""
+    _dev(logits, torch.float32)
+    _dev(x, torch.bfloat16)
+    _dev(gamma, torch.bfloat16)
+    _dev(dense_gamma, torch.bfloat16)
+    if per_expert_scale is not None:
+        _dev(per_expert_scale, torch.bfloat16)
+    t, e = logits.shape
+    h = x.shape[1]
+    if sqrt_n is None:
+        sqrt_n, n_eps = norm_consts(h)
+    d = logits.device
+    if out is None:
+        idx = torch.empty((t, top_k), dtype=torch.int32, device=d)
+        w = torch.empty((t, top_k), dtype=torch.float32, device=d)
+        eo = torch.empty(e + 1, dtype=torch.int32, device=d)
+        routes = torch.zeros((t * top_k, 2), dtype=torch.int32, device=d)
+        xq = torch.empty((t, h), dtype=torch.int8, device=d)
+        sa = torch.empty(t, dtype=torch.float32, device=d)
+        dq = torch.empty((t, h), dtype=torch.int8, device=d)
+        dsa = torch.empty(t, dtype=torch.float32, device=d)
+    else:
+        idx, w, eo, routes, xq, sa, dq, dsa = out
+    _check(_lib.bq_ffn_prep(_p(logits), _p(per_expert_scale), _p(x), _p(gamma), _p(dense_gamma),
+                            t, e, top_k, h, block, sqrt_n, n_eps, _p(idx), _p(w), _p(eo),
+                            _p(routes), _p(xq), _p(sa), _p(dq), _p(dsa), _stream()))
+    return idx, w, eo, routes, xq, sa, dq, dsa
 
 
 def build_schedule(route_idx: torch.Tensor, route_w: torch.Tensor, experts: int,

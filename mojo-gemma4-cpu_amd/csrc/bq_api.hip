@@ -469,6 +469,31 @@ int bq_moe_prep(const float* logits, const uint16_t* per_expert_scale, const uin
                    "moe_prep");
 }
 
+int bq_ffn_prep(const float* logits, const uint16_t* per_expert_scale, const uint16_t* x,
+                const uint16_t* gamma, const uint16_t* dense_gamma, int seq_len, int experts,
+                int top_k, int hidden, int block, float sqrt_n, float n_eps, int32_t* route_idx,
+                float* route_w, int32_t* expert_offset, bq_route* routes, int8_t* x_i8,
+                float* x_sa, int8_t* dense_i8, float* dense_sa, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!logits || !x || !gamma || !dense_gamma || !route_idx || !route_w || !expert_offset ||
+      !routes || !x_i8 || !x_sa || !dense_i8 || !dense_sa)
+    return fail(BQ_ERR_INVALID, "bq_ffn_prep: null pointer");
+  if (experts <= 0 || top_k <= 0) return fail(BQ_ERR_SHAPE, "bq_ffn_prep: bad top_k/experts");
+  if (experts > 256 || top_k > 16)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_ffn_prep: experts %d > 256 or top_k %d > 16", experts,
+                top_k);
+  if (!fwht_block_ok(block)) return fail(BQ_ERR_SHAPE, "bq_ffn_prep: unsupported FWHT block %d", block);
+  if (hidden <= 0 || hidden % 64 || hidden % block)
+    return fail(BQ_ERR_SHAPE, "bq_ffn_prep: hidden %d must be a multiple of 64 and of block %d", hidden, block);
+  if (hidden > kMaxRowLds) return fail(BQ_ERR_UNSUPPORTED, "bq_ffn_prep: hidden %d > %d", hidden, kMaxRowLds);
+  if (!a16(x)) return fail(BQ_ERR_INVALID, "bq_ffn_prep: x must be 16-byte aligned");
+  return check_hip(bq::launch_moe_prep(logits, per_expert_scale, x, gamma, seq_len, experts,
+                                       top_k, hidden, block, sqrt_n, n_eps, route_idx, route_w,
+                                       expert_offset, reinterpret_cast<bq::Route*>(routes), x_i8,
+                                       x_sa, S(stream), dense_gamma, dense_i8, dense_sa),
+                   "ffn_prep");
+}
+
 int bq_moe_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len, int top_k,
                           int expert_base, int experts, int32_t* expert_offset, bq_route* routes,
                           void* stream) {

@@ -151,7 +151,8 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
                            const uint16_t* gamma, int T, int E, int top_k, int hidden, int block,
                            float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
                            int32_t* expert_offset, Route* routes, int8_t* xq, float* sa,
-                           hipStream_t st);
+                           hipStream_t st, const uint16_t* gamma2 = nullptr,
+                           int8_t* xq2 = nullptr, float* sa2 = nullptr);
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);

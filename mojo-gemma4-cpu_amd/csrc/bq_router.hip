@@ -363,8 +363,10 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_route_schedule_small(
 // (modeling/gemma_4_moe_bq.mojo:673-688) -- with the same results.
 // Workgroups [0, nq_blocks) norm-quantize two tokens each (the pair layout of
 // k_norm_quant_pair: a token over WPT <= 8 waves of SPW segments, the row's
-// amax through LDS); the others take 16 tokens' top-k each, one wave per
-// token.  The last top-k workgroup to finish builds the schedule from every
+// amax through LDS); with a second gain (gamma2, the decoder's dense-MLP
+// input norm, gemma_4_moe_bq.mojo:749-753) the second half of them quantizes
+// the same rows into xq2 / sa2.  The others take 16 tokens' top-k each, one
+// wave per token.  The last top-k workgroup to finish builds the schedule from every
 // workgroup's routes (schedule_small, one thread per slot): each top-k
 // workgroup fences its route stores at device scope before it counts itself
 // done on *done, and the last one fences again before it reads them.  The
@@ -386,7 +388,8 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
     int8_t* __restrict__ xq, float* __restrict__ sa, int32_t* __restrict__ route_idx,
     float* __restrict__ route_w, int32_t* __restrict__ expert_offset, Route* __restrict__ routes,
     int T, int E, int top_k, int hidden, int block, float sqrt_n, float n_eps, float fwht_scale,
-    int nq_blocks, unsigned* done) {
+    int nq_blocks, unsigned* done, int nq_per, const uint16_t* __restrict__ gamma2,
+    int8_t* __restrict__ xq2, float* __restrict__ sa2) {
   __shared__ float s_max[kPrepThreads / 64];
   __shared__ int s_wc[kSchedWavesSmall][kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
@@ -394,10 +397,14 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   const int tid = threadIdx.x, lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if ((int)blockIdx.x < nq_blocks) {
-    // ---- norm-quant: token 2 b + g on waves 8 g .. 8 g + WPT - 1
+    // ---- norm-quant: token 2 b + g on waves 8 g .. 8 g + WPT - 1.  Blocks
+    // [nq_per, 2 nq_per) quantize the same rows with a second gain into
+    // xq2 / sa2 (the dense MLP's input beside the experts')
+    const bool second = (int)blockIdx.x >= nq_per;  // workgroup-uniform
+    if (second) { gamma = gamma2; xq = xq2; sa = sa2; }
     const int nseg = hidden >> 7, wpt = (nseg + SPW - 1) / SPW;
     const int g = wave >> 3, wv = wave & 7;
-    const int t = (int)blockIdx.x * 2 + g, q0 = wv * SPW;
+    const int t = ((int)blockIdx.x - (second ? nq_per : 0)) * 2 + g, q0 = wv * SPW;
     const bool live = t < T && wv < wpt;  // wave-uniform
     float v[SPW][2];
     if (live) {
@@ -611,7 +618,7 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
                            const uint16_t* gamma, int T, int E, int top_k, int hidden, int block,
                            float sqrt_n, float n_eps, int32_t* route_idx, float* route_w,
                            int32_t* expert_offset, Route* routes, int8_t* xq, float* sa,
-                           hipStream_t st) {
+                           hipStream_t st, const uint16_t* gamma2, int8_t* xq2, float* sa2) {
   if (T <= 0) return hipSuccess;
   if (E > kMaxExperts) return hipErrorInvalidValue;
   const int ns = hidden >> 7;
@@ -622,7 +629,7 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
   unsigned* done = nullptr;
   bool fused = T * top_k <= kSchedSmallSlots && hidden % 256 == 0 && hidden <= 4096 &&
                tune().nq_pair && tune().moe_prep && !(reinterpret_cast<uintptr_t>(xq) & 1u) &&
-               (ns + spw - 1) / spw <= 8;
+               !(reinterpret_cast<uintptr_t>(xq2) & 1u) && (ns + spw - 1) / spw <= 8;
   if (fused && !one) {  // the spread form's hand-off needs the stream's counter
     const hipError_t ra = prep_counter(st, &done);
     if (ra != hipSuccess) return ra;
@@ -634,6 +641,12 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
                     hidden <= 4096 && tune().nq_pair && tune().nq_v8 && tune().moe_prep &&
                     !(reinterpret_cast<uintptr_t>(gamma) & 15u) &&
                     !(reinterpret_cast<uintptr_t>(xq) & 7u);
+  // the second norm-quant (gamma2) runs in the k_moe_prep launch; on the
+  // other paths it is a launch of its own, first
+  if (gamma2 && !fused) {
+    const hipError_t r2 = launch_norm_quant(src, gamma2, xq2, sa2, T, hidden, block, sqrt_n, n_eps, st);
+    if (r2 != hipSuccess) return r2;
+  }
   if (wide) {
     const int tk_blocks = (T + 3) / 4;
     const dim3 g(2 * tk_blocks), b(256);
@@ -661,7 +674,7 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
     if (r != hipSuccess) return r;
     return launch_norm_quant(src, gamma, xq, sa, T, hidden, block, sqrt_n, n_eps, st);
   }
-  const int nq_blocks = (T + 1) / 2;
+  const int nq_per = (T + 1) / 2, nq_blocks = gamma2 ? 2 * nq_per : nq_per;
   // up to 16 tokens one workgroup takes every top-k (one token per wave) and
   // builds the schedule from LDS, with no cross-workgroup hand-off: the
   // batch-16 decoder layer's MoE 106.6 -> 105.1 us.  At 32 tokens (two per
@@ -676,11 +689,11 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
     if (one)                                                                                      \
       hipLaunchKernelGGL((k_moe_prep<NEV, N, S, 1>), g, b, 0, st, logits, pes, src, gamma, xq, sa, \
                          route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,  \
-                         sqrt_n, n_eps, sc, nq_blocks, done);                                     \
+                         sqrt_n, n_eps, sc, nq_blocks, done, nq_per, gamma2, xq2, sa2);           \
     else                                                                                          \
       hipLaunchKernelGGL((k_moe_prep<NEV, N, S>), g, b, 0, st, logits, pes, src, gamma, xq, sa,   \
                          route_idx, route_w, expert_offset, routes, T, E, top_k, hidden, block,  \
-                         sqrt_n, n_eps, sc, nq_blocks, done);                                     \
+                         sqrt_n, n_eps, sc, nq_blocks, done, nq_per, gamma2, xq2, sa2);           \
     return hipGetLastError();                                                                     \
   }
 #define BQ_PREP_NQ(NEV) \

@@ -94,6 +94,15 @@ def test_validation_errors(L):
     assert prep(4, 128, 0, 2816, 128, P, P, P, P, P, P) == 2             # top_k
     assert prep(4, 128, 8, 2816, 48, P, P, P, P, P, P) == 2              # FWHT block
     assert prep(4, 128, 8, 2880, 128, P, P, P, P, P, P) == 2             # hidden % block
+    fprep = lambda T, E, k, H, B, *ptrs: L.bq_ffn_prep(P, None, P, P, P, T, E, k, H, B, f1, f1,
+                                                       *ptrs, None)
+    assert fprep(0, 128, 8, 2816, 128, *([None] * 8)) == 0               # empty batch
+    assert fprep(4, 128, 8, 2816, 128, P, P, P, P, P, P, None, P) == 1   # null dense codes
+    assert fprep(4, 512, 8, 2816, 128, *([P] * 8)) == 4                  # experts > 256
+    assert fprep(4, 128, 0, 2816, 128, *([P] * 8)) == 2                  # top_k
+    assert fprep(4, 128, 8, 2880, 128, *([P] * 8)) == 2                  # hidden % block
+    assert L.bq_ffn_prep(P, None, P, P, None, 4, 128, 8, 2816, 128, f1, f1, *([P] * 8),
+                         None) == 1                                       # null dense gain
     assert L.bq_moe_router_logits(P, P, P, P, 4, 2880 + 32, 128, C.c_float(1), C.c_float(1),
                                   None) == 2
     assert L.bq_moe_router_logits(P, C.c_void_p(18), P, P, 4, 2816, 128, C.c_float(1),

@@ -488,6 +488,54 @@ def test_moe_prep_batches_in_a_row(gpu, O):
             np.testing.assert_array_equal(host(a), host(b))
 
 
+@pytest.mark.parametrize("T,E,k,H,B", [(1, 128, 8, 2816, 128), (7, 128, 8, 2816, 128),
+                                       (16, 128, 8, 2816, 128), (17, 128, 8, 2816, 128),
+                                       (32, 128, 8, 2816, 128), (9, 256, 16, 4096, 256),
+                                       (129, 128, 8, 2816, 128), (301, 128, 8, 2816, 256)])
+def test_ffn_prep(gpu, O, T, E, k, H, B):
+    """bq_ffn_prep = bq_moe_prep plus the dense MLP's norm-quant of the same
+    rows with a second gain, against the oracle, bit-exact: the dense rows in
+    more workgroups of the one prep launch (T <= 128 at top-8), or a launch of
+    their own before the two-launch and separate paths (T = 129, 301).  Three
+    calls in a row."""
+    logits = O.synth_normal_f32(80 + T, 1.0, (T, E))
+    x = O.synth_normal_bf16(81 + T, 1.0, (T, H))
+    g = O.f32_to_bf16(O.synth_normal_f32(82, 0.3, (H,)) + 1.0)
+    gd = O.f32_to_bf16(O.synth_normal_f32(83, 0.3, (H,)) + 1.0)
+    ridx, rw = O.route_topk_softmax(logits, k, None)
+    reo, rroutes = O.build_schedule(ridx, rw, E)
+    rq, rsa = O.norm_quant(x, g, B)
+    rdq, rdsa = O.norm_quant(x, gd, B)
+    for _ in range(3):
+        idx, w, eo, routes, xq, sa, dq, dsa = gpu.ffn_prep(dev(logits), dev(x), dev(g), dev(gd), k,
+                                                           block=B)
+        np.testing.assert_array_equal(host(idx), ridx)
+        np.testing.assert_array_equal(host(w), rw)
+        np.testing.assert_array_equal(host(eo), reo)
+        r = host(routes)
+        np.testing.assert_array_equal(r[:, 0], rroutes["token"])
+        np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
+        np.testing.assert_array_equal(host(xq), rq)
+        np.testing.assert_array_equal(host(sa), rsa)
+        np.testing.assert_array_equal(host(dq), rdq)
+        np.testing.assert_array_equal(host(dsa), rdsa)
+
+
+def test_ffn_prep_matches_separate_calls(gpu, O):
+    """batches of different sizes in a row (the spread form's counter is
+    shared): bq_ffn_prep = bq_moe_prep + bq_norm_quant with the dense gain"""
+    E, k, H = 128, 8, 2816
+    g = dev(O.f32_to_bf16(O.synth_normal_f32(85, 0.3, (H,)) + 1.0))
+    gd = dev(O.f32_to_bf16(O.synth_normal_f32(86, 0.3, (H,)) + 1.0))
+    for T in (32, 5, 64, 1, 16, 17, 32):
+        logits = dev(O.synth_normal_f32(87 + T, 1.0, (T, E)))
+        x = dev(O.synth_normal_bf16(88 + T, 1.0, (T, H)))
+        outs = gpu.ffn_prep(logits, x, g, gd, k)
+        ref = gpu.moe_prep(logits, x, g, k) + gpu.norm_quant(x, gd, 128)
+        for a, b in zip(outs, ref):
+            np.testing.assert_array_equal(host(a), host(b))
+
+
 def test_build_schedule_expert_range(gpu, O):
     # expert-parallel slice [32, 64) as a rank of degree 4 would build it
     idx, w = route_table(O, 40)

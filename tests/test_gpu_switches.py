@@ -132,6 +132,14 @@ def test_moe_prep_switches(gpu, O, tune_env, sw, T):
         np.testing.assert_array_equal(r[:, 1].view(np.float32), rroutes["weight"])
         np.testing.assert_array_equal(host(xq), rq)
         np.testing.assert_array_equal(host(sa), rsa)
+    # bq_ffn_prep under the same switch: the dense norm-quant of the same rows
+    gd = O.f32_to_bf16(O.synth_normal_f32(74, 0.3, (H,)) + 1.0)
+    rdq, rdsa = O.norm_quant(x, gd, B)
+    outs = gpu.ffn_prep(dev(logits), dev(x), dev(g), dev(gd), k, block=B)
+    for a, b in zip(outs[:6], (idx, w, eo, routes, xq, sa)):
+        np.testing.assert_array_equal(host(a), host(b))
+    np.testing.assert_array_equal(host(outs[6]), rdq)
+    np.testing.assert_array_equal(host(outs[7]), rdsa)
 
 
 # ----------------------------------------------------------------- MoE kernels
