@@ -641,8 +641,9 @@ def bench_moe(bq, torch, T, weights, steps):
 def bench_layer16(bq, torch, Wgu, Wd, steps):
     """All quantized projections of one decoder layer at decode batch 16:
     sliding (q/k/v 4096/2048/2048, o B=256) and full (q 8192, k 1024, o
-    B=512) attention projections, dense MLP (gate/up 2112, down B=64) and the
-    128-expert MoE, each with its activation prep."""
+    B=512) attention projections, dense MLP (gate/up 2112, GELU-tanh(gate) *
+    up, FWHT64 block-quant, down B=64) and the 128-expert MoE, each with its
+    activation prep."""
     T = 16
     gen = torch.Generator(device="cuda").manual_seed(0)
     d = "cuda"
@@ -669,7 +670,6 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     q_s, k_s, v_s = e(T, 4096), e(T, 2048), e(T, 2048)
     q_f, k_f = e(T, 8192), e(T, 1024)
     o = e(T, H)
-    gt, up = e(T, 2112), e(T, 2112)
     gq_, gsa = e(T, 2112, dt=torch.int8), e(T, 2112 // 64, dt=torch.float32)
     moe = MoeLayer(bq, torch, T, Wgu, Wd)
     moe.x = x   # the dense MLP and the MoE both read the post-attention residual
@@ -679,13 +679,16 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
 
     def ffn():
         # routing, schedule and both norm-quants of x (the MoE's gamma and the
-        # dense MLP's) in one launch (bq_ffn_prep)
+        # dense MLP's) in one launch (bq_ffn_prep); the dense MLP's gate/up,
+        # GELU and FWHT64 block-quant in the experts' gate/up launch
+        # (bq_ffn_gate_up), its down projection in the experts' down launch
+        # (bq_ffn_down)
         bq.ffn_prep(moe.logits, x, moe.gamma, gamma, TOPK, moe.pes, 128,
                     out=(moe.idx, moe.w, moe.eo, moe.routes, moe.xq, moe.xsa, xqd, xsad))
-        bq.linear_pair(xqd, xsad, dg, du, outs=(gt, up))   # gate and up: one launch
-        bq.block_quant(gt, 64, True, out=(gq_, gsa))   # GELU(gate)*up is elementwise (not a bq op)
-        bq.block_linear(gq_, gsa, dd, 64, out=od)
-        moe(prep=False)
+        bq.ffn_gate_up(moe.xq, moe.xsa, moe.eo, moe.routes, moe.Wgu, E, T, TOPK, I, xqd, xsad,
+                       dg, du, out=(moe.bi8, moe.bsa, gq_, gsa))
+        bq.ffn_down(moe.bi8, moe.bsa, moe.eo, moe.routes, moe.Wd, E, T, TOPK, H, gq_, gsa, dd,
+                    64, workspace=moe.ws, out=(moe.accum, moe.out, od))
 
     def sliding(_i=0):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
@@ -718,9 +721,11 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     nq = lambda k: 2 * T * k + 2 * k + T * k + 4 * T            # norm-quant: bf16 in, int8 + scale out
     lin = lambda n, k, nb=1: T * k + 4 * T * nb + 2 * T * n     # linear: int8 + scales in, bf16 out
     bqz = lambda k, b: 2 * T * k + T * k + 4 * T * (k // b)     # block-quant
-    # the dense MLP's norm-quant shares the MoE's read of x (one bq_ffn_prep launch)
-    mlp = (nq(H) - 2 * T * H + 2 * wb(2112, H) + lin(2 * 2112, H) + bqz(2112, 64) + wb(H, 2112) +
-           lin(H, 2112, 2112 // 64))
+    # the dense MLP's norm-quant shares the MoE's read of x (one bq_ffn_prep
+    # launch); its gate/up reads the int8 rows and writes the down
+    # projection's block-quantized activation (bq_ffn_gate_up)
+    mlp = (nq(H) - 2 * T * H + 2 * wb(2112, H) + T * H + 4 * T + T * 2112 + 4 * T * (2112 // 64) +
+           wb(H, 2112) + lin(H, 2112, 2112 // 64))
     sliding_b = (nq(H) + wb(4096, H) + wb(2048, H) + wb(2048, H) + lin(8192, H) +
                  bqz(4096, 256) + wb(H, 4096) + lin(H, 4096, 16) + mlp)
     full_b = (nq(H) + wb(8192, H) + wb(1024, H) + lin(9216, H) + bqz(8192, 512) +

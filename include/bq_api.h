@@ -327,6 +327,45 @@ int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
                                uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
                                int hidden, int inter, int block, void* stream);
 
+/* The decoder layer's FFN gate/up: bq_moe_phase1_gate_up_quant (no bf16
+ * bucket) plus the dense MLP's gate/up of the same seq_len tokens
+ * (modeling/gemma_4_moe_bq.mojo:755-769: dispatch_bq_linear of gate and of
+ * up on dense_x_i8 / dense_x_sa, dispatch_gelu_gate_up, then
+ * dispatch_bq_block_quant[64, apply_fwht=True]).  dense_i8 [seq_len,
+ * dense_inter] and dense_sa [seq_len, dense_inter / 64] equal
+ * bq_block_quant(bf16(gelu_tanh(bf16(gate)) * bf16(up)), 64, FWHT) with gate
+ * and up the bq_linear outputs (kernels/elementwise.mojo:17-27).  dense_gate
+ * and dense_up are [dense_inter, hidden] per-row (B = 128) weights.  While
+ * the experts use the 16-row kernel (few routes per expert) the dense rows
+ * are more workgroups of its launch; otherwise they are a launch of their
+ * own after the experts'.  The checks of bq_moe_phase1_gate_up_quant apply;
+ * dense_inter % 64 == 0; dense_x_i8, dense_gate, dense_up 16-byte, dense_i8
+ * 8-byte, dense_sa 4-byte aligned. */
+int bq_ffn_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
+                   const bq_route* routes, const int8_t* w_gate_up, const float* gate_up_scale,
+                   int8_t* bucket_i8, float* bucket_sa, int experts_per_rank, int seq_len,
+                   int top_k, int hidden, int inter, const int8_t* dense_x_i8,
+                   const float* dense_x_sa, const int8_t* dense_gate,
+                   const float* dense_gate_scale, const int8_t* dense_up,
+                   const float* dense_up_scale, int dense_inter, int8_t* dense_i8,
+                   float* dense_sa, void* stream);
+
+/* The decoder layer's FFN down: bq_moe_phase2_down plus the dense MLP's down
+ * projection of the same seq_len tokens (gemma_4_moe_bq.mojo:774-778:
+ * dispatch_bq_block_linear of dense_i8 / dense_sa, per-block activations of
+ * the same block): dense_out [seq_len, hidden] bf16 = bq_block_linear(
+ * dense_i8, dense_sa, dense_down, block).  dense_down is [hidden,
+ * dense_inter].  While the experts use the 16-row kernel the dense rows are
+ * more workgroups of its launch; otherwise a launch of their own.  The checks
+ * of bq_moe_phase2_down apply; dense_inter % block == 0, dense_inter / block
+ * <= 64; dense_i8 and dense_down 16-byte, dense_out 8-byte aligned. */
+int bq_ffn_down(const int8_t* bucket_i8, const float* bucket_sa, const int32_t* expert_offset,
+                const bq_route* routes, const int8_t* w_down, const float* down_scale,
+                float* moe_accum, uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
+                int hidden, int inter, int block, const int8_t* dense_i8, const float* dense_sa,
+                const int8_t* dense_down, const float* dense_down_scale, int dense_inter,
+                uint16_t* dense_out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- vocabulary head and embedding ----------------------------------------- */
 
 #define BQ_SAMPLE_NMAX 256 /* continuous_batching/schedule.mojo:9 MAXIMUM_SAMPLING_LOGITS */

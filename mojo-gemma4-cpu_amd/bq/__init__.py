@@ -75,6 +75,8 @@ SIGNATURES = {
                            _vp, _sz, _vp],
     "bq_moe_phase2_down_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                    _i, _vp],
+    "bq_ffn_gate_up": [_vp] * 8 + [_i] * 5 + [_vp] * 6 + [_i] + [_vp] * 3,
+    "bq_ffn_down": [_vp] * 8 + [_i] * 6 + [_vp] * 4 + [_i, _vp, _vp, _sz, _vp],
 }
 _RESTYPES = {"bq_last_error": C.c_char_p, "bq_version": C.c_char_p,
              "bq_moe_phase2_workspace_size": C.c_size_t,
@@ -559,6 +561,58 @@ def moe_phase2_noalloc(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: 
                                            _p(w_d.scale), _p(accum), _p(o), experts, seq_len,
                                            top_k, hidden, inter, block, _stream()))
     return accum, o
+
+
+def ffn_gate_up(x_i8, x_sa, eo, routes, w_gu: ButterquantWeight, experts: int, seq_len: int,
+                top_k: int, inter: int, dense_x_i8, dense_x_sa, dense_gate: ButterquantWeight,
+                dense_up: ButterquantWeight, out=None):
+    """bq_ffn_gate_up: moe_phase1_quant plus the dense MLP's gate/up, GELU and
+    FWHT64 block-quant of the same tokens in the experts' launch ->
+    (bucket_i8, bucket_sa, dense_i8, dense_sa)."""
+    hidden = x_i8.shape[1]
+    dev = x_i8.device
+    R, di = seq_len * top_k, dense_gate.n_rows
+    if dense_up.n_rows != di or dense_gate.k != hidden or dense_up.k != hidden:
+        raise ValueError("dense gate and up must both be [dense_inter, hidden]")
+    if out is None:
+        bi8 = torch.empty((R, inter), dtype=torch.int8, device=dev)
+        bsa = torch.empty((R, inter // 64), dtype=torch.float32, device=dev)
+        dq = torch.empty((seq_len, di), dtype=torch.int8, device=dev)
+        dsa = torch.empty((seq_len, di // 64), dtype=torch.float32, device=dev)
+    else:
+        bi8, bsa, dq, dsa = out
+    _check(_lib.bq_ffn_gate_up(_p(x_i8), _p(x_sa), _p(eo), _p(routes), _p(w_gu.data),
+                               _p(w_gu.scale), _p(bi8), _p(bsa), experts, seq_len, top_k, hidden,
+                               inter, _p(dense_x_i8), _p(dense_x_sa), _p(dense_gate.data),
+                               _p(dense_gate.scale), _p(dense_up.data), _p(dense_up.scale), di,
+                               _p(dq), _p(dsa), _stream()))
+    return bi8, bsa, dq, dsa
+
+
+def ffn_down(b_i8, b_sa, eo, routes, w_d: ButterquantWeight, experts: int, seq_len: int,
+             top_k: int, hidden: int, dense_i8, dense_sa, dense_down: ButterquantWeight,
+             block: int = 64, workspace=None, out=None):
+    """bq_ffn_down: moe_phase2 plus the dense MLP's per-block down projection
+    of the same tokens in the experts' launch -> (accum, out, dense_out)."""
+    inter = b_i8.shape[1]
+    dev = b_i8.device
+    if dense_down.n_rows != hidden or dense_down.k != dense_i8.shape[1]:
+        raise ValueError("dense down must be [hidden, dense_inter]")
+    if workspace is None:
+        nbytes = max(moe_phase2_workspace_size(seq_len, top_k, hidden), 256)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if out is None:
+        accum = torch.empty((seq_len, hidden), dtype=torch.float32, device=dev)
+        o = torch.empty((seq_len, hidden), dtype=torch.bfloat16, device=dev)
+        do = torch.empty((seq_len, hidden), dtype=torch.bfloat16, device=dev)
+    else:
+        accum, o, do = out
+    _check(_lib.bq_ffn_down(_p(b_i8), _p(b_sa), _p(eo), _p(routes), _p(w_d.data), _p(w_d.scale),
+                            _p(accum), _p(o), experts, seq_len, top_k, hidden, inter, block,
+                            _p(dense_i8), _p(dense_sa), _p(dense_down.data),
+                            _p(dense_down.scale), dense_down.k, _p(do), _p(workspace),
+                            workspace.numel(), _stream()))
+    return accum, o, do
 
 
 # --------------------------------------------------------------------------

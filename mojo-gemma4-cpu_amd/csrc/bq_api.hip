@@ -597,6 +597,89 @@ int bq_moe_phase2_down(const int8_t* bucket_i8, const float* bucket_sa,
                                          S(stream)), "moe_phase2");
 }
 
+int bq_ffn_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
+                   const bq_route* routes, const int8_t* w_gate_up, const float* gate_up_scale,
+                   int8_t* bucket_i8, float* bucket_sa, int experts_per_rank, int seq_len,
+                   int top_k, int hidden, int inter, const int8_t* dense_x_i8,
+                   const float* dense_x_sa, const int8_t* dense_gate,
+                   const float* dense_gate_scale, const int8_t* dense_up,
+                   const float* dense_up_scale, int dense_inter, int8_t* dense_i8,
+                   float* dense_sa, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  if (!x_i8 || !x_sa || !expert_offset || !routes || !w_gate_up || !gate_up_scale ||
+      !bucket_i8 || !bucket_sa || !dense_x_i8 || !dense_x_sa || !dense_gate ||
+      !dense_gate_scale || !dense_up || !dense_up_scale || !dense_i8 || !dense_sa)
+    return fail(BQ_ERR_INVALID, "bq_ffn_gate_up: null pointer");
+  if (experts_per_rank <= 0 || top_k <= 0 || hidden <= 0 || hidden % 64 || inter <= 0 ||
+      inter % 64 || dense_inter <= 0 || dense_inter % 64)
+    return fail(BQ_ERR_SHAPE, "bq_ffn_gate_up: need hidden, inter and dense_inter multiples of 64");
+  if (!a16(x_i8) || !a16(w_gate_up) || (reinterpret_cast<uintptr_t>(bucket_i8) & 7u) ||
+      (reinterpret_cast<uintptr_t>(bucket_sa) & 3u) || !a16(dense_x_i8) || !a16(dense_gate) ||
+      !a16(dense_up) || (reinterpret_cast<uintptr_t>(dense_i8) & 7u) ||
+      (reinterpret_cast<uintptr_t>(dense_sa) & 3u))
+    return fail(BQ_ERR_INVALID, "bq_ffn_gate_up: x_i8, w_gate_up, dense_x_i8, dense_gate, dense_up "
+                                "must be 16-byte, bucket_i8 and dense_i8 8-byte, the scales "
+                                "4-byte aligned");
+  bq::DenseGateUp dn{};
+  dn.wg = dense_gate;
+  dn.wu = dense_up;
+  dn.sg = dense_gate_scale;
+  dn.su = dense_up_scale;
+  dn.x_i8 = dense_x_i8;
+  dn.x_sa = dense_x_sa;
+  dn.out_i8 = dense_i8;
+  dn.out_sa = dense_sa;
+  dn.T = seq_len;
+  dn.inter = dense_inter;
+  return check_hip(bq::launch_moe_phase1(x_i8, x_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_gate_up,
+                                         gate_up_scale, nullptr, bucket_i8, bucket_sa,
+                                         experts_per_rank, seq_len * top_k, hidden, inter,
+                                         S(stream), &dn),
+                   "ffn_gate_up");
+}
+
+int bq_ffn_down(const int8_t* bucket_i8, const float* bucket_sa, const int32_t* expert_offset,
+                const bq_route* routes, const int8_t* w_down, const float* down_scale,
+                float* moe_accum, uint16_t* moe_out, int experts_per_rank, int seq_len, int top_k,
+                int hidden, int inter, int block, const int8_t* dense_i8, const float* dense_sa,
+                const int8_t* dense_down, const float* dense_down_scale, int dense_inter,
+                uint16_t* dense_out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (seq_len <= 0) return BQ_OK;
+  const int r = phase2_args("bq_ffn_down", bucket_i8, bucket_sa, expert_offset, routes, w_down,
+                            down_scale, moe_accum, moe_out, top_k, hidden, inter, block);
+  if (r != BQ_OK) return r;
+  if (!workspace || !dense_i8 || !dense_sa || !dense_down || !dense_down_scale || !dense_out)
+    return fail(BQ_ERR_INVALID, "bq_ffn_down: null pointer");
+  if (dense_inter <= 0 || dense_inter % 64 || dense_inter % block)
+    return fail(BQ_ERR_SHAPE, "bq_ffn_down: dense_inter %d must be a multiple of 64 and of block %d",
+                dense_inter, block);
+  if (dense_inter / block > 64)
+    return fail(BQ_ERR_UNSUPPORTED, "bq_ffn_down: dense_inter/block = %d > 64", dense_inter / block);
+  if (!a16(dense_i8) || !a16(dense_down) || (reinterpret_cast<uintptr_t>(dense_out) & 7u))
+    return fail(BQ_ERR_INVALID, "bq_ffn_down: dense_i8 and dense_down must be 16-byte, dense_out "
+                                "8-byte aligned");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(BQ_ERR_INVALID, "bq_ffn_down: workspace must be 256-byte aligned");
+  const size_t need = bq::moe_phase2_workspace(seq_len * top_k, seq_len, hidden);
+  if (workspace_bytes < need)
+    return fail(BQ_ERR_SHAPE, "bq_ffn_down: workspace %zu < %zu bytes", workspace_bytes, need);
+  bq::DenseDown dn{};
+  dn.w = dense_down;
+  dn.ws = dense_down_scale;
+  dn.x_i8 = dense_i8;
+  dn.x_sa = dense_sa;
+  dn.out = dense_out;
+  dn.T = seq_len;
+  dn.inter = dense_inter;
+  return check_hip(bq::launch_moe_phase2(bucket_i8, bucket_sa, expert_offset,
+                                         reinterpret_cast<const bq::Route*>(routes), w_down,
+                                         down_scale, moe_accum, moe_out, experts_per_rank, seq_len,
+                                         seq_len * top_k, hidden, inter, block, workspace,
+                                         S(stream), &dn),
+                   "ffn_down");
+}
+
 int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
                                const int32_t* expert_offset, const bq_route* routes,
                                const int8_t* w_down, const float* down_scale, float* moe_accum,

@@ -156,18 +156,49 @@ hipError_t launch_moe_prep(const float* logits, const uint16_t* pes, const uint1
 hipError_t launch_build_schedule(const int32_t* route_idx, const float* route_w, int seq_len,
                                  int top_k, int expert_base, int experts, int32_t* expert_offset,
                                  Route* routes, hipStream_t st);
+// The decoder layer's dense MLP carried by the MoE launches (bq_ffn_gate_up,
+// bq_ffn_down): T tokens' gate and up projections (per-row weights, the
+// linears' bf16 outputs, GELU-tanh(gate) * up, FWHT64 block-quant) in extra
+// workgroups of the MoE gate/up launch, and their down projection (per-block
+// activations, bf16 out) in extra workgroups of the MoE down launch.
+struct DenseGateUp {
+  const int8_t* wg;    // gate [inter, hidden], tile16x64
+  const int8_t* wu;    // up [inter, hidden], tile16x64
+  const float* sg;     // gate per-row scales [inter]
+  const float* su;     // up per-row scales [inter]
+  const int8_t* x_i8;  // [T, hidden]
+  const float* x_sa;   // [T]
+  int8_t* out_i8;      // [T, inter]
+  float* out_sa;       // [T, inter / 64]
+  int T, inter;
+  int ytiles, cpg, gx;  // the launcher's: grid rows taken, 64-column chunks per row, grid x
+};
+struct DenseDown {
+  const int8_t* w;     // down [hidden, inter], tile16x64
+  const float* ws;     // per-row scales [hidden]
+  const int8_t* x_i8;  // [T, inter]
+  const float* x_sa;   // [T, inter / block]
+  uint16_t* out;       // [T, hidden] bf16
+  int T, inter;
+  int ytiles;          // the launcher's: grid rows taken
+};
 // bi8 / bsa non-null: the bucket's FWHT64 block-quant fused into the
-// epilogue (bucket may then be null); inter % 64 == 0 for that
+// epilogue (bucket may then be null); inter % 64 == 0 for that.  dn: the
+// dense MLP's gate/up in the same launch (bi8 required, dn->inter % 64 == 0).
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
                              const Route* routes, const int8_t* w_gu, const float* gu_scale,
                              uint16_t* bucket, int8_t* bi8, float* bsa, int experts,
-                             int max_routes, int hidden, int inter, hipStream_t st);
+                             int max_routes, int hidden, int inter, hipStream_t st,
+                             const DenseGateUp* dn = nullptr);
 size_t moe_phase2_workspace(int max_routes, int seq_len, int hidden);
+// dn: the dense MLP's down projection in the down launch (dn->inter % block
+// == 0, dn->inter / block <= 64)
 hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa,
                              const int32_t* expert_offset, const Route* routes,
                              const int8_t* w_down, const float* down_scale, float* accum,
                              uint16_t* out, int experts, int seq_len, int max_routes, int hidden,
-                             int inter, int block, void* workspace, hipStream_t st);
+                             int inter, int block, void* workspace, hipStream_t st,
+                             const DenseDown* dn = nullptr);
 
 // int8-KV attention (bq_attn.hip)
 struct KvRun {  // kernels/attention_ops.mojo:54-58 KVRun

@@ -140,7 +140,11 @@ __global__ __launch_bounds__(kSchedSmallSlots) void k_build_schedule_small(
 // Phase 1: blockIdx.y = m-tile, blockIdx.x = group of 4 intermediate subtiles
 // (64 columns).  With bi8 the workgroup's 16 x 64 bf16 bucket block goes
 // through LDS to the fused FWHT64 block-quant (inter % 64 == 0: no wave of
-// the group is idle).
+// the group is idle).  The first dn.ytiles rows of the grid are the dense
+// MLP's (16 tokens x 64 columns of its gate and up each): the same products,
+// with the dense linears' bf16 rounding of gate and up before the GELU
+// (gemma_4_moe_bq.mojo:755-769: two dispatch_bq_linear, dispatch_gelu_gate_up,
+// dispatch_bq_block_quant[64, True]).
 template <int U>
 // (the scalars the m-tile lookup and the first addresses need come first:
 // the dispatch preloads the first 14 argument dwords into SGPRs)
@@ -149,29 +153,51 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
     const Route* __restrict__ routes, const int8_t* __restrict__ w_gu,
     const int8_t* __restrict__ x_i8, const float* __restrict__ gu_scale,
     const float* __restrict__ x_sa, uint16_t* __restrict__ bucket, int8_t* __restrict__ bi8,
-    float* __restrict__ bsa, float fwht64) {
+    float* __restrict__ bsa, float fwht64, DenseGateUp dn) {
   __shared__ __attribute__((aligned(16))) uint16_t qtile[16 * 64];
-  int e, r0, r1;
-  if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
-  const int isub = blockIdx.x * 4 + wave;
-  if (isub * 16 >= inter) return;  // never with bi8 (inter % 64 == 0)
   const int K = hidden, K64 = K >> 6;
-  const size_t gate_up = (size_t)2 * inter;
-  const int8_t* we = w_gu + (size_t)e * gate_up * K;
-  const int8_t* wg = we + (size_t)isub * K64 * 1024 + lane * 16;
-  const int8_t* wu = we + (size_t)((inter >> 4) + isub) * K64 * 1024 + lane * 16;
+  const bool dense = (int)blockIdx.y < dn.ytiles;  // uniform
+  int r0, r1, grp = blockIdx.x, n_inter = inter;
+  const int8_t *wg, *wu, *xa;
+  const float *sg, *su, *xs;
+  int8_t* oq;
+  float* os;
+  if (dense) {
+    const int ty = blockIdx.y / dn.cpg;
+    grp = ((int)blockIdx.y - ty * dn.cpg) * dn.gx + blockIdx.x;
+    if (grp * 64 >= dn.inter) return;  // whole workgroup
+    r0 = ty * 16;
+    r1 = min(dn.T, r0 + 16);
+    n_inter = dn.inter;
+    wg = dn.wg; wu = dn.wu; sg = dn.sg; su = dn.su;
+    xa = dn.x_i8; xs = dn.x_sa; oq = dn.out_i8; os = dn.out_sa;
+  } else {
+    int e;
+    if (!find_mtile(eo, E, 16, blockIdx.y - dn.ytiles, max_routes, e, r0, r1)) return;
+    const size_t gate_up = (size_t)2 * inter;
+    wg = w_gu + (size_t)e * gate_up * K;
+    wu = wg + (size_t)inter * K;  // the up rows follow the expert's inter gate rows
+    sg = gu_scale + (size_t)e * gate_up;
+    su = sg + inter;
+    xa = x_i8; xs = x_sa; oq = bi8; os = bsa;
+  }
+  const int isub = grp * 4 + wave;
+  if (isub * 16 >= n_inter) return;  // never with bi8 (inter % 64 == 0)
+  // a record's token: its route's for the experts, the record itself for the dense MLP
+  auto tok = [&](int rec) { return dense ? rec : routes[rec].token; };
+  const int8_t* wgp = wg + (size_t)isub * K64 * 1024 + lane * 16;
+  const int8_t* wup = wu + (size_t)isub * K64 * 1024 + lane * 16;
   const int arow = r0 + (lane & 15);
-  const int8_t* ab = x_i8 + (size_t)routes[arow < r1 ? arow : r0].token * K + (lane >> 4) * 16;
+  const int8_t* ab = xa + (size_t)tok(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
   // epilogue operands
-  const float* ws = gu_scale + (size_t)e * gate_up;
   const int col = isub * 16 + (lane & 15);
-  const float wsg = ws[col], wsu = ws[inter + col];
+  const float wsg = sg[col], wsu = su[col];
   float ad[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int rec = r0 + 4 * (lane >> 4) + v;
-    ad[v] = x_sa[routes[rec < r1 ? rec : r0].token] * kInv127;
+    ad[v] = xs[tok(rec < r1 ? rec : r0)] * kInv127;
   }
   const v4i zero = {0, 0, 0, 0};
   v4i cg = zero, cu = zero;
@@ -180,8 +206,8 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kt = min(c * U + u, K64 - 1);
-      bg[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wg + (size_t)kt * 1024));
-      bu[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wu + (size_t)kt * 1024));
+      bg[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wgp + (size_t)kt * 1024));
+      bu[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wup + (size_t)kt * 1024));
       af[s][u] = ld16(ab + kt * 64);
     }
   };
@@ -208,13 +234,17 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   for (int v = 0; v < 4; ++v) {
     const int rec = r0 + 4 * (lane >> 4) + v;
     if (rec >= r1) continue;
-    const float gv = (float)g4[v] * ad[v] * wsg;
-    const float uv = (float)u4[v] * ad[v] * wsu;
+    float gv = (float)g4[v] * ad[v] * wsg;
+    float uv = (float)u4[v] * ad[v] * wsu;
+    if (dense) {  // the dense linears write bf16 gate and up
+      gv = bf16_to_f32(f32_to_bf16(gv));
+      uv = bf16_to_f32(f32_to_bf16(uv));
+    }
     const uint16_t hb = f32_to_bf16(gelu_tanh_f32(gv) * uv);
-    if (bi8) qtile[(rec - r0) * 64 + wave * 16 + (lane & 15)] = hb;
+    if (oq) qtile[(rec - r0) * 64 + wave * 16 + (lane & 15)] = hb;
     else bucket[(size_t)rec * inter + col] = hb;
   }
-  if (!bi8) return;  // uniform
+  if (!oq) return;  // uniform
   __syncthreads();
   // 16 records x one 64-column block: 8 lanes per record (waves 0 and 1)
   if (wave >= 2) return;
@@ -225,11 +255,11 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   uint32_t w[2];
   const float m = block_quant_lanes<8>(v, true, fwht64, w);
   if (r0 + r < r1) {
-    const size_t rec = (size_t)(r0 + r), c0 = (size_t)blockIdx.x * 64 + i * 8;
+    const size_t rec = (size_t)(r0 + r), c0 = (size_t)grp * 64 + i * 8;
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-    *reinterpret_cast<u2*>(bi8 + rec * inter + c0) = u2{w[0], w[1]};
-    if (i == 0) bsa[rec * (inter / 64) + blockIdx.x] = m;
-    if (bucket) *reinterpret_cast<v4i*>(bucket + rec * inter + c0) = raw;
+    *reinterpret_cast<u2*>(oq + rec * n_inter + c0) = u2{w[0], w[1]};
+    if (i == 0) os[rec * (n_inter / 64) + grp] = m;
+    if (bucket && !dense) *reinterpret_cast<v4i*>(bucket + rec * inter + c0) = raw;
   }
 }
 
@@ -246,21 +276,39 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 // Up to two weight fragments per k-step slot the kernel fits 64 registers,
 // eight waves per SIMD (waves_per_eu(8)): a 16-token batch's 86 experts x 22
 // workgroups then fit in one round on 256 CUs instead of leaving ~100
-// workgroups for a second.
+// workgroups for a second.  The first dn.ytiles rows of the grid are the
+// dense MLP's down projection (16 tokens each, K = dn.inter): the same fma
+// chain over blocks, out = bf16(facc * ws) with no route weight
+// (dispatch_bq_block_linear, gemma_4_moe_bq.mojo:774-778).
 template <int U, int NS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(U * NS <= 2 ? 8 : 1)))
 void k_moe_down_skinny(
     int E, int hidden, int inter, int block, int max_routes, const int32_t* __restrict__ eo,
     const Route* __restrict__ routes, const float* __restrict__ b_sa,
     const int8_t* __restrict__ w_d, const int8_t* __restrict__ b_i8,
-    const float* __restrict__ d_scale, float* __restrict__ y) {
+    const float* __restrict__ d_scale, float* __restrict__ y, DenseDown dn) {
   __shared__ float s_sa[16 * 64];
-  int e, r0, r1;
-  if (!find_mtile(eo, E, 16, blockIdx.y, max_routes, e, r0, r1)) return;  // whole workgroup
-  const int K = inter, K64 = K >> 6, fpb = block >> 6, nb = K / block;
+  const bool dense = (int)blockIdx.y < dn.ytiles;  // uniform
+  int r0, r1, K;
+  const int8_t *wbase, *xa;
+  const float *dsc, *xsa;
+  if (dense) {
+    r0 = blockIdx.y * 16;
+    r1 = min(dn.T, r0 + 16);
+    K = dn.inter;
+    wbase = dn.w; dsc = dn.ws; xa = dn.x_i8; xsa = dn.x_sa;
+  } else {
+    int e;
+    if (!find_mtile(eo, E, 16, blockIdx.y - dn.ytiles, max_routes, e, r0, r1)) return;  // whole workgroup
+    K = inter;
+    wbase = w_d + (size_t)e * hidden * K;
+    dsc = d_scale + (size_t)e * hidden;
+    xa = b_i8; xsa = b_sa;
+  }
+  const int K64 = K >> 6, fpb = block >> 6, nb = K / block;
   for (int i = threadIdx.x; i < 16 * nb; i += 256) {  // 256-thread blocks
     const int row = r0 + i / nb;
-    s_sa[i] = b_sa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
+    s_sa[i] = xsa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
   }
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
@@ -272,15 +320,14 @@ void k_moe_down_skinny(
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int ns = min(nsub0 + j, nstrips - 1);  // a strip past the end is never stored
-    wb[j] = w_d + (size_t)e * hidden * K + (size_t)ns * K64 * 1024 + lane * 16;
+    wb[j] = wbase + (size_t)ns * K64 * 1024 + lane * 16;
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      wsc[j][v] = d_scale[(size_t)e * hidden + ns * 16 + 4 * (lane >> 4) + v];
+    for (int v = 0; v < 4; ++v) wsc[j][v] = dsc[ns * 16 + 4 * (lane >> 4) + v];
   }
   // this lane's record: its activation fragment row and its result row
   const int arow = r0 + (lane & 15);
-  const int8_t* ab = b_i8 + (size_t)(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
-  const float rw = routes[arow < r1 ? arow : r0].weight;
+  const int8_t* ab = xa + (size_t)(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
+  const float rw = dense ? 1.0f : routes[arow < r1 ? arow : r0].weight;
   const v4i zero = {0, 0, 0, 0};
   float facc[NS][4];
   v4i c[NS];
@@ -336,9 +383,18 @@ void k_moe_down_skinny(
   for (int j = 0; j < NS; ++j) {
     if (nsub0 + j >= nstrips) continue;
     const int col = (nsub0 + j) * 16 + 4 * (lane >> 4);
-    *reinterpret_cast<float4*>(&y[(size_t)arow * hidden + col]) =
-        float4{facc[j][0] * wsc[j][0] * rw, facc[j][1] * wsc[j][1] * rw,
-               facc[j][2] * wsc[j][2] * rw, facc[j][3] * wsc[j][3] * rw};
+    if (dense) {
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      const uint32_t lo = (uint32_t)f32_to_bf16(facc[j][0] * wsc[j][0]) |
+                          ((uint32_t)f32_to_bf16(facc[j][1] * wsc[j][1]) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(facc[j][2] * wsc[j][2]) |
+                          ((uint32_t)f32_to_bf16(facc[j][3] * wsc[j][3]) << 16);
+      *reinterpret_cast<u2*>(dn.out + (size_t)arow * hidden + col) = u2{lo, hi};
+    } else {
+      *reinterpret_cast<float4*>(&y[(size_t)arow * hidden + col]) =
+          float4{facc[j][0] * wsc[j][0] * rw, facc[j][1] * wsc[j][1] * rw,
+                 facc[j][2] * wsc[j][2] * rw, facc[j][3] * wsc[j][3] * rw};
+    }
   }
 }
 
@@ -458,19 +514,38 @@ int moe_tile_bm(int max_routes, int experts) {
 hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_t* eo,
                              const Route* routes, const int8_t* w_gu, const float* gu_scale,
                              uint16_t* bucket, int8_t* bi8, float* bsa, int experts,
-                             int max_routes, int hidden, int inter, hipStream_t st) {
-  if (max_routes <= 0) return hipSuccess;
+                             int max_routes, int hidden, int inter, hipStream_t st,
+                             const DenseGateUp* dense) {
+  const bool has_dense = dense && dense->T > 0;
+  if (max_routes <= 0 && !has_dense) return hipSuccess;
   if (bi8 && inter % 64) return hipErrorInvalidValue;
-  const int bm = moe_tile_bm(max_routes, experts);
-  if (bm >= 64 && inter % 64 == 0)
-    return launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket, bi8, bsa,
-                                    experts, max_routes, hidden, inter, bm, st);
-  dim3 g((inter / 16 + 3) / 4, mtile_bound(max_routes, experts, 16)), b(256);
+  if (has_dense && (!bi8 || dense->inter <= 0 || dense->inter % 64)) return hipErrorInvalidValue;
+  const int gx = (inter / 16 + 3) / 4;
+  DenseGateUp dn{};  // ytiles 0: no dense rows
+  if (has_dense) {
+    dn = *dense;
+    dn.gx = gx;
+    dn.cpg = (dn.inter / 64 + gx - 1) / gx;
+    dn.ytiles = (dn.T + 15) / 16 * dn.cpg;
+  }
+  int E = experts, moe_rows = max_routes > 0 ? mtile_bound(max_routes, experts, 16) : 0;
+  if (max_routes > 0) {
+    const int bm = moe_tile_bm(max_routes, experts);
+    if (bm >= 64 && inter % 64 == 0) {
+      const hipError_t r = launch_moe_gate_up_tiled(x_i8, x_sa, eo, routes, w_gu, gu_scale, bucket,
+                                                    bi8, bsa, experts, max_routes, hidden, inter,
+                                                    bm, st);
+      if (r != hipSuccess || !has_dense) return r;
+      E = 0;  // the dense rows in a skinny launch of their own
+      moe_rows = 0;
+    }
+  }
+  dim3 g(gx, dn.ytiles + moe_rows), b(256);
 #define BQ_GU(U)                                                                                  \
   case U:                                                                                         \
-    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, experts, hidden, inter, max_routes,  \
-                       eo, routes, w_gu, x_i8, gu_scale, x_sa, bucket, bi8, bsa,                  \
-                       fwht_scale_host(64));                                                      \
+    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, E, hidden, inter, max_routes, eo,    \
+                       routes, w_gu, x_i8, gu_scale, x_sa, bucket, bi8, bsa,                      \
+                       fwht_scale_host(64), dn);                                                  \
     break;
   switch (tune().gu_skinny) {  // 2 or 6 k-steps per register slot; 4 measured best
     BQ_GU(2) BQ_GU(6)
@@ -491,9 +566,36 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                              const Route* routes, const int8_t* w_down, const float* down_scale,
                              float* accum, uint16_t* out, int experts, int seq_len,
                              int max_routes, int hidden, int inter, int block, void* workspace,
-                             hipStream_t st) {
+                             hipStream_t st, const DenseDown* dense) {
   if (seq_len <= 0) return hipSuccess;
+  const bool has_dense = dense && dense->T > 0;
+  DenseDown dn{};  // ytiles 0: no dense rows
+  if (has_dense) {
+    if (dense->inter <= 0 || dense->inter % 64 || dense->inter % block || dense->inter / block > 64)
+      return hipErrorInvalidValue;
+    dn = *dense;
+    dn.ytiles = (dn.T + 15) / 16;
+  }
   float* y = (float*)workspace;
+  // one k-step per register slot and two strips per wave (57 VGPRs, eight
+  // waves per SIMD; BQ_DOWN_SKINNY): the 32-token layer 127.6 us against
+  // 128.0-130.6 us for 1-4 k-steps x 1-4 strips
+  auto skinny = [&](int E, int moe_rows) {
+#define BQ_DS(U, NS)                                                                              \
+  case U * 10 + NS: {                                                                             \
+    dim3 g((hidden / 16 + 4 * NS - 1) / (4 * NS), dn.ytiles + moe_rows), b(256);                 \
+    hipLaunchKernelGGL((k_moe_down_skinny<U, NS>), g, b, 0, st, E, hidden, inter, block,          \
+                       max_routes, eo, routes, bucket_sa, w_down, bucket_i8, down_scale, y, dn);  \
+    break;                                                                                        \
+  }
+    switch (tune().down_skinny) {
+      BQ_DS(2, 2) BQ_DS(1, 4) BQ_DS(2, 1)
+      default: BQ_DS(1, 2)
+    }
+#undef BQ_DS
+    return hipGetLastError();
+  };
+  bool dense_done = !has_dense;
   if (max_routes > 0) {
     const int bm = moe_tile_bm(max_routes, experts);
     if (bm >= 64 && hidden % 128 == 0) {
@@ -503,23 +605,14 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
                                            experts, max_routes, hidden, inter, block, bm_down, st);
       if (e != hipSuccess) return e;
     } else {
-      // one k-step per register slot and two strips per wave (57 VGPRs, eight
-      // waves per SIMD; BQ_DOWN_SKINNY): the 32-token layer 127.6 us against
-      // 128.0-130.6 us for 1-4 k-steps x 1-4 strips
-      const int ut = tune().down_skinny;
-#define BQ_DS(U, NS)                                                                              \
-  case U * 10 + NS: {                                                                             \
-    dim3 g((hidden / 16 + 4 * NS - 1) / (4 * NS), mtile_bound(max_routes, experts, 16)), b(256); \
-    hipLaunchKernelGGL((k_moe_down_skinny<U, NS>), g, b, 0, st, experts, hidden, inter, block,    \
-                       max_routes, eo, routes, bucket_sa, w_down, bucket_i8, down_scale, y);      \
-    break;                                                                                        \
-  }
-      switch (ut) {
-        BQ_DS(2, 2) BQ_DS(1, 4) BQ_DS(2, 1)
-        default: BQ_DS(1, 2)
-      }
-#undef BQ_DS
+      const hipError_t e = skinny(experts, mtile_bound(max_routes, experts, 16));
+      if (e != hipSuccess) return e;
+      dense_done = true;
     }
+  }
+  if (!dense_done) {  // the dense rows in a skinny launch of their own
+    const hipError_t e = skinny(0, 0);
+    if (e != hipSuccess) return e;
   }
   // below 256 tokens each workgroup takes 256 columns of its token (32
   // tokens: 32 workgroups -> 352, the layer ~130 -> 128.7 us), else the

@@ -307,6 +307,16 @@ def gelu_tanh(x: np.ndarray) -> np.ndarray:
     return np.array([f(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))
 
 
+def gelu_gate_up(gate_bf16: np.ndarray, up_bf16: np.ndarray) -> np.ndarray:
+    """gelu_gate_up_row (kernels/elementwise.mojo:17-27), the dense MLP's step
+    between its gate/up linears and the FWHT64 block-quant
+    (modeling/gemma_4_moe_bq.mojo:763-764): bf16(gelu_tanh_f32(f32(gate)) *
+    f32(up)) elementwise."""
+    g = bf16_to_f32(_c(gate_bf16, np.uint16))
+    u = bf16_to_f32(_c(up_bf16, np.uint16))
+    return f32_to_bf16((gelu_tanh(g) * u).astype(np.float32))
+
+
 def exp_fast(x):
     f = lib().bqo_exp_f32_fast
     return np.array([f(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))

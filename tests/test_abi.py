@@ -103,6 +103,23 @@ def test_validation_errors(L):
     assert fprep(4, 128, 8, 2880, 128, *([P] * 8)) == 2                  # hidden % block
     assert L.bq_ffn_prep(P, None, P, P, None, 4, 128, 8, 2816, 128, f1, f1, *([P] * 8),
                          None) == 1                                       # null dense gain
+    # bq_ffn_gate_up: bq_moe_phase1_gate_up_quant's checks plus the dense MLP's
+    fgu = lambda E, T, k, H, I, DI, *dense: L.bq_ffn_gate_up(*([P] * 8), E, T, k, H, I, *dense,
+                                                           DI, P, P, None)
+    assert fgu(128, 0, 8, 2816, 704, 2112, *([None] * 6)) == 0          # empty batch
+    assert fgu(128, 4, 8, 2816, 704, 2112, P, P, P, P, None, P) == 1    # null dense up
+    assert fgu(128, 4, 8, 2816, 704, 2100, *([P] * 6)) == 2             # dense_inter % 64
+    assert fgu(128, 4, 8, 2816, 700, 2112, *([P] * 6)) == 2             # inter % 64
+    assert fgu(128, 4, 8, 2816, 704, 2112, C.c_void_p(24), *([P] * 5)) == 1  # alignment
+    # bq_ffn_down: bq_moe_phase2_down's checks plus the dense MLP's
+    fdn = lambda T, k, H, I, B, DI, *dense: L.bq_ffn_down(*([P] * 8), 128, T, k, H, I, B, *dense,
+                                                          DI, P, C.c_void_p(256), 1 << 30, None)
+    assert fdn(0, 8, 2816, 704, 64, 2112, *([None] * 4)) == 0           # empty batch
+    assert fdn(4, 8, 2816, 704, 64, 2112, P, P, None, P) == 1           # null dense down
+    assert fdn(4, 8, 2816, 704, 64, 2100, *([P] * 4)) == 2              # dense_inter % block
+    assert fdn(4, 8, 2816, 704, 64, 8192, *([P] * 4)) == 4              # dense_inter / block
+    assert fdn(4, 17, 2816, 704, 64, 2112, *([P] * 4)) == 4             # top_k
+    assert fdn(4, 8, 2816, 704, 64, 2112, C.c_void_p(24), P, P, P) == 1  # alignment
     assert L.bq_moe_router_logits(P, P, P, P, 4, 2880 + 32, 128, C.c_float(1), C.c_float(1),
                                   None) == 2
     assert L.bq_moe_router_logits(P, C.c_void_p(18), P, P, 4, 2816, 128, C.c_float(1),

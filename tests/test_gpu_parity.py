@@ -605,6 +605,107 @@ def test_moe_phase1_quant(gpu, O, T, E, k, H, I):
     np.testing.assert_array_equal(host(bsa)[:n], rsa)
 
 
+# (T, E, top_k, hidden, expert inter, dense inter): the experts in the 16-row
+# kernels (T <= 40 here; 1..10 routes per expert) or the LDS-tiled ones (T =
+# 300 over 4 experts); dense_inter narrower than, a multiple of, and not a
+# multiple of the experts' 64-column groups; ragged 16-token tiles
+FFN_CASES = [(1, 8, 2, 1024, 128, 192), (16, 8, 2, 1024, 128, 320), (17, 16, 4, 2816, 128, 256),
+             (40, 8, 2, 1024, 192, 128), (300, 4, 2, 1024, 128, 192)]
+
+
+def _dense_gate_up_ref(O, dq, dsa, qg, sg, qu, su, DI):
+    """oracle chain of the dense MLP up to the down projection's activation:
+    gate and up linears (bf16), gelu_gate_up, FWHT64 block-quant"""
+    pg, cg = O.pack_and_colsum(qg)
+    pu, cu = O.pack_and_colsum(qu)
+    rg, _ = O.linear(dq, dsa, pg, sg, cg, DI)
+    ru, _ = O.linear(dq, dsa, pu, su, cu, DI)
+    return O.block_quant(O.gelu_gate_up(rg, ru), 64, True)
+
+
+@pytest.mark.parametrize("T,E,k,H,I,DI", FFN_CASES)
+def test_ffn_gate_up(gpu, O, T, E, k, H, I, DI):
+    """bq_ffn_gate_up = bq_moe_phase1_gate_up_quant (bit for bit) plus the
+    dense MLP's gate and up linears, GELU-tanh product and FWHT64 block-quant
+    against the oracle, bit-exact; two calls in a row."""
+    import torch
+    idx, w = O.route_topk_softmax(O.synth_normal_f32(T + 5, 1.0, (T, E)), k)
+    _, _, Wgu = weight(gpu, O, E * 2 * I, H, 128, seed=9)
+    ones = np.full(H, ONE, np.uint16)
+    xq, xsa = O.norm_quant(O.synth_normal_bf16(T + 1, 1.0, (T, H)), ones, 128)
+    dq, dsa = O.norm_quant(O.synth_normal_bf16(T + 2, 1.0, (T, H)), ones, 128)
+    (qg, sg, Wg), (qu, su, Wu) = (weight(gpu, O, DI, H, 128, seed=sd) for sd in (21, 22))
+    rdq, rdsa = _dense_gate_up_ref(O, dq, dsa, qg, sg, qu, su, DI)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    mi8, msa = gpu.moe_phase1_quant(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I)
+    n = int(host(eo)[-1])
+    for _ in range(2):
+        bi8, bsa, di8, dsa_ = gpu.ffn_gate_up(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I,
+                                              dev(dq), dev(dsa), Wg, Wu)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(bi8)[:n], host(mi8)[:n])
+        np.testing.assert_array_equal(host(bsa)[:n], host(msa)[:n])
+        np.testing.assert_array_equal(host(di8), rdq)
+        np.testing.assert_array_equal(host(dsa_), rdsa)
+
+
+@pytest.mark.parametrize("T,E,k,H,I,DI", FFN_CASES)
+def test_ffn_down(gpu, O, T, E, k, H, I, DI):
+    """bq_ffn_down = bq_moe_phase2_down (bit for bit) plus the dense MLP's
+    per-block (B = 64) down projection against the oracle's block linear,
+    bit-exact; two calls in a row."""
+    import torch
+    idx, w = O.route_topk_softmax(O.synth_normal_f32(T + 5, 1.0, (T, E)), k)
+    _, _, Wd = weight(gpu, O, E * H, I, 64, seed=11)
+    bi8, bsa = O.block_quant(O.synth_normal_bf16(T + 7, 1.0, (T * k, I)), 64, True)
+    di8, dsa = O.block_quant(O.synth_normal_bf16(T + 8, 1.0, (T, DI)), 64, True)
+    qd, sd, Wdd = weight(gpu, O, H, DI, 64, seed=23)
+    pd, cd = O.pack_and_colsum(qd, 64, False)
+    rdo, _ = O.block_linear(di8, dsa, pd, sd, cd, H, 64)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    macc, mout = gpu.moe_phase2(dev(bi8), dev(bsa), eo, routes, Wd, E, T, k, H)
+    for _ in range(2):
+        acc, out, do = gpu.ffn_down(dev(bi8), dev(bsa), eo, routes, Wd, E, T, k, H, dev(di8),
+                                    dev(dsa), Wdd)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(acc), host(macc))
+        np.testing.assert_array_equal(host(out), host(mout))
+        np.testing.assert_array_equal(host(do), rdo)
+
+
+def test_ffn_model_shape_decode(gpu, O, moe_model):
+    """The batch-16 decoder layer's FFN at the model's shapes (128 experts,
+    top-8, hidden 2816, expert inter 704, dense inter 2112): bq_ffn_gate_up and
+    bq_ffn_down against the separate MoE calls and the oracle's dense chain
+    (gate, up, gelu_gate_up, FWHT64 block-quant, per-block down)."""
+    import torch
+    m = moe_model
+    E, H, I, T, k, DI = m["E"], m["H"], m["I"], 16, 8, 2112
+    ones = np.full(H, ONE, np.uint16)
+    idx, w = route_table(O, T)
+    xq, xsa = O.norm_quant(O.synth_normal_bf16(31, 1.0, (T, H)), ones, 128)
+    dq, dsa = O.norm_quant(O.synth_normal_bf16(32, 1.0, (T, H)), ones, 128)
+    (qg, sg, Wg), (qu, su, Wu) = (weight(gpu, O, DI, H, 128, seed=sd) for sd in (24, 25))
+    qd, sd, Wdd = weight(gpu, O, H, DI, 64, seed=26)
+    rdq, rdsa = _dense_gate_up_ref(O, dq, dsa, qg, sg, qu, su, DI)
+    pd, cd = O.pack_and_colsum(qd, 64, False)
+    rdo, _ = O.block_linear(rdq, rdsa, pd, sd, cd, H, 64)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    mi8, msa = gpu.moe_phase1_quant(dev(xq), dev(xsa), eo, routes, m["Wgu"], E, T, k, I)
+    macc, mout = gpu.moe_phase2(mi8, msa, eo, routes, m["Wd"], E, T, k, H)
+    bi8, bsa, di8, dsa_ = gpu.ffn_gate_up(dev(xq), dev(xsa), eo, routes, m["Wgu"], E, T, k, I,
+                                          dev(dq), dev(dsa), Wg, Wu)
+    acc, out, do = gpu.ffn_down(bi8, bsa, eo, routes, m["Wd"], E, T, k, H, di8, dsa_, Wdd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(bi8), host(mi8))
+    np.testing.assert_array_equal(host(bsa), host(msa))
+    np.testing.assert_array_equal(host(di8), rdq)
+    np.testing.assert_array_equal(host(dsa_), rdsa)
+    np.testing.assert_array_equal(host(acc), host(macc))
+    np.testing.assert_array_equal(host(out), host(mout))
+    np.testing.assert_array_equal(host(do), rdo)
+
+
 def test_moe_duplicate_experts(gpu, O):
     """A token that lists an expert more than once (the router pads a token
     with fewer than top_k valid logits with expert 0, moe_router.mojo:266):

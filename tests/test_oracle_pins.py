@@ -16,6 +16,8 @@ Pin map (oracle function -> pins):
   gemm per-row/block  int64 brute force + f64 epilogue closed forms; VNNI
                       (u8, colsum) form == signed form
   exp/tanh/gelu fast  numpy exp/tanh/exact GELU within the stated error
+  gelu_gate_up        up = 1 -> bf16(gelu(gate)); gate = 10 -> 10 * up;
+                      gate = 0 -> 0; exact tanh-GELU product within bf16
   route top-k/softmax numpy stable argsort; weights sum to 1
   build_schedule      python stable sort of (expert, token, k)
   moe phase1/phase2   f64 closed forms over the unpacked weights
@@ -307,6 +309,27 @@ def test_tanh_gelu_closed_forms(O):
     xd = xs[:4801].astype(np.float64)
     exact = 0.5 * xd * (1 + np.tanh(math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)))
     assert (np.abs(g - exact) <= 4e-3 * np.abs(xd) + 1e-6).all()
+
+
+def test_gelu_gate_up_pins(O):
+    """gelu_gate_up (elementwise.mojo:17-27) = bf16(gelu_tanh(gate) * up):
+    with up = 1 it is bf16 of the pinned gelu_tanh of gate alone (a swapped
+    gate/up would give gelu(1) * gate); gate = 10 gives exactly 10 * up
+    (tanh rounds to 1); gate = 0 gives 0; and random operands stay within
+    bf16 rounding of the exact tanh-GELU product."""
+    rng = np.random.default_rng(3)
+    g = O.f32_to_bf16(rng.normal(0, 2, 4096).astype(np.float32))
+    one = np.full(4096, 0x3F80, np.uint16)
+    np.testing.assert_array_equal(O.gelu_gate_up(g, one), O.f32_to_bf16(O.gelu_tanh(O.bf16_to_f32(g))))
+    u = O.f32_to_bf16(rng.normal(0, 1, 4096).astype(np.float32))
+    ten = np.full(4096, O.f32_to_bf16(np.float32([10.0]))[0], np.uint16)
+    np.testing.assert_array_equal(O.gelu_gate_up(ten, u),
+                                  O.f32_to_bf16(np.float32(10.0) * O.bf16_to_f32(u)))
+    assert (O.bf16_to_f32(O.gelu_gate_up(np.zeros(4096, np.uint16), u)) == 0).all()
+    gd, ud = O.bf16_to_f32(g).astype(np.float64), O.bf16_to_f32(u).astype(np.float64)
+    exact = 0.5 * gd * (1 + np.tanh(math.sqrt(2 / math.pi) * (gd + 0.044715 * gd ** 3))) * ud
+    got = O.bf16_to_f32(O.gelu_gate_up(g, u)).astype(np.float64)
+    assert (np.abs(got - exact) <= 1e-2 * np.abs(exact) + 4e-3 * np.abs(gd * ud) + 1e-6).all()
 
 
 def test_softmax_exp_known_values(O):
