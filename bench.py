@@ -699,8 +699,9 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
 
     def full(_i=0):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
-        bq.linear(xq, xsa, fq, out=q_f)
-        bq.linear(xq, xsa, fk, out=k_f)               # k_eq_v: one projection for K and V
+        # q and k (k_eq_v: one projection for K and V), the reference's two
+        # dispatch_bq_linear on one activation, as one bq_linear_pair launch
+        bq.linear_pair(xq, xsa, fq, fk, outs=(q_f, k_f))
         bq.block_quant(attn_f, 512, False, out=(oq_f, osa_f))
         bq.block_linear(oq_f, osa_f, fo, 512, out=o)
         ffn()

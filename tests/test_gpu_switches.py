@@ -5,7 +5,7 @@ paths are covered by the other GPU tests."""
 import numpy as np
 import pytest
 
-from test_gpu_parity import dev, host, weight
+from test_gpu_parity import _dense_gate_up_ref, dev, host, weight
 
 pytestmark = pytest.mark.gpu
 ONE = 0x3F80
@@ -180,6 +180,35 @@ def _moe_check(gpu, O, T, E=8, k=2, H=256, I=128, seed=5):
 def test_moe_skinny_switches(gpu, O, tune_env, sw, T):
     tune_env(**sw)
     _moe_check(gpu, O, T)
+    _ffn_check(gpu, O, T)
+
+
+def _ffn_check(gpu, O, T, E=8, k=2, H=256, I=128, DI=192):
+    """bq_ffn_gate_up / bq_ffn_down: the experts' outputs equal the separate
+    MoE calls', the dense MLP's the oracle chain's (the dense rows ride in
+    the same skinny kernels, so every variant of them is checked)."""
+    idx, w = O.route_topk_softmax(O.synth_normal_f32(T + 9, 1.0, (T, E)), k)
+    _, _, Wgu = weight(gpu, O, E * 2 * I, H, 128, seed=31)
+    _, _, Wd = weight(gpu, O, E * H, I, 64, seed=32)
+    ones = np.full(H, ONE, np.uint16)
+    xq, xsa = O.norm_quant(O.synth_normal_bf16(T + 10, 1.0, (T, H)), ones, 128)
+    dq, dsa = O.norm_quant(O.synth_normal_bf16(T + 11, 1.0, (T, H)), ones, 128)
+    (qg, sg, Wg), (qu, su, Wu) = (weight(gpu, O, DI, H, 128, seed=sd) for sd in (33, 34))
+    qd, sd, Wdd = weight(gpu, O, H, DI, 64, seed=35)
+    rdq, rdsa = _dense_gate_up_ref(O, dq, dsa, qg, sg, qu, su, DI)
+    pd, cd = O.pack_and_colsum(qd, 64, False)
+    rdo, _ = O.block_linear(rdq, rdsa, pd, sd, cd, H, 64)
+    eo, routes = gpu.build_schedule(dev(idx), dev(w), E)
+    mi8, msa = gpu.moe_phase1_quant(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I)
+    macc, mout = gpu.moe_phase2(mi8, msa, eo, routes, Wd, E, T, k, H)
+    bi8, bsa, di8, dsa_ = gpu.ffn_gate_up(dev(xq), dev(xsa), eo, routes, Wgu, E, T, k, I,
+                                          dev(dq), dev(dsa), Wg, Wu)
+    acc, out, do = gpu.ffn_down(bi8, bsa, eo, routes, Wd, E, T, k, H, di8, dsa_, Wdd)
+    for a, b in ((bi8, mi8), (bsa, msa), (acc, macc), (out, mout)):
+        np.testing.assert_array_equal(host(a), host(b))
+    np.testing.assert_array_equal(host(di8), rdq)
+    np.testing.assert_array_equal(host(dsa_), rdsa)
+    np.testing.assert_array_equal(host(do), rdo)
 
 
 @pytest.mark.parametrize("sw", [dict(BQ_MOE_ORDER=1), dict(BQ_MOE_ORDER=2),
