@@ -677,7 +677,9 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     xqd, xsad = e(T, H, dt=torch.int8), e(T, dt=torch.float32)
     od = e(T, H)
 
-    def ffn():
+    base = dict(q=sq, k=sk, v=sv, o=so, fq=fq, fk=fk, fo=fo, dg=dg, du=du, dd=dd, gu=Wgu, d=Wd)
+
+    def ffn(L):
         # routing, schedule and both norm-quants of x (the MoE's gamma and the
         # dense MLP's) in one launch (bq_ffn_prep); the dense MLP's gate/up,
         # GELU and FWHT64 block-quant in the experts' gate/up launch
@@ -685,33 +687,49 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
         # (bq_ffn_down)
         bq.ffn_prep(moe.logits, x, moe.gamma, gamma, TOPK, moe.pes, 128,
                     out=(moe.idx, moe.w, moe.eo, moe.routes, moe.xq, moe.xsa, xqd, xsad))
-        bq.ffn_gate_up(moe.xq, moe.xsa, moe.eo, moe.routes, moe.Wgu, E, T, TOPK, I, xqd, xsad,
-                       dg, du, out=(moe.bi8, moe.bsa, gq_, gsa))
-        bq.ffn_down(moe.bi8, moe.bsa, moe.eo, moe.routes, moe.Wd, E, T, TOPK, H, gq_, gsa, dd,
-                    64, workspace=moe.ws, out=(moe.accum, moe.out, od))
+        bq.ffn_gate_up(moe.xq, moe.xsa, moe.eo, moe.routes, L["gu"], E, T, TOPK, I, xqd, xsad,
+                       L["dg"], L["du"], out=(moe.bi8, moe.bsa, gq_, gsa))
+        bq.ffn_down(moe.bi8, moe.bsa, moe.eo, moe.routes, L["d"], E, T, TOPK, H, gq_, gsa,
+                    L["dd"], 64, workspace=moe.ws, out=(moe.accum, moe.out, od))
 
-    def sliding(_i=0):
+    def sliding_layer(L):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
-        bq.qkv(xq, xsa, sq, sk, sv, outs=(q_s, k_s, v_s))
+        bq.qkv(xq, xsa, L["q"], L["k"], L["v"], outs=(q_s, k_s, v_s))
         bq.block_quant(attn_s, 256, False, out=(oq_s, osa_s))
-        bq.block_linear(oq_s, osa_s, so, 256, out=o)
-        ffn()
+        bq.block_linear(oq_s, osa_s, L["o"], 256, out=o)
+        ffn(L)
 
-    def full(_i=0):
+    def full_layer(L):
         bq.norm_quant(x, gamma, 128, out=(xq, xsa))
         # q and k (k_eq_v: one projection for K and V), the reference's two
         # dispatch_bq_linear on one activation, as one bq_linear_pair launch
-        bq.linear_pair(xq, xsa, fq, fk, outs=(q_f, k_f))
+        bq.linear_pair(xq, xsa, L["fq"], L["fk"], outs=(q_f, k_f))
         bq.block_quant(attn_f, 512, False, out=(oq_f, osa_f))
-        bq.block_linear(oq_f, osa_f, fo, 512, out=o)
-        ffn()
+        bq.block_linear(oq_f, osa_f, L["fo"], 512, out=o)
+        ffn(L)
 
-    gs_ = graph_of(sliding, 1)
+    gs_ = graph_of(lambda _i: sliding_layer(base), 1)
     ms_s = time_graph(gs_, 1, steps, 0).p50
-    gf_ = graph_of(full, 1)
+    gf_ = graph_of(lambda _i: full_layer(base), 1)
     ms_f = time_graph(gf_, 1, steps, 0).p50
     gm_ = graph_of(lambda _i: moe(), 1)
     ms_m = time_graph(gm_, 1, steps, 0).p50
+    del gs_, gf_, gm_
+    # The 30-layer stack as one graph, as a decode step runs it: five sliding
+    # layers then a full one, five times, each layer on device copies of its
+    # own (distinct addresses: no layer finds another's weights in L2 or the
+    # Infinity Cache).  One graph launch per step instead of one per layer.
+    cp = lambda W: bq.ButterquantWeight(W.data.clone(), W.scale.clone(), W.n_rows, W.k)
+    layers = [("f" if j % 6 == 5 else "s", {k: cp(w) for k, w in base.items()
+                                          if k in (("fq", "fk", "fo") if j % 6 == 5 else
+                                                   ("q", "k", "v", "o")) + ("dg", "du", "dd",
+                                                                            "gu", "d")})
+              for j in range(30)]
+    g_st = graph_of(lambda _i: [(sliding_layer if kd == "s" else full_layer)(L)
+                                for kd, L in layers], 1)
+    ms_graph = time_graph(g_st, 1, max(5, steps // 4), 0).p50
+    del g_st, layers
+    torch.cuda.empty_cache()
     stack_ms = 25 * ms_s + 5 * ms_f
     bf = lambda t: t.view(torch.int16).cpu().numpy().view("uint16")
     host.update(x=bf(x), attn_s=bf(attn_s), attn_f=bf(attn_f), moe=moe)
@@ -737,7 +755,9 @@ def bench_layer16(bq, torch, Wgu, Wd, steps):
     moe_b = (touched * (2 * I * H + 2 * I * 4 + H * I + H * 4) + 4 * T * E + nq(H) +
              R * (I + 4 * (I // 64)) * 2 + R * H * 4 * 2 + T * H * (4 + 2))
     return dict(sliding_layer_ms=ms_s, full_layer_ms=ms_f, moe_ms=ms_m,
-                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3), cpu_inputs=host,
+                stack_ms=stack_ms, stack_tokens_per_s=T / (stack_ms * 1e-3),
+                stack_graph_ms=ms_graph, stack_graph_tokens_per_s=T / (ms_graph * 1e-3),
+                cpu_inputs=host,
                 experts_touched=touched, sliding_bytes=sliding_b + moe_b, full_bytes=full_b + moe_b,
                 moe_bytes=moe_b)
 
@@ -1450,6 +1470,10 @@ def main():
             stack = 25 * (l16["sliding_layer_ms"] + sl) + 5 * (l16["full_layer_ms"] + fl)
             line["decoder_layer_b16"]["stack_with_attention_ms"] = round(stack, 4)
             line["decoder_layer_b16"]["stack_with_attention_tokens_per_s"] = round(16 / (stack * 1e-3), 1)
+            # the one-graph stack plus each layer's attention step
+            sg = l16["stack_graph_ms"] + 25 * sl + 5 * fl
+            line["decoder_layer_b16"]["stack_graph_with_attention_ms"] = round(sg, 4)
+            line["decoder_layer_b16"]["stack_graph_with_attention_tokens_per_s"] = round(16 / (sg * 1e-3), 1)
     if "stream_sweep" in res:
         line["launch_shape_sweep"] = res["stream_sweep"]
     if "load" in res:
