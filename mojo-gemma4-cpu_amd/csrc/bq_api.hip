@@ -94,6 +94,7 @@ void tune_init(int device) {
   Tune t{};
   t.gemv_waves = env_int("BQ_GEMV_WAVES");
   t.gemv_m1_waves = env_int("BQ_GEMV_M1_WAVES");
+  t.skinny2 = getenv("BQ_SKINNY2") ? env_int("BQ_SKINNY2") : 1;
   t.tile_bm = env_int("BQ_TILE_BM");
   t.tile_bn = env_int("BQ_TILE_BN");
   t.ring = env_int("BQ_RING");

@@ -238,6 +238,84 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny_1(BQ_SEG1_PARAMS) 
   linear_skinny<WAVES, PER_BLOCK, U>(Seg1Args{BQ_SEG1_FIELDS});
 }
 
+// Two 16-row n-tiles per workgroup (per-row, 2 <= M <= 16, K <= 4096): each
+// of the 16 waves takes the same one-shot K slice of both tiles, so the
+// slice's activation fragments (the whole M x K activation per workgroup,
+// as much as one tile's weights at M = 16) are read once for two tiles.
+// The tiles are global n-tiles 2b and 2b + 1 and may lie in different
+// segments (q | k | v); an odd last one is alone.  The same exact int32
+// sums and y = (f32(acc) * (sa*(1/127))) * ws[n] epilogue as
+// k_linear_skinny.
+template <int U>
+__global__ __launch_bounds__(1024) void k_linear_skinny2(LinArgs args) {
+  constexpr int WAVES = 16;
+  __shared__ int lds[2 * WAVES * 256];
+  const LinSeg& last_seg = args.seg[args.nseg - 1];
+  const int tiles = last_seg.tile0 + last_seg.n / 16;
+  const int g0 = 2 * blockIdx.x;
+  const bool two = g0 + 1 < tiles;
+  int nt0, nt1;
+  const LinSeg s0 = pick_seg(args, g0, nt0);
+  const LinSeg s1 = pick_seg(args, two ? g0 + 1 : g0, nt1);
+  const int K = args.K, K64 = K >> 6, M = args.M;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int per = (K64 + WAVES - 1) / WAVES;
+  const int kt0 = min(K64, wave * per), kt1 = min(K64, kt0 + per);
+  const int last = max(kt1 - 1, 0);  // loads past the wave's range read this k-step
+  // both tiles' weight slices go out first
+  const int8_t* wb0 = s0.w + (size_t)nt0 * K64 * 1024 + lane * 16;
+  const int8_t* wb1 = s1.w + (size_t)nt1 * K64 * 1024 + lane * 16;
+  v4i b0[U], b1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    b0[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb0 + (size_t)min(kt0 + u, last) * 1024));
+    b1[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb1 + (size_t)min(kt0 + u, last) * 1024));
+  }
+  // epilogue operands: thread t < 512 owns element t % 256 of tile t / 256
+  const int t = threadIdx.x, tile = (t >> 8) & 1;
+  const int ev = (t & 255) >> 6, eL = t & 63;
+  const int ei = 4 * (eL >> 4) + ev;
+  const LinSeg& es = tile ? s1 : s0;
+  const int en = (tile ? nt1 : nt0) * 16 + (eL & 15);
+  const bool eact = t < 512 && ei < M && (tile == 0 || two);
+  const float ews = es.ws[en];
+  const float ead = args.sa[min(ei, M - 1)] * kInv127;
+  // rows >= M read row 0 (accumulator row i depends only on A row i; rows
+  // >= M are never stored)
+  const int8_t* ab = args.act + (size_t)((lane & 15) < M ? (lane & 15) : 0) * K + (lane >> 4) * 16;
+  v4i af[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) af[u] = ld16(ab + min(kt0 + u, last) * 64);
+  const v4i zero = {0, 0, 0, 0};
+  v4i c0 = zero, c0b = zero, c1 = zero, c1b = zero;  // two chains per tile
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (kt0 + u < kt1) {
+      if (u & 1) {
+        c0b = mfma16x16x64(af[u], b0[u], c0b);
+        c1b = mfma16x16x64(af[u], b1[u], c1b);
+      } else {
+        c0 = mfma16x16x64(af[u], b0[u], c0);
+        c1 = mfma16x16x64(af[u], b1[u], c1);
+      }
+    }
+  }
+  c0 += c0b;
+  c1 += c1b;
+  int* l0 = lds + wave * 256 + lane;
+  int* l1 = lds + (WAVES + wave) * 256 + lane;
+  l0[0] = c0.x; l0[64] = c0.y; l0[128] = c0.z; l0[192] = c0.w;
+  l1[0] = c1.x; l1[64] = c1.y; l1[128] = c1.z; l1[192] = c1.w;
+  __syncthreads();
+  if (!eact) return;
+  int acc = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) acc += lds[(tile * WAVES + w) * 256 + (t & 255)];
+  const float y = (float)acc * ead * ews;
+  es.out[(size_t)ei * es.n + en] = f32_to_bf16(y);
+  if (es.out_f32) es.out_f32[(size_t)ei * es.n + en] = y;
+}
+
 // ---------------------------------------------------------------------------
 // M = 1, per-row (the decode GEMV)
 // ---------------------------------------------------------------------------
@@ -367,6 +445,12 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
         else if (w1 >= 8) hipLaunchKernelGGL((k_gemv_m1<8, 8>), g1, dim3(512), 0, st, a);
         else hipLaunchKernelGGL((k_gemv_m1<4, 16>), g1, dim3(256), 0, st, a);
       }
+      return hipGetLastError();
+    }
+    // two n-tiles per workgroup while there are >= 2 per CU (BQ_SKINNY2)
+    if (!per_block && a.M >= 2 && !tune().gemv_waves && a.K <= 4096 && tune().skinny2 &&
+        tiles >= 2 * tune().cus) {
+      hipLaunchKernelGGL((k_linear_skinny2<4>), dim3((tiles + 1) / 2), dim3(1024), 0, st, a);
       return hipGetLastError();
     }
     // 16 waves split K so that each wave's whole slice (<= 4 fragments for

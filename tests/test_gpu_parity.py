@@ -255,6 +255,29 @@ def test_qkv_matches_three_linears(gpu, O, M):
         np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
 
 
+@pytest.mark.parametrize("M", [2, 5, 16])
+def test_linear_two_tiles(gpu, O, M):
+    """2..16 rows with >= 2 n-tiles per CU take two n-tiles per workgroup,
+    bit-exact: q/k/v of 4112/2048/2048 rows (257 + 128 + 128 tiles: one
+    workgroup's pair straddles q and k, the last tile is alone) against the
+    three linears alone (each under 512 tiles: one tile per workgroup; the
+    oracle's VNNI pack takes no 4112-row weight), and the full layer's q/k
+    pair (8192 + 1024 rows) against the oracle."""
+    K = 2816
+    x = O.synth_normal_bf16(40 + M, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    Ws = [weight(gpu, O, n, K, 128, seed=sd)[2] for n, sd in ((4112, 41), (2048, 42), (2048, 43))]
+    outs = gpu.qkv(dev(xq), dev(sa), *Ws)
+    for o, W in zip(outs, Ws):
+        np.testing.assert_array_equal(host(o), host(gpu.linear(dev(xq), dev(sa), W)))
+    ws = [weight(gpu, O, n, K, 128, seed=sd) for n, sd in ((8192, 44), (1024, 45))]
+    outs = gpu.linear_pair(dev(xq), dev(sa), ws[0][2], ws[1][2])
+    for o, (q, s, W) in zip(outs, ws):
+        p, cs = O.pack_and_colsum(q)
+        rb, _ = O.linear(xq, sa, p, s, cs, W.n_rows)
+        np.testing.assert_array_equal(host(o), rb)
+
+
 @pytest.mark.parametrize("M,K", [(1, 2816), (16, 2816), (17, 512), (300, 1024)])
 def test_linear_pair(gpu, O, M, K):
     """gate and up in one launch = the two linears (and the oracle), bit-exact."""

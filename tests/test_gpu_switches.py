@@ -109,6 +109,21 @@ def test_norm_linear_switches(gpu, O, tune_env, sw, K, B):
     np.testing.assert_array_equal(host(ob), rb)
 
 
+# ------------------------------------------- one n-tile per workgroup (2..16 rows)
+@pytest.mark.parametrize("M", [2, 16])
+def test_skinny_one_tile_per_workgroup(gpu, O, tune_env, M):
+    tune_env(BQ_SKINNY2=0)
+    K, N = 2816, 8224  # 514 tiles
+    q, s, W = weight(gpu, O, N, K, 128, seed=46)
+    p, cs = O.pack_and_colsum(q)
+    x = O.synth_normal_bf16(47, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    ob, of = gpu.linear(dev(xq), dev(sa), W, want_f32=True)
+    rb, rf = O.linear(xq, sa, p, s, cs, N)
+    np.testing.assert_array_equal(host(of), rf)
+    np.testing.assert_array_equal(host(ob), rb)
+
+
 # --------------------------------------------------------------- MoE prep forms
 @pytest.mark.parametrize("sw", [dict(BQ_MOE_PREP=0), dict(BQ_PREP_ONE=0),
                                 dict(BQ_NQ_V8=0)])
