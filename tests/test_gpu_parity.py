@@ -198,7 +198,8 @@ def test_block_quant_golden(gpu, G):
 
 # ---------------------------------------------------------------- linears
 @pytest.mark.parametrize("M,K", [(1, 256), (1, 2816), (2, 2816), (16, 2816), (17, 256),
-                                 (40, 512), (128, 256), (300, 256)])
+                                 (40, 512), (128, 256), (300, 256), (3, 8192), (16, 6144),
+                                 (16, 12288)])
 def test_linear(gpu, O, M, K):
     N = 256
     q, s, W = weight(gpu, O, N, K, 128)
@@ -221,7 +222,7 @@ def test_linear_golden(gpu, G):
     np.testing.assert_array_equal(host(ob), G["lin_out_bf16"])
 
 
-@pytest.mark.parametrize("M,K,B", [(1, 2112, 64), (3, 4096, 256), (16, 8192, 512),
+@pytest.mark.parametrize("M,K,B", [(1, 2112, 64), (3, 4096, 256), (16, 8192, 512), (5, 8192, 128),
                                    (17, 2112, 64), (33, 1024, 256), (100, 1024, 512),
                                    (64, 704, 64)])
 def test_block_linear(gpu, O, M, K, B):
