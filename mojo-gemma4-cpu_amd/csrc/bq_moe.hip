@@ -184,33 +184,51 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   }
   const int isub = grp * 4 + wave;
   if (isub * 16 >= n_inter) return;  // never with bi8 (inter % 64 == 0)
-  // a record's token: its route's for the experts, the record itself for the dense MLP
-  auto tok = [&](int rec) { return dense ? rec : routes[rec].token; };
   const int8_t* wgp = wg + (size_t)isub * K64 * 1024 + lane * 16;
   const int8_t* wup = wu + (size_t)isub * K64 * 1024 + lane * 16;
-  const int arow = r0 + (lane & 15);
-  const int8_t* ab = xa + (size_t)tok(arow < r1 ? arow : r0) * K + (lane >> 4) * 16;
-  // epilogue operands
-  const int col = isub * 16 + (lane & 15);
-  const float wsg = sg[col], wsu = su[col];
-  float ad[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int rec = r0 + 4 * (lane >> 4) + v;
-    ad[v] = xs[tok(rec < r1 ? rec : r0)] * kInv127;
-  }
-  const v4i zero = {0, 0, 0, 0};
-  v4i cg = zero, cu = zero;
   v4i bg[2][U], bu[2][U], af[2][U];
-  auto load = [&](int s, int c) {
+  auto load_w = [&](int s, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kt = min(c * U + u, K64 - 1);
       bg[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wgp + (size_t)kt * 1024));
       bu[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wup + (size_t)kt * 1024));
-      af[s][u] = ld16(ab + kt * 64);
     }
   };
+  // this lane's activation row and its four epilogue rows: the records'
+  // tokens (their routes' for the experts, the records themselves for the
+  // dense MLP), requested together; then the weight stream, which depends
+  // only on the expert, goes out while they are in flight (loads return in
+  // issue order, so the activation loads wait for the tokens alone)
+  int tk[5];
+  tk[0] = min(r0 + (lane & 15), r1 - 1);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) tk[1 + v] = min(r0 + 4 * (lane >> 4) + v, r1 - 1);
+  if (!dense) {
+#pragma unroll
+    for (int i = 0; i < 5; ++i) tk[i] = routes[tk[i]].token;
+  }
+  asm volatile("" ::: "memory");  // keep the three groups of loads in this order
+  load_w(0, 0);
+  asm volatile("" ::: "memory");
+  const int8_t* ab = xa + (size_t)tk[0] * K + (lane >> 4) * 16;
+  auto load_a = [&](int s, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) af[s][u] = ld16(ab + min(c * U + u, K64 - 1) * 64);
+  };
+  auto load = [&](int s, int c) {
+    load_w(s, c);
+    load_a(s, c);
+  };
+  load_a(0, 0);
+  // epilogue operands
+  const int col = isub * 16 + (lane & 15);
+  const float wsg = sg[col], wsu = su[col];
+  float ad[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) ad[v] = xs[tk[1 + v]] * kInv127;
+  const v4i zero = {0, 0, 0, 0};
+  v4i cg = zero, cu = zero;
   auto mul = [&](int s, int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -220,8 +238,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
       }
   };
   const int nch = (K64 + U - 1) / U;
-  load(0, 0);
-  for (int c = 0; c < nch; c += 2) {
+  for (int c = 0; c < nch; c += 2) {  // (chunk 0 is in flight)
     if (c + 1 < nch) load(1, c + 1);
     mul(0, c);
     if (c + 1 >= nch) break;
@@ -306,15 +323,10 @@ void k_moe_down_skinny(
     xa = b_i8; xsa = b_sa;
   }
   const int K64 = K >> 6, fpb = block >> 6, nb = K / block;
-  for (int i = threadIdx.x; i < 16 * nb; i += 256) {  // 256-thread blocks
-    const int row = r0 + i / nb;
-    s_sa[i] = xsa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
-  }
-  __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
   const int nsub0 = (blockIdx.x * 4 + wave) * NS;
   const int nstrips = hidden / 16;
-  if (nsub0 >= nstrips) return;
+  const bool active = nsub0 < nstrips;  // wave-uniform; idle waves still meet the barrier
   const int8_t* wb[NS];
   float wsc[NS][4];
 #pragma unroll
@@ -370,7 +382,15 @@ void k_moe_down_skinny(
     }
   };
   const int nch = (K64 + U - 1) / U;
-  load(0, 0);
+  // the first weight and activation fragments go out before the block
+  // scales are staged: the staging's loads and barrier overlap them
+  if (active) load(0, 0);
+  for (int i = threadIdx.x; i < 16 * nb; i += 256) {  // 256-thread blocks
+    const int row = r0 + i / nb;
+    s_sa[i] = xsa[(size_t)(row < r1 ? row : r0) * nb + i % nb] * kInv127;
+  }
+  __syncthreads();
+  if (!active) return;
   for (int ch = 0; ch < nch; ch += 2) {
     if (ch + 1 < nch) load(1, ch + 1);
     mul(0, ch);
