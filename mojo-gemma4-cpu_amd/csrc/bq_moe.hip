@@ -290,10 +290,12 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 // holds columns 4 (L/16) .. +3 of a strip for record L % 16, so a drain
 // reads one activation scale per lane and a record's four y values are one
 // 16-byte store; the integer dot of each (record, column) is the same.
-// Up to two weight fragments per k-step slot the kernel fits 64 registers,
-// eight waves per SIMD (waves_per_eu(8)): a 16-token batch's 86 experts x 22
-// workgroups then fit in one round on 256 CUs instead of leaving ~100
-// workgroups for a second.  The first dn.ytiles rows of the grid are the
+// With up to two weight fragments per k-step slot the kernel fits 64
+// registers, eight waves per SIMD (waves_per_eu(8)), so a 16-token batch's
+// 86 experts x 22 workgroups fit in one round on 256 CUs; the default, two
+// k-steps x two strips, has more weight bytes in flight per wave instead,
+// which measured faster once the dense rows (K = 2112) joined the launch.
+// The first dn.ytiles rows of the grid are the
 // dense MLP's down projection (16 tokens each, K = dn.inter): the same fma
 // chain over blocks, out = bf16(facc * ws) with no route weight
 // (dispatch_bq_block_linear, gemma_4_moe_bq.mojo:774-778).
@@ -597,9 +599,10 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     dn.ytiles = (dn.T + 15) / 16;
   }
   float* y = (float*)workspace;
-  // one k-step per register slot and two strips per wave (57 VGPRs, eight
-  // waves per SIMD; BQ_DOWN_SKINNY): the 32-token layer 127.6 us against
-  // 128.0-130.6 us for 1-4 k-steps x 1-4 strips
+  // two k-steps per register slot and two strips per wave (BQ_DOWN_SKINNY):
+  // the batch-16 decoder layer, whose dense down rows run K = 2112, 125.0 ->
+  // 122.2 us against one k-step per slot, and the 32-token MoE layer 122.4 ->
+  // 122.2 us; four strips or one were slower
   auto skinny = [&](int E, int moe_rows) {
 #define BQ_DS(U, NS)                                                                              \
   case U * 10 + NS: {                                                                             \
@@ -609,8 +612,8 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     break;                                                                                        \
   }
     switch (tune().down_skinny) {
-      BQ_DS(2, 2) BQ_DS(1, 4) BQ_DS(2, 1)
-      default: BQ_DS(1, 2)
+      BQ_DS(1, 2) BQ_DS(1, 4) BQ_DS(2, 1)
+      default: BQ_DS(2, 2)
     }
 #undef BQ_DS
     return hipGetLastError();
