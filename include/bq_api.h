@@ -336,9 +336,12 @@ int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
  * bq_block_quant(bf16(gelu_tanh(bf16(gate)) * bf16(up)), 64, FWHT) with gate
  * and up the bq_linear outputs (kernels/elementwise.mojo:17-27).  dense_gate
  * and dense_up are [dense_inter, hidden] per-row (B = 128) weights.  While
- * the experts use the 16-row kernel (few routes per expert) the dense rows
- * are more workgroups of its launch; otherwise they are a launch of their
- * own after the experts'.  The checks of bq_moe_phase1_gate_up_quant apply;
+ * the experts use the 16-row kernel (few routes per expert, decode) the
+ * dense rows are more workgroups of its launch; otherwise they are a launch
+ * of their own after the experts', still in 16-token tiles, which re-read
+ * the dense weights per tile (2048 tokens: 229 us for the dense rows,
+ * against 68 us for bq_linear_pair of gate and up alone), so prefill-sized
+ * batches are better served by the separate calls.  The checks of bq_moe_phase1_gate_up_quant apply;
  * dense_inter % 64 == 0; dense_x_i8, dense_gate, dense_up 16-byte, dense_i8
  * 8-byte, dense_sa 4-byte aligned. */
 int bq_ffn_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,
@@ -356,7 +359,8 @@ int bq_ffn_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_
  * the same block): dense_out [seq_len, hidden] bf16 = bq_block_linear(
  * dense_i8, dense_sa, dense_down, block).  dense_down is [hidden,
  * dense_inter].  While the experts use the 16-row kernel the dense rows are
- * more workgroups of its launch; otherwise a launch of their own.  The checks
+ * more workgroups of its launch; otherwise they are bq_block_linear's own
+ * (tiled) launch.  The checks
  * of bq_moe_phase2_down apply; dense_inter % block == 0, dense_inter / block
  * <= 64; dense_i8 and dense_down 16-byte, dense_out 8-byte aligned. */
 int bq_ffn_down(const int8_t* bucket_i8, const float* bucket_sa, const int32_t* expert_offset,

@@ -633,8 +633,19 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
       dense_done = true;
     }
   }
-  if (!dense_done) {  // the dense rows in a skinny launch of their own
-    const hipError_t e = skinny(0, 0);
+  if (!dense_done) {
+    // the experts took the tiled kernels (many tokens): the dense down
+    // projection is the per-block linear's own launch (bq_block_linear), whose
+    // tiles reuse each weight block across many tokens
+    LinArgs la{};
+    la.seg[0] = {dn.w, dn.ws, dn.out, nullptr, hidden, 0};
+    la.nseg = 1;
+    la.act = dn.x_i8;
+    la.sa = dn.x_sa;
+    la.M = dn.T;
+    la.K = dn.inter;
+    la.block = block;
+    const hipError_t e = launch_linear(la, 1, st);
     if (e != hipSuccess) return e;
   }
   // below 256 tokens each workgroup takes 256 columns of its token (32
