@@ -109,7 +109,7 @@ void tune_init(int device) {
   t.nq_pair = getenv("BQ_NQ_PAIR") ? env_int("BQ_NQ_PAIR") : 1;
   t.moe_prep = getenv("BQ_MOE_PREP") ? env_int("BQ_MOE_PREP") : 1;
   t.nq_v8 = getenv("BQ_NQ_V8") ? env_int("BQ_NQ_V8") : 1;
-  t.down_skinny = getenv("BQ_DOWN_SKINNY") ? env_int("BQ_DOWN_SKINNY") : 22;
+  t.down_skinny = getenv("BQ_DOWN_SKINNY") ? env_int("BQ_DOWN_SKINNY") : 32;
   t.gu_skinny = getenv("BQ_GU_SKINNY") ? env_int("BQ_GU_SKINNY") : 4;
   t.head_grid = env_int("BQ_HEAD_GRID");
   t.attn_waves = env_int("BQ_ATTN_WAVES");

@@ -28,7 +28,7 @@ struct Tune {
   int nq_v8;        // BQ_NQ_V8: 0 disables the 8-values-per-lane norm-quant and head prep (block 128)
   int moe_prep;     // BQ_MOE_PREP: 0 runs bq_moe_prep as separate launches
   int mf;           // BQ_MF: MFMA tile of the LDS-ring kernels (16: 16x16x64, 32: 32x32x32)
-  int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (22; 12, 14, 21)
+  int down_skinny;  // BQ_DOWN_SKINNY: skinny MoE down, 10 x k-steps per slot + strips per wave (32; 12, 14, 21, 22, 42)
   int gu_skinny;    // BQ_GU_SKINNY: skinny MoE gate/up, k-steps per register slot (4; 2, 6)
   int head_grid;    // BQ_HEAD_GRID: vocabulary-head workgroups (one per CU)
   int sel_fused;    // BQ_SEL_FUSED: 0 keeps the head selection's two threshold launches

@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
 // 16-byte store; the integer dot of each (record, column) is the same.
 // With up to two weight fragments per k-step slot the kernel fits 64
 // registers, eight waves per SIMD (waves_per_eu(8)), so a 16-token batch's
-// 86 experts x 22 workgroups fit in one round on 256 CUs; the default, two
+// 86 experts x 22 workgroups fit in one round on 256 CUs; the default, three
 // k-steps x two strips, has more weight bytes in flight per wave instead,
 // which measured faster once the dense rows (K = 2112) joined the launch.
 // The first dn.ytiles rows of the grid are the
@@ -599,10 +599,11 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     dn.ytiles = (dn.T + 15) / 16;
   }
   float* y = (float*)workspace;
-  // two k-steps per register slot and two strips per wave (BQ_DOWN_SKINNY):
-  // the batch-16 decoder layer, whose dense down rows run K = 2112, 125.0 ->
-  // 122.2 us against one k-step per slot, and the 32-token MoE layer 122.4 ->
-  // 122.2 us; four strips or one were slower
+  // three k-steps per register slot and two strips per wave (BQ_DOWN_SKINNY):
+  // the 30-layer batch-16 decode stack, whose dense down rows run K = 2112,
+  // 3.587 / 3.522 / 3.501 / 3.524 ms with 1 / 2 / 3 / 4 k-steps per slot, and
+  // the 32-token MoE layer 122.4 / 122.8 / 122.6 us (1 / 2 / 3); four strips
+  // or one were slower
   auto skinny = [&](int E, int moe_rows) {
 #define BQ_DS(U, NS)                                                                              \
   case U * 10 + NS: {                                                                             \
@@ -612,8 +613,8 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     break;                                                                                        \
   }
     switch (tune().down_skinny) {
-      BQ_DS(1, 2) BQ_DS(1, 4) BQ_DS(2, 1)
-      default: BQ_DS(2, 2)
+      BQ_DS(1, 2) BQ_DS(1, 4) BQ_DS(2, 1) BQ_DS(2, 2) BQ_DS(4, 2)
+      default: BQ_DS(3, 2)
     }
 #undef BQ_DS
     return hipGetLastError();

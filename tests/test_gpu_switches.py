@@ -189,7 +189,8 @@ def _moe_check(gpu, O, T, E=8, k=2, H=256, I=128, seed=5):
 
 
 @pytest.mark.parametrize("sw", [dict(BQ_DOWN_SKINNY=12), dict(BQ_DOWN_SKINNY=14),
-                                dict(BQ_DOWN_SKINNY=21), dict(BQ_GU_SKINNY=2),
+                                dict(BQ_DOWN_SKINNY=21), dict(BQ_DOWN_SKINNY=22),
+                                dict(BQ_DOWN_SKINNY=42), dict(BQ_GU_SKINNY=2),
                                 dict(BQ_GU_SKINNY=6)])
 @pytest.mark.parametrize("T", [5, 40])
 def test_moe_skinny_switches(gpu, O, tune_env, sw, T):
