@@ -599,11 +599,11 @@ hipError_t launch_moe_phase2(const int8_t* bucket_i8, const float* bucket_sa, co
     dn.ytiles = (dn.T + 15) / 16;
   }
   float* y = (float*)workspace;
-  // three k-steps per register slot and two strips per wave (BQ_DOWN_SKINNY):
-  // the 30-layer batch-16 decode stack, whose dense down rows run K = 2112,
-  // 3.587 / 3.522 / 3.501 / 3.524 ms with 1 / 2 / 3 / 4 k-steps per slot, and
-  // the 32-token MoE layer 122.4 / 122.8 / 122.6 us (1 / 2 / 3); four strips
-  // or one were slower
+  // three k-steps per register slot and two strips per wave (BQ_DOWN_SKINNY).
+  // The 30-layer batch-16 decode stack, whose dense down rows run K = 2112:
+  // 1 / 2 k-steps 3.587 / 3.512 ms on one box, 2 / 3 / 4 k-steps 3.522 /
+  // 3.501 / 3.524 ms on another; the 32-token MoE layer 2 / 3 k-steps 122.8 /
+  // 122.6 us.  Four strips or one were slower.
   auto skinny = [&](int E, int moe_rows) {
 #define BQ_DS(U, NS)                                                                              \
   case U * 10 + NS: {                                                                             \
