@@ -338,10 +338,9 @@ int bq_moe_phase2_down_noalloc(const int8_t* bucket_i8, const float* bucket_sa,
  * and dense_up are [dense_inter, hidden] per-row (B = 128) weights.  While
  * the experts use the 16-row kernel (few routes per expert, decode) the
  * dense rows are more workgroups of its launch; otherwise they are a launch
- * of their own after the experts', still in 16-token tiles, which re-read
- * the dense weights per tile (2048 tokens: 229 us for the dense rows,
- * against 68 us for bq_linear_pair of gate and up alone), so prefill-sized
- * batches are better served by the separate calls.  The checks of bq_moe_phase1_gate_up_quant apply;
+ * of their own after the experts', in 64-token tiles (2048 tokens: 135 us
+ * for the dense rows, against 68 us for bq_linear_pair of gate and up
+ * alone, which leaves the GELU and the block-quant to further calls).  The checks of bq_moe_phase1_gate_up_quant apply;
  * dense_inter % 64 == 0; dense_x_i8, dense_gate, dense_up 16-byte, dense_i8
  * 8-byte, dense_sa 4-byte aligned. */
 int bq_ffn_gate_up(const int8_t* x_i8, const float* x_sa, const int32_t* expert_offset,

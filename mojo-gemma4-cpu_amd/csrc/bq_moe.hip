@@ -280,6 +280,97 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   }
 }
 
+// The dense MLP's gate/up alone at many tokens (the experts on the tiled
+// kernels): as the dense rows of k_moe_gate_up_skinny, but a workgroup takes
+// RT 16-token tiles of its 64-column group, so every weight fragment feeds
+// RT tiles' products (the 16-token form re-reads the dense weights once per
+// 16 tokens).  Each tile's epilogue is the skinny kernel's: the linears'
+// bf16 gate and up, GELU-tanh(gate) * up, FWHT64 block-quant through LDS.
+template <int RT, int U>  // U: k-steps per register slot
+__global__ __launch_bounds__(256) void k_dense_gate_up(int hidden, float fwht64, DenseGateUp dn) {
+  __shared__ __attribute__((aligned(16))) uint16_t qtile[16 * 64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+  const int K = hidden, K64 = K >> 6;
+  const int grp = blockIdx.x, t0 = blockIdx.y * 16 * RT;  // grid x = inter / 64
+  const int isub = grp * 4 + wave;
+  const int8_t* wgp = dn.wg + (size_t)isub * K64 * 1024 + lane * 16;
+  const int8_t* wup = dn.wu + (size_t)isub * K64 * 1024 + lane * 16;
+  v4i bg[2][U], bu[2][U], af[2][U][RT];
+  const int8_t* ab[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)  // rows past the batch read its last row, never stored
+    ab[r] = dn.x_i8 + (size_t)min(t0 + 16 * r + (lane & 15), dn.T - 1) * K + (lane >> 4) * 16;
+  auto load = [&](int s, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = min(c * U + u, K64 - 1);
+      bg[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wgp + (size_t)kt * 1024));
+      bu[s][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wup + (size_t)kt * 1024));
+#pragma unroll
+      for (int r = 0; r < RT; ++r) af[s][u][r] = ld16(ab[r] + kt * 64);
+    }
+  };
+  load(0, 0);
+  const int col = isub * 16 + (lane & 15);
+  const float wsg = dn.sg[col], wsu = dn.su[col];
+  const v4i zero = {0, 0, 0, 0};
+  v4i cg[RT], cu[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) cg[r] = cu[r] = zero;
+  auto mul = [&](int s, int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c * U + u < K64) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          cg[r] = mfma16x16x64(af[s][u][r], bg[s][u], cg[r]);
+          cu[r] = mfma16x16x64(af[s][u][r], bu[s][u], cu[r]);
+        }
+      }
+  };
+  const int nch = (K64 + U - 1) / U;
+  for (int c = 0; c < nch; c += 2) {  // (chunk 0 is in flight)
+    if (c + 1 < nch) load(1, c + 1);
+    mul(0, c);
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) load(0, c + 2);
+    mul(1, c + 1);
+  }
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int r0 = t0 + 16 * r;
+    if (r0 >= dn.T) break;  // workgroup-uniform
+    const int r1 = min(dn.T, r0 + 16);
+    const int g4[4] = {cg[r].x, cg[r].y, cg[r].z, cg[r].w};
+    const int u4[4] = {cu[r].x, cu[r].y, cu[r].z, cu[r].w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rec = r0 + 4 * (lane >> 4) + v;
+      if (rec >= r1) continue;
+      const float ad = dn.x_sa[rec] * kInv127;
+      const float gv = bf16_to_f32(f32_to_bf16((float)g4[v] * ad * wsg));  // the linears' bf16
+      const float uv = bf16_to_f32(f32_to_bf16((float)u4[v] * ad * wsu));
+      qtile[(rec - r0) * 64 + wave * 16 + (lane & 15)] = f32_to_bf16(gelu_tanh_f32(gv) * uv);
+    }
+    __syncthreads();
+    if (wave < 2) {  // 16 records x one 64-column block: 8 lanes per record
+      const int rr = wave * 8 + (lane >> 3), i = lane & 7;
+      const v4i raw = *reinterpret_cast<const v4i*>(&qtile[rr * 64 + i * 8]);
+      float vv[8];
+      bf16x8_to_f32(raw, vv);
+      uint32_t w[2];
+      const float m = block_quant_lanes<8>(vv, true, fwht64, w);
+      if (r0 + rr < r1) {
+        const size_t rec = (size_t)(r0 + rr), c0 = (size_t)grp * 64 + i * 8;
+        *reinterpret_cast<u2*>(dn.out_i8 + rec * dn.inter + c0) = u2{w[0], w[1]};
+        if (i == 0) dn.out_sa[rec * (dn.inter / 64) + grp] = m;
+      }
+    }
+    __syncthreads();  // qtile is refilled by the next tile
+  }
+}
+
 // Phase 2 GEMM: y[rec, n] = (facc * ws[n]) * route_w[rec] with facc the fma
 // chain over K blocks (moe.mojo:198-223).  The m-tile's per-block activation
 // scales (16 records x K/block <= 64) are staged in LDS up front.  A wave
@@ -550,7 +641,7 @@ hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_
     dn.cpg = (dn.inter / 64 + gx - 1) / gx;
     dn.ytiles = (dn.T + 15) / 16 * dn.cpg;
   }
-  int E = experts, moe_rows = max_routes > 0 ? mtile_bound(max_routes, experts, 16) : 0;
+  const int moe_rows = max_routes > 0 ? mtile_bound(max_routes, experts, 16) : 0;
   if (max_routes > 0) {
     const int bm = moe_tile_bm(max_routes, experts);
     if (bm >= 64 && inter % 64 == 0) {
@@ -558,15 +649,20 @@ hipError_t launch_moe_phase1(const int8_t* x_i8, const float* x_sa, const int32_
                                                     bi8, bsa, experts, max_routes, hidden, inter,
                                                     bm, st);
       if (r != hipSuccess || !has_dense) return r;
-      E = 0;  // the dense rows in a skinny launch of their own
-      moe_rows = 0;
+      // the dense rows alone: 64 tokens per workgroup share each weight
+      // fragment (2048 tokens: 135 us for them, against 229 us in 16-token
+      // tiles and 306 us with 128 tokens and one k-step per slot)
+      constexpr int RT = 4, U = 2;
+      hipLaunchKernelGGL((k_dense_gate_up<RT, U>), dim3(dn.inter / 64, (dn.T + 16 * RT - 1) / (16 * RT)),
+                         dim3(256), 0, st, hidden, fwht_scale_host(64), dn);
+      return hipGetLastError();
     }
   }
   dim3 g(gx, dn.ytiles + moe_rows), b(256);
 #define BQ_GU(U)                                                                                  \
   case U:                                                                                         \
-    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, E, hidden, inter, max_routes, eo,    \
-                       routes, w_gu, x_i8, gu_scale, x_sa, bucket, bi8, bsa,                      \
+    hipLaunchKernelGGL(k_moe_gate_up_skinny<U>, g, b, 0, st, experts, hidden, inter, max_routes,  \
+                       eo, routes, w_gu, x_i8, gu_scale, x_sa, bucket, bi8, bsa,                  \
                        fwht_scale_host(64), dn);                                                  \
     break;
   switch (tune().gu_skinny) {  // 2 or 6 k-steps per register slot; 4 measured best

@@ -631,10 +631,11 @@ def test_moe_phase1_quant(gpu, O, T, E, k, H, I):
 
 # (T, E, top_k, hidden, expert inter, dense inter): the experts in the 16-row
 # kernels (T <= 40 here; 1..10 routes per expert) or the LDS-tiled ones (T =
-# 300 over 4 experts); dense_inter narrower than, a multiple of, and not a
+# 300 and 129 over 4 experts, the dense gate/up then in 64-token workgroups,
+# the last one partial); dense_inter narrower than, a multiple of, and not a
 # multiple of the experts' 64-column groups; ragged 16-token tiles
 FFN_CASES = [(1, 8, 2, 1024, 128, 192), (16, 8, 2, 1024, 128, 320), (17, 16, 4, 2816, 128, 256),
-             (40, 8, 2, 1024, 192, 128), (300, 4, 2, 1024, 128, 192)]
+             (40, 8, 2, 1024, 192, 128), (300, 4, 2, 1024, 128, 192), (129, 4, 2, 1024, 128, 320)]
 
 
 def _dense_gate_up_ref(O, dq, dsa, qg, sg, qu, su, DI):
