@@ -199,7 +199,9 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_skinny(
   // tokens (their routes' for the experts, the records themselves for the
   // dense MLP), requested together; then the weight stream, which depends
   // only on the expert, goes out while they are in flight (loads return in
-  // issue order, so the activation loads wait for the tokens alone)
+  // issue order, so the activation loads wait for the tokens alone).  Rows
+  // past the tile's last record read that record: accumulator row i depends
+  // only on A row i, and those rows are never stored.
   int tk[5];
   tk[0] = min(r0 + (lane & 15), r1 - 1);
 #pragma unroll
