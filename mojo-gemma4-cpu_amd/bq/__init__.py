@@ -264,6 +264,8 @@ def block_linear(x_i8, x_sa, w: ButterquantWeight, block: int, want_f32: bool = 
 
 def qkv(x_i8, x_sa, q: ButterquantWeight, k: ButterquantWeight, v: ButterquantWeight, outs=None):
     m, hidden = x_i8.shape
+    if v.n_rows != k.n_rows:
+        raise ValueError(f"qkv: v has {v.n_rows} rows, k {k.n_rows}; they must match")
     if outs is None:
         outs = tuple(torch.empty((m, w.n_rows), dtype=torch.bfloat16, device=x_i8.device)
                      for w in (q, k, v))

@@ -238,46 +238,51 @@ __global__ __launch_bounds__(WAVES * 64) void k_linear_skinny_1(BQ_SEG1_PARAMS) 
   linear_skinny<WAVES, PER_BLOCK, U>(Seg1Args{BQ_SEG1_FIELDS});
 }
 
-// Two 16-row n-tiles per workgroup (per-row, 2 <= M <= 16, K <= 4096): each
-// of the 16 waves takes the same one-shot K slice of both tiles, so the
+// NT 16-row n-tiles per workgroup (per-row, 2 <= M <= 16, K <= 4096): each
+// of the 16 waves takes the same one-shot K slice of every tile, so the
 // slice's activation fragments (the whole M x K activation per workgroup,
-// as much as one tile's weights at M = 16) are read once for two tiles.
-// The tiles are global n-tiles 2b and 2b + 1 and may lie in different
-// segments (q | k | v); an odd last one is alone.  The same exact int32
+// as much as one tile's weights at M = 16) are read once for NT tiles.  The
+// tiles are global n-tiles NT b .. NT b + NT - 1 and may lie in different
+// segments (q | k | v); a short last group has fewer.  The same exact int32
 // sums and y = (f32(acc) * (sa*(1/127))) * ws[n] epilogue as
 // k_linear_skinny.
-template <int U>
+template <int NT, int U>
 __global__ __launch_bounds__(1024) void k_linear_skinny2(LinArgs args) {
   constexpr int WAVES = 16;
-  __shared__ int lds[2 * WAVES * 256];
+  __shared__ int lds[NT * WAVES * 256];
   const LinSeg& last_seg = args.seg[args.nseg - 1];
   const int tiles = last_seg.tile0 + last_seg.n / 16;
-  const int g0 = 2 * blockIdx.x;
-  const bool two = g0 + 1 < tiles;
-  int nt0, nt1;
-  const LinSeg s0 = pick_seg(args, g0, nt0);
-  const LinSeg s1 = pick_seg(args, two ? g0 + 1 : g0, nt1);
+  const int g0 = NT * blockIdx.x;
+  const int ntl = min(NT, tiles - g0);  // tiles of this workgroup
+  LinSeg sg[NT];
+  int ntt[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) sg[j] = pick_seg(args, j < ntl ? g0 + j : g0, ntt[j]);
   const int K = args.K, K64 = K >> 6, M = args.M;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int per = (K64 + WAVES - 1) / WAVES;
   const int kt0 = min(K64, wave * per), kt1 = min(K64, kt0 + per);
   const int last = max(kt1 - 1, 0);  // loads past the wave's range read this k-step
-  // both tiles' weight slices go out first
-  const int8_t* wb0 = s0.w + (size_t)nt0 * K64 * 1024 + lane * 16;
-  const int8_t* wb1 = s1.w + (size_t)nt1 * K64 * 1024 + lane * 16;
-  v4i b0[U], b1[U];
+  // every tile's weight slice goes out first
+  v4i b[NT][U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    b0[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb0 + (size_t)min(kt0 + u, last) * 1024));
-    b1[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb1 + (size_t)min(kt0 + u, last) * 1024));
+  for (int j = 0; j < NT; ++j) {
+    const int8_t* wb = sg[j].w + (size_t)ntt[j] * K64 * 1024 + lane * 16;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      b[j][u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb + (size_t)min(kt0 + u, last) * 1024));
   }
-  // epilogue operands: thread t < 512 owns element t % 256 of tile t / 256
-  const int t = threadIdx.x, tile = (t >> 8) & 1;
+  // epilogue operands: thread t < 256 NT owns element t % 256 of tile t / 256
+  const int t = threadIdx.x, tile = min(t >> 8, NT - 1);
   const int ev = (t & 255) >> 6, eL = t & 63;
   const int ei = 4 * (eL >> 4) + ev;
-  const LinSeg& es = tile ? s1 : s0;
-  const int en = (tile ? nt1 : nt0) * 16 + (eL & 15);
-  const bool eact = t < 512 && ei < M && (tile == 0 || two);
+  LinSeg es = sg[0];
+  int ent = ntt[0];
+#pragma unroll
+  for (int j = 1; j < NT; ++j)
+    if (tile == j) { es = sg[j]; ent = ntt[j]; }
+  const int en = ent * 16 + (eL & 15);
+  const bool eact = t < 256 * NT && ei < M && tile < ntl;
   const float ews = es.ws[en];
   const float ead = args.sa[min(ei, M - 1)] * kInv127;
   // rows >= M read row 0 (accumulator row i depends only on A row i; rows
@@ -287,25 +292,25 @@ __global__ __launch_bounds__(1024) void k_linear_skinny2(LinArgs args) {
 #pragma unroll
   for (int u = 0; u < U; ++u) af[u] = ld16(ab + min(kt0 + u, last) * 64);
   const v4i zero = {0, 0, 0, 0};
-  v4i c0 = zero, c0b = zero, c1 = zero, c1b = zero;  // two chains per tile
+  v4i c[NT], cb[NT];  // two chains per tile
+#pragma unroll
+  for (int j = 0; j < NT; ++j) c[j] = cb[j] = zero;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (kt0 + u < kt1) {
-      if (u & 1) {
-        c0b = mfma16x16x64(af[u], b0[u], c0b);
-        c1b = mfma16x16x64(af[u], b1[u], c1b);
-      } else {
-        c0 = mfma16x16x64(af[u], b0[u], c0);
-        c1 = mfma16x16x64(af[u], b1[u], c1);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (u & 1) cb[j] = mfma16x16x64(af[u], b[j][u], cb[j]);
+        else c[j] = mfma16x16x64(af[u], b[j][u], c[j]);
       }
     }
   }
-  c0 += c0b;
-  c1 += c1b;
-  int* l0 = lds + wave * 256 + lane;
-  int* l1 = lds + (WAVES + wave) * 256 + lane;
-  l0[0] = c0.x; l0[64] = c0.y; l0[128] = c0.z; l0[192] = c0.w;
-  l1[0] = c1.x; l1[64] = c1.y; l1[128] = c1.z; l1[192] = c1.w;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    c[j] += cb[j];
+    int* l = lds + (j * WAVES + wave) * 256 + lane;
+    l[0] = c[j].x; l[64] = c[j].y; l[128] = c[j].z; l[192] = c[j].w;
+  }
   __syncthreads();
   if (!eact) return;
   int acc = 0;
@@ -447,10 +452,16 @@ hipError_t launch_linear(const LinArgs& a, int per_block, hipStream_t st) {
       }
       return hipGetLastError();
     }
-    // two n-tiles per workgroup while there are >= 2 per CU (BQ_SKINNY2)
+    // ceil(tiles / CUs) n-tiles per workgroup (at most 4, or BQ_SKINNY2 when
+    // that is 2 or 3) while there are >= 2 per CU: one workgroup per CU, each
+    // activation read shared by its tiles
     if (!per_block && a.M >= 2 && !tune().gemv_waves && a.K <= 4096 && tune().skinny2 &&
         tiles >= 2 * tune().cus) {
-      hipLaunchKernelGGL((k_linear_skinny2<4>), dim3((tiles + 1) / 2), dim3(1024), 0, st, a);
+      const int cap = tune().skinny2 >= 2 ? min(tune().skinny2, 4) : 4;
+      const int nt = min(cap, (tiles + tune().cus - 1) / tune().cus);
+      if (nt <= 2) hipLaunchKernelGGL((k_linear_skinny2<2, 4>), dim3((tiles + 1) / 2), dim3(1024), 0, st, a);
+      else if (nt == 3) hipLaunchKernelGGL((k_linear_skinny2<3, 4>), dim3((tiles + 2) / 3), dim3(1024), 0, st, a);
+      else hipLaunchKernelGGL((k_linear_skinny2<4, 4>), dim3((tiles + 3) / 4), dim3(1024), 0, st, a);
       return hipGetLastError();
     }
     // 16 waves split K so that each wave's whole slice (<= 4 fragments for

@@ -34,7 +34,7 @@ struct Tune {
   int sel_fused;    // BQ_SEL_FUSED: 0 keeps the head selection's two threshold launches
   int attn_waves;   // BQ_ATTN_WAVES: waves the attention split plan aims for (2048)
   int prep_one;     // BQ_PREP_ONE: MoE prep's top-k + schedule in one workgroup (up to 16 tokens)
-  int skinny2;      // BQ_SKINNY2: 0 keeps one n-tile per workgroup for 2..16-row per-row linears
+  int skinny2;      // BQ_SKINNY2: 0 keeps one n-tile per workgroup for 2..16-row per-row linears; 2 or 3 caps the tiles per workgroup (default 4)
   int cus;          // compute units of the device
 };
 const Tune& tune();

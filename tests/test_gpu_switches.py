@@ -124,6 +124,28 @@ def test_skinny_one_tile_per_workgroup(gpu, O, tune_env, M):
     np.testing.assert_array_equal(host(ob), rb)
 
 
+@pytest.mark.parametrize("M", [2, 7, 16])
+def test_skinny_tiles_per_workgroup(gpu, O, tune_env, M):
+    """q/k/v of 8224/4128/4128 rows (514 + 258 + 258 = 1030 tiles) with 4 (the
+    default here), 3, 2 and 1 n-tiles per workgroup: groups straddle segments
+    and the last group is short; every segment = the oracle, bit-exact."""
+    K = 2816
+    x = O.synth_normal_bf16(48 + M, 1.0, (M, K))
+    xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
+    ws = [weight(gpu, O, n, K, 128, seed=sd) for n, sd in ((8224, 49), (4128, 50), (4128, 51))]
+    refs = []
+    for q, s, W in ws:
+        p, cs = O.pack_and_colsum(q)
+        refs.append(O.linear(xq, sa, p, s, cs, W.n_rows)[0])
+    for cap in (1, 3, 2, 0):
+        tune_env(BQ_SKINNY2=cap)
+        outs = gpu.qkv(dev(xq), dev(sa), *(w[2] for w in ws))
+        for seg, (o, r) in enumerate(zip(outs, refs)):
+            o = host(o)
+            bad = np.argwhere(o != r)
+            assert bad.size == 0, (cap, seg, bad[:8].tolist(), o[tuple(bad[0])], r[tuple(bad[0])])
+
+
 # --------------------------------------------------------------- MoE prep forms
 @pytest.mark.parametrize("sw", [dict(BQ_MOE_PREP=0), dict(BQ_PREP_ONE=0),
                                 dict(BQ_NQ_V8=0)])
