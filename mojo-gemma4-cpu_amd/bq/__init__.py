@@ -314,6 +314,8 @@ def norm_qkv(x: torch.Tensor, gamma: torch.Tensor, q: ButterquantWeight, k: Butt
              v: ButterquantWeight, block: int = 128, sqrt_n=None, n_eps=None, outs=None,
              act_out=None):
     """norm_quant(x) then qkv on its codes, fused into one launch for one token."""
+    if v.n_rows != k.n_rows:
+        raise ValueError(f"norm_qkv: v has {v.n_rows} rows, k {k.n_rows}; they must match")
     _dev(x, torch.bfloat16)
     _dev(gamma, torch.bfloat16)
     m, h = x.shape

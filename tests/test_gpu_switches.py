@@ -50,7 +50,7 @@ def test_gemv_m1_segments(gpu, O, tune_env, waves):
     """q/k/v of one token in one k_gemv_m1 launch: each segment = the oracle."""
     tune_env(BQ_GEMV_M1_WAVES=waves)
     K = 2816
-    ws = [weight(gpu, O, n, K, 128, seed=sd) for n, sd in ((256, 1), (128, 2), (64, 3))]
+    ws = [weight(gpu, O, n, K, 128, seed=sd) for n, sd in ((256, 1), (128, 2), (128, 3))]
     x = O.synth_normal_bf16(10, 1.0, (1, K))
     xq, sa = O.norm_quant(x, np.full(K, ONE, np.uint16), 128)
     outs = gpu.qkv(dev(xq), dev(sa), *(w[2] for w in ws))
