@@ -130,7 +130,8 @@ int bq_block_linear(const int8_t* x_i8, const float* x_sa, const int8_t* w, cons
 
 /* dispatch_bq_qkv[hidden, qn_full, kvn_full] (linear.mojo:273-326): three
  * per-row linears sharing one activation, in ONE launch over the
- * concatenated q|k|v output tiles (the reference's Chain split). */
+ * concatenated q|k|v output tiles (the reference's Chain split).  q has qn
+ * rows; k and v both have kvn rows (v_out holds seq_len x kvn). */
 int bq_qkv(const int8_t* x_i8, const float* x_sa, const int8_t* q_w, const float* q_scale,
            const int8_t* k_w, const float* k_scale, const int8_t* v_w, const float* v_scale,
            uint16_t* q_out, uint16_t* k_out, uint16_t* v_out, int qn, int kvn, int seq_len,

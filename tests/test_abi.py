@@ -275,3 +275,20 @@ def test_calib_library_exports():
     assert lib.bqc_dma_l2(0, 8, P, 4096, 500, 4, 8, P, None) != 0   # rows not whole blocks
     assert lib.bqc_dma_l2(0, 8, C.c_void_p(17), 4096, 512, 4, 8, P, None) != 0  # misaligned
     assert lib.bqc_mfma_chain(0, 1, P, P, None) != 0
+
+
+def test_qkv_rejects_v_rows_unlike_k(L):
+    """bq_qkv sizes v from k's row count, so the wrappers refuse a v of
+    another row count before any launch (no GPU needed to reach the check)."""
+    import bq
+    import torch
+
+    def w(n):
+        return bq.ButterquantWeight(torch.empty(0, dtype=torch.int8), torch.empty(0), n, 256)
+
+    x = torch.empty((1, 256), dtype=torch.int8)
+    with pytest.raises(ValueError, match="must match"):
+        bq.qkv(x, torch.empty(1), w(256), w(128), w(64))
+    with pytest.raises(ValueError, match="must match"):
+        bq.norm_qkv(torch.empty((1, 256), dtype=torch.bfloat16), torch.empty(256), w(256), w(128),
+                    w(64))
